@@ -1,0 +1,158 @@
+/*
+ * mosaic_bsa.h -- C ABI of the MI355X (gfx950) block-sparse attention library.
+ *
+ * The library computes Mosaic's three-branch block-sparse attention forward on HEALPix
+ * nested-order sequences: local attention inside contiguous blocks, compressed attention
+ * between mean-pooled blocks, top-k block selection with attention over the selected key
+ * blocks, and the gated merge of the three.  All entry points are asynchronous on the given
+ * HIP stream, allocate nothing, never synchronise the host, and validate their arguments
+ * before any launch.  Tensors are device pointers; bf16 tensors of shape [B, N, H, d] are
+ * described by element strides for the batch, token and head dimensions, with the head_dim
+ * dimension contiguous.  head_dim must be 64.
+ *
+ * Every entry point returns a mosaic_status (0 = success); mosaic_bsa_strerror() names it.
+ */
+#ifndef MOSAIC_BSA_H
+#define MOSAIC_BSA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOSAIC_BSA_ABI_VERSION 1
+
+#if defined(__GNUC__) || defined(__clang__)
+#define MOSAIC_API __attribute__((visibility("default")))
+#else
+#define MOSAIC_API
+#endif
+
+typedef enum {
+    MOSAIC_OK = 0,
+    MOSAIC_ERR_NULL_POINTER = 1,   /* a required pointer is NULL                          */
+    MOSAIC_ERR_HEAD_DIM = 2,       /* head_dim != 64                                      */
+    MOSAIC_ERR_HEADS = 3,          /* num_q_heads not a positive multiple of num_kv_heads */
+    MOSAIC_ERR_BLOCK_SIZE = 4,     /* block sizes not multiples of 64 / not dividing N    */
+    MOSAIC_ERR_BLOCK_COUNT = 5,    /* sparse_block_count < 0 or > number of blocks        */
+    MOSAIC_ERR_WORKSPACE = 6,      /* workspace missing, too small or misaligned          */
+    MOSAIC_ERR_ALIGNMENT = 7,      /* bf16 rows not 16-byte aligned                       */
+    MOSAIC_ERR_SHAPE = 8,          /* non-positive or too large sizes                     */
+    MOSAIC_ERR_LAUNCH = 9,         /* the HIP runtime rejected a kernel launch            */
+    MOSAIC_ERR_MODE = 10,          /* unknown mode                                        */
+    MOSAIC_ERR_UNSUPPORTED = 11    /* valid request outside the library's limits          */
+} mosaic_status;
+
+/* Branch combination, matching mosaic_attn_func (primitives.py:54-89). */
+typedef enum {
+    MOSAIC_BSA_FULL = 0,           /* o_ba*w0 + o_cmp*w1 + o_slc*w2           (:86-89) */
+    MOSAIC_BSA_LOCAL_ONLY = 1,     /* block_attn_only: o_ba                  (:62-63) */
+    MOSAIC_BSA_NO_COMPRESSION = 2, /* (o_ba*w0 + o_slc*w2) / (w0+w2+1e-8)    (:68-74) */
+    MOSAIC_BSA_NO_SELECTION = 3    /* sparse_block_count == 0:
+                                      (o_ba*w0 + o_cmp*w1) / (w0+w1+1e-8)    (:80-84) */
+} mosaic_bsa_mode;
+
+/* A bf16 [B, N, H, 64] tensor: element strides of b, n and h; head_dim stride is 1. */
+typedef struct {
+    const void* ptr;
+    int64_t stride_b, stride_n, stride_h;
+} mosaic_bnhd;
+
+/*
+ * Arguments of the full forward.  Replaces the Python function
+ *   mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
+ *                    sparse_block_count, block_attn_only, no_compression)
+ * (primitives.py:54-89) including the helpers it calls: block_attention (:28-32), the
+ * einops mean pooling (:65-66,76), flash_attn_func on the pooled blocks (:77-78), attn_topk
+ * (:35-51) and mosaic_sparse_attn (ops.py:557-566).
+ */
+typedef struct {
+    int32_t batch, seq_len, num_q_heads, num_kv_heads, head_dim;
+    int32_t block_attn_size;       /* local block (multiple of 64, divides seq_len)          */
+    int32_t sparse_block_size;     /* pooling / selection block (multiple of 64, divides N)  */
+    int32_t sparse_block_count;    /* top-k blocks per query block                           */
+    int32_t mode;                  /* mosaic_bsa_mode                                        */
+    float softmax_scale;           /* <= 0 selects head_dim^-0.5 (flash-attn / ops.py:565)   */
+    mosaic_bnhd q, k, v;
+    /* weight_ba_cmp_slc, bf16 [3, B, N, Hq(, 1)] with arbitrary element strides; unused
+       (may be NULL) in MOSAIC_BSA_LOCAL_ONLY mode. */
+    const void* weights;
+    int64_t w_stride_s, w_stride_b, w_stride_n, w_stride_h;
+    void* out;                     /* bf16 [B, N, Hq, 64], contiguous                        */
+    int64_t* block_indices_out;    /* optional: int64 [B, N/bs, Hk, K] selected blocks       */
+} mosaic_bsa_args;
+
+/* Bytes of device workspace mosaic_bsa_fwd needs for these arguments (256-byte aligned). */
+MOSAIC_API size_t mosaic_bsa_workspace_size(const mosaic_bsa_args* args);
+
+/* Full forward (primitives.py:54-89).  workspace: device memory of at least
+   mosaic_bsa_workspace_size(args) bytes, 256-byte aligned.  stream: hipStream_t. */
+MOSAIC_API int mosaic_bsa_fwd(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* As mosaic_bsa_fwd, recording events[0..4] (hipEvent_t) on the stream before the pooling
+   kernel, before the compressed/score kernel, before the top-k kernel, before the attention
+   kernel and after it, so a caller can time each kernel.  No reference counterpart: it is
+   the measurement hook of the benchmark. */
+MOSAIC_API int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* workspace,
+                            size_t workspace_bytes, void* stream, void* const* events);
+
+/*
+ * Selected-branch attention given block indices.  Replaces mosaic_sparse_attn /
+ * MosaicAttnFunction.forward / mosaic_attn_fwd (ops.py:557-566, 510-538, 137-176):
+ * for query token n of block i = n / block_size, query head j and kv head c = j / (Hq/Hk),
+ * attend to the tokens of blocks block_indices[b, i, c, 0..K-1].  out: bf16 [B, N, Hq, 64]
+ * contiguous; lse (optional): fp32 [B, N, Hq] base-2 log-sum-exp of the scaled logits.
+ * block_indices: int64 [B, N/block_size, Hk, K] contiguous; entries outside [0, N/bs) are
+ * skipped (a row whose entries are all invalid yields NaN).
+ */
+MOSAIC_API int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v,
+                           const int64_t* block_indices, int32_t batch, int32_t seq_len,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t block_size, int32_t block_count, float softmax_scale,
+                           void* out, float* lse, void* stream);
+
+/* Local attention inside contiguous blocks.  Replaces block_attention (primitives.py:28-32),
+   i.e. flash_attn_func on [(B*N/bs), bs, H, d] views.  out: bf16 [B, N, Hq, 64] contiguous. */
+MOSAIC_API int mosaic_block_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, int32_t batch,
+                          int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t block_size, float softmax_scale, void* out,
+                          void* stream);
+
+/* Dense (full-sequence) attention: the baseline the sparse op is compared with.  Same
+   contract as mosaic_block_attn_fwd with block_size = seq_len (flash_attn_func on the whole
+   sequence, primitives.py:31 with one block). */
+MOSAIC_API int mosaic_dense_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, int32_t batch,
+                          int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                          int32_t head_dim, float softmax_scale, void* out, void* stream);
+
+/* Mean over runs of block_size tokens, rounded to bf16.  Replaces the einops
+   reduce(x, 'b (nb bs) h d -> b nb h d', 'mean') of primitives.py:65-66,76.
+   out: bf16 [B, N/block_size, H, 64] contiguous. */
+MOSAIC_API int mosaic_pool_mean_fwd(mosaic_bnhd x, int32_t batch, int32_t seq_len, int32_t num_heads,
+                         int32_t head_dim, int32_t block_size, void* out, void* stream);
+
+/* Top-k block selection from pooled queries/keys.  Replaces attn_topk (primitives.py:35-51):
+   scores[b, h, t, u] = mean over g of bf16(q_cmp[b, t, g*Hk + h] . k_cmp[b, u, (g*Hk+h)/G]),
+   rounded to bf16; indices_out[b, t, h, :] = the block_count largest u, in descending score
+   order (ties: lower u first).  q_cmp/k_cmp: bf16 [B, nb, H, 64]; indices_out: int64
+   [B, nb, Hk, K] contiguous.  workspace: mosaic_attn_topk_workspace_size() bytes. */
+MOSAIC_API size_t mosaic_attn_topk_workspace_size(int32_t batch, int32_t num_blocks, int32_t num_kv_heads);
+MOSAIC_API int mosaic_attn_topk_fwd(mosaic_bnhd q_cmp, mosaic_bnhd k_cmp, int32_t batch,
+                         int32_t num_blocks, int32_t num_q_heads, int32_t num_kv_heads,
+                         int32_t head_dim, int32_t block_count, int64_t* indices_out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Name of a status code (static storage). */
+MOSAIC_API const char* mosaic_bsa_strerror(int status);
+
+/* MOSAIC_BSA_ABI_VERSION of the loaded library. */
+MOSAIC_API int mosaic_bsa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOSAIC_BSA_H */

@@ -1,0 +1,123 @@
+"""ctypes binding of libmosaic_bsa.so (the C ABI declared in include/mosaic_bsa.h).
+
+The library is loaded from this package directory.  There is no fallback: if it is missing
+the first call raises ``MosaicLibraryError`` naming the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_NAME = "libmosaic_bsa.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+ABI_VERSION = 1
+
+# mosaic_bsa_mode
+MODE_FULL = 0
+MODE_LOCAL_ONLY = 1
+MODE_NO_COMPRESSION = 2
+MODE_NO_SELECTION = 3
+
+EXPORTED_SYMBOLS = (
+    "mosaic_bsa_workspace_size",
+    "mosaic_bsa_fwd",
+    "mosaic_bsa_fwd_profiled",
+    "mosaic_sparse_attn_fwd",
+    "mosaic_block_attn_fwd",
+    "mosaic_dense_attn_fwd",
+    "mosaic_pool_mean_fwd",
+    "mosaic_attn_topk_workspace_size",
+    "mosaic_attn_topk_fwd",
+    "mosaic_bsa_strerror",
+    "mosaic_bsa_abi_version",
+)
+
+
+class MosaicLibraryError(RuntimeError):
+    pass
+
+
+class Bnhd(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("stride_b", ctypes.c_int64),
+                ("stride_n", ctypes.c_int64), ("stride_h", ctypes.c_int64)]
+
+
+class BsaArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("seq_len", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("block_attn_size", ctypes.c_int32),
+        ("sparse_block_size", ctypes.c_int32), ("sparse_block_count", ctypes.c_int32),
+        ("mode", ctypes.c_int32), ("softmax_scale", ctypes.c_float),
+        ("q", Bnhd), ("k", Bnhd), ("v", Bnhd),
+        ("weights", ctypes.c_void_p),
+        ("w_stride_s", ctypes.c_int64), ("w_stride_b", ctypes.c_int64),
+        ("w_stride_n", ctypes.c_int64), ("w_stride_h", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("block_indices_out", ctypes.c_void_p),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    c_int, c_i32, c_size, c_vp, c_f = ctypes.c_int, ctypes.c_int32, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
+    P = ctypes.POINTER
+    lib.mosaic_bsa_workspace_size.argtypes = [P(BsaArgs)]
+    lib.mosaic_bsa_workspace_size.restype = c_size
+    lib.mosaic_bsa_fwd.argtypes = [P(BsaArgs), c_vp, c_size, c_vp]
+    lib.mosaic_bsa_fwd.restype = c_int
+    lib.mosaic_bsa_fwd_profiled.argtypes = [P(BsaArgs), c_vp, c_size, c_vp, P(c_vp)]
+    lib.mosaic_bsa_fwd_profiled.restype = c_int
+    lib.mosaic_sparse_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                           c_i32, c_i32, c_f, c_vp, c_vp, c_vp]
+    lib.mosaic_sparse_attn_fwd.restype = c_int
+    lib.mosaic_block_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f,
+                                          c_vp, c_vp]
+    lib.mosaic_block_attn_fwd.restype = c_int
+    lib.mosaic_dense_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_i32, c_i32, c_i32, c_i32, c_i32, c_f, c_vp, c_vp]
+    lib.mosaic_dense_attn_fwd.restype = c_int
+    lib.mosaic_pool_mean_fwd.argtypes = [Bnhd, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]
+    lib.mosaic_pool_mean_fwd.restype = c_int
+    lib.mosaic_attn_topk_workspace_size.argtypes = [c_i32, c_i32, c_i32]
+    lib.mosaic_attn_topk_workspace_size.restype = c_size
+    lib.mosaic_attn_topk_fwd.argtypes = [Bnhd, Bnhd, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp,
+                                         c_size, c_vp]
+    lib.mosaic_attn_topk_fwd.restype = c_int
+    lib.mosaic_bsa_strerror.argtypes = [c_int]
+    lib.mosaic_bsa_strerror.restype = ctypes.c_char_p
+    lib.mosaic_bsa_abi_version.argtypes = []
+    lib.mosaic_bsa_abi_version.restype = c_int
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded once per process)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise MosaicLibraryError(
+                    f"{LIB_PATH} is missing: build it with `python -m mosaic_amd.build` "
+                    "(hipcc, gfx950). There is no CPU fallback.")
+            handle = ctypes.CDLL(LIB_PATH)
+            _declare(handle)
+            ver = handle.mosaic_bsa_abi_version()
+            if ver != ABI_VERSION:
+                raise MosaicLibraryError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}")
+            _lib = handle
+    return _lib
+
+
+def strerror(status: int) -> str:
+    return lib().mosaic_bsa_strerror(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what}: {strerror(status)} (mosaic status {status})")

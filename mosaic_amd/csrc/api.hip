@@ -1,0 +1,352 @@
+// api.hip -- the extern "C" entry points of include/mosaic_bsa.h.
+//
+// Host side only: argument validation (before any launch), workspace layout, choice of the
+// compressed-attention split count, and the launch sequence on the caller's stream:
+//   pool (q, k, v -> pooled)  ->  cmp (compressed attention partials + selection scores)
+//   ->  top-k (indices)  ->  attn (local + selected + merge)
+// Nothing here allocates device memory or synchronises the host.
+#include <cmath>
+
+#include "bsa_common.h"
+#include "../../include/mosaic_bsa.h"
+
+using namespace mosaic;
+
+namespace {
+
+constexpr size_t kAlign = 256;
+constexpr int kMaxBlocksTopk = 8192;  // selection rows live in registers: 128 keys per lane
+constexpr int kMaxGroup = 16;         // query heads per kv head (one wave each in cmp_kernel)
+constexpr int kMaxSplits = 4;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_bnhd(const mosaic_bnhd& t) {
+    if (t.ptr == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(t.ptr) || (t.stride_b % 8) || (t.stride_n % 8) || (t.stride_h % 8)) return MOSAIC_ERR_ALIGNMENT;
+    return MOSAIC_OK;
+}
+
+float resolve_scale(float s, int d) { return s > 0.f ? s : 1.f / std::sqrt((float)d); }
+
+int check_heads(int Hq, int Hk) {
+    if (Hq <= 0 || Hk <= 0 || Hq % Hk) return MOSAIC_ERR_HEADS;
+    if (Hq / Hk > kMaxGroup) return MOSAIC_ERR_UNSUPPORTED;
+    return MOSAIC_OK;
+}
+
+// Waves per attention workgroup: the whole GQA group when it is 1, 2 or 4 heads, otherwise
+// groups of 4 (G a multiple of 4) or single heads.
+int attn_waves(int G) {
+    if (G == 1 || G == 2 || G == 4) return G;
+    if (G % 4 == 0) return 4;
+    if (G % 2 == 0) return 2;
+    return 1;
+}
+
+int choose_splits(int B, int nb, int Hk) {
+    const int tt = (nb + 31) / 32;
+    const int wgs = tt * Hk * B;
+    int s = 1;
+    while (s < kMaxSplits && wgs * s < 512 && 2 * s <= tt) s *= 2;
+    return s;
+}
+
+struct Layout {
+    int nb = 0, nb_pad = 0, nsplit = 1;
+    size_t qc = 0, kc = 0, vct = 0, sbar = 0, idx = 0, opart = 0, ml = 0, total = 0;
+};
+
+bool uses_selection(int mode) { return mode == MOSAIC_BSA_FULL || mode == MOSAIC_BSA_NO_COMPRESSION; }
+bool uses_compression(int mode) { return mode == MOSAIC_BSA_FULL || mode == MOSAIC_BSA_NO_SELECTION; }
+
+int validate(const mosaic_bsa_args* a) {
+    if (a == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (a->mode < MOSAIC_BSA_FULL || a->mode > MOSAIC_BSA_NO_SELECTION) return MOSAIC_ERR_MODE;
+    if (a->batch <= 0 || a->seq_len <= 0) return MOSAIC_ERR_SHAPE;
+    if (a->head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
+    if (int e = check_heads(a->num_q_heads, a->num_kv_heads)) return e;
+    if (int e = check_bnhd(a->q)) return e;
+    if (int e = check_bnhd(a->k)) return e;
+    if (int e = check_bnhd(a->v)) return e;
+    if (a->out == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(a->out)) return MOSAIC_ERR_ALIGNMENT;
+    if ((int64_t)a->batch * a->seq_len * a->num_q_heads * kHeadDim >= ((int64_t)1 << 40)) return MOSAIC_ERR_SHAPE;
+    if (a->block_attn_size <= 0 || a->block_attn_size % kTile || a->seq_len % a->block_attn_size)
+        return MOSAIC_ERR_BLOCK_SIZE;
+    if (a->mode == MOSAIC_BSA_LOCAL_ONLY) return MOSAIC_OK;
+    if (a->weights == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (a->sparse_block_size <= 0 || a->sparse_block_size % kTile || a->seq_len % a->sparse_block_size)
+        return MOSAIC_ERR_BLOCK_SIZE;
+    const int nb = a->seq_len / a->sparse_block_size;
+    if (a->sparse_block_count < 0 || a->sparse_block_count > nb) return MOSAIC_ERR_BLOCK_COUNT;
+    if (uses_selection(a->mode)) {
+        if (a->sparse_block_count == 0) return MOSAIC_ERR_BLOCK_COUNT;
+        if (nb > kMaxBlocksTopk || nb > 65535) return MOSAIC_ERR_UNSUPPORTED;
+    }
+    return MOSAIC_OK;
+}
+
+Layout layout_of(const mosaic_bsa_args* a) {
+    Layout L;
+    if (a->mode == MOSAIC_BSA_LOCAL_ONLY) return L;
+    const size_t B = a->batch, Hq = a->num_q_heads, Hk = a->num_kv_heads;
+    L.nb = a->seq_len / a->sparse_block_size;
+    L.nb_pad = (L.nb + 31) / 32 * 32;
+    L.nsplit = choose_splits(a->batch, L.nb, a->num_kv_heads);
+    const size_t nb = L.nb, nbp = L.nb_pad, K = a->sparse_block_count, U = L.nsplit;
+    size_t off = 0;
+    L.qc = off; off = align_up(off + B * nb * Hq * kHeadDim * 2);
+    L.kc = off; off = align_up(off + B * nb * Hk * kHeadDim * 2);
+    if (uses_compression(a->mode)) {
+        L.vct = off; off = align_up(off + B * Hk * kHeadDim * nbp * 2);
+        L.opart = off; off = align_up(off + B * U * nb * Hq * kHeadDim * 4);
+        L.ml = off; off = align_up(off + B * U * nb * Hq * 8);
+    }
+    if (uses_selection(a->mode)) {
+        L.sbar = off; off = align_up(off + B * Hk * nb * nbp * 2);
+        L.idx = off; off = align_up(off + B * nb * Hk * K * 4);
+    }
+    L.total = off;
+    return L;
+}
+
+AttnParams attn_params(const mosaic_bnhd& q, const mosaic_bnhd& k, const mosaic_bnhd& v, int B, int N,
+                       int Hq, int Hk, float scale) {
+    AttnParams p{};
+    p.q = static_cast<const bf16_t*>(q.ptr); p.q_sb = q.stride_b; p.q_sn = q.stride_n; p.q_sh = q.stride_h;
+    p.k = static_cast<const bf16_t*>(k.ptr); p.k_sb = k.stride_b; p.k_sn = k.stride_n; p.k_sh = k.stride_h;
+    p.v = static_cast<const bf16_t*>(v.ptr); p.v_sb = v.stride_b; p.v_sn = v.stride_n; p.v_sh = v.stride_h;
+    p.B = B; p.N = N; p.Hq = Hq; p.Hk = Hk; p.G = Hq / Hk;
+    const int waves = attn_waves(p.G);
+    p.head_groups = p.G / waves;
+    p.qtiles = N / kTile;
+    p.total_wgs = B * Hk * p.head_groups * p.qtiles;
+    p.scale = scale;
+    p.scale_log2 = scale * kLog2e;
+    p.nsplit = 1;
+    return p;
+}
+
+int launch_status(hipError_t e) { return e == hipSuccess ? MOSAIC_OK : MOSAIC_ERR_LAUNCH; }
+
+int record(void* const* events, int i, hipStream_t s) {
+    if (events == nullptr || events[i] == nullptr) return MOSAIC_OK;
+    return launch_status(hipEventRecord(static_cast<hipEvent_t>(events[i]), s));
+}
+
+int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* stream, void* const* events) {
+    if (int e = validate(a)) return e;
+    const Layout L = layout_of(a);
+    if (L.total > 0) {
+        if (ws == nullptr || ws_bytes < L.total) return MOSAIC_ERR_WORKSPACE;
+        if ((reinterpret_cast<uintptr_t>(ws) & (kAlign - 1)) != 0) return MOSAIC_ERR_WORKSPACE;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* w = static_cast<char*>(ws);
+    const int B = a->batch, N = a->seq_len, Hq = a->num_q_heads, Hk = a->num_kv_heads;
+    const float scale = resolve_scale(a->softmax_scale, a->head_dim);
+    const bool sel = uses_selection(a->mode), cmp = uses_compression(a->mode);
+
+    AttnParams ap = attn_params(a->q, a->k, a->v, B, N, Hq, Hk, scale);
+    ap.out = static_cast<bf16_t*>(a->out);
+    ap.bs_l = a->block_attn_size;
+    ap.bs = a->mode == MOSAIC_BSA_LOCAL_ONLY ? kTile : a->sparse_block_size;
+    ap.K = a->sparse_block_count;
+    ap.nb = N / ap.bs;
+    ap.w = static_cast<const bf16_t*>(a->weights);
+    ap.w_ss = a->w_stride_s; ap.w_sb = a->w_stride_b; ap.w_sn = a->w_stride_n; ap.w_sh = a->w_stride_h;
+    const int waves = attn_waves(ap.G);
+
+    if (int e = record(events, 0, s)) return e;
+    if (a->mode != MOSAIC_BSA_LOCAL_ONLY) {
+        const bf16_t* qc = reinterpret_cast<const bf16_t*>(w + L.qc);
+        const bf16_t* kc = reinterpret_cast<const bf16_t*>(w + L.kc);
+
+        PoolParams pp{};
+        pp.x[0] = ap.q; pp.sb[0] = ap.q_sb; pp.sn[0] = ap.q_sn; pp.sh[0] = ap.q_sh; pp.heads[0] = Hq;
+        pp.x[1] = ap.k; pp.sb[1] = ap.k_sb; pp.sn[1] = ap.k_sn; pp.sh[1] = ap.k_sh; pp.heads[1] = Hk;
+        pp.out_bnhd[0] = reinterpret_cast<bf16_t*>(w + L.qc);
+        pp.out_bnhd[1] = reinterpret_cast<bf16_t*>(w + L.kc);
+        if (cmp) {
+            pp.x[2] = ap.v; pp.sb[2] = ap.v_sb; pp.sn[2] = ap.v_sn; pp.sh[2] = ap.v_sh; pp.heads[2] = Hk;
+            pp.out_t = reinterpret_cast<bf16_t*>(w + L.vct);
+        }
+        pp.B = B; pp.nb = L.nb; pp.nb_pad = L.nb_pad; pp.bs = a->sparse_block_size;
+        if (int e = launch_status(launch_pool(pp, s))) return e;
+        if (int e = record(events, 1, s)) return e;
+
+        CmpParams cp{};
+        cp.qc = qc; cp.q_sb = (int64_t)L.nb * Hq * kHeadDim; cp.q_sn = (int64_t)Hq * kHeadDim; cp.q_sh = kHeadDim;
+        cp.kc = kc; cp.k_sb = (int64_t)L.nb * Hk * kHeadDim; cp.k_sn = (int64_t)Hk * kHeadDim; cp.k_sh = kHeadDim;
+        cp.vct = cmp ? reinterpret_cast<const bf16_t*>(w + L.vct) : nullptr;
+        cp.sbar = sel ? reinterpret_cast<bf16_t*>(w + L.sbar) : nullptr;
+        cp.opart = cmp ? reinterpret_cast<float*>(w + L.opart) : nullptr;
+        cp.ml = cmp ? reinterpret_cast<float2*>(w + L.ml) : nullptr;
+        cp.B = B; cp.nb = L.nb; cp.nb_pad = L.nb_pad; cp.Hq = Hq; cp.Hk = Hk; cp.G = Hq / Hk;
+        cp.nsplit = L.nsplit; cp.ut_total = L.nb_pad / 32;
+        cp.scale_log2 = scale * kLog2e;
+        if (int e = launch_status(launch_cmp(cp, sel, cmp, s))) return e;
+        if (int e = record(events, 2, s)) return e;
+
+        if (sel) {
+            TopkParams tp{};
+            tp.sbar = cp.sbar;
+            tp.idx32 = reinterpret_cast<int32_t*>(w + L.idx);
+            tp.idx64 = a->block_indices_out;
+            tp.B = B; tp.nb = L.nb; tp.nb_pad = L.nb_pad; tp.Hk = Hk; tp.K = a->sparse_block_count;
+            tp.rows = B * Hk * L.nb;
+            if (int e = launch_status(launch_topk(tp, s))) return e;
+            ap.idx = tp.idx32;
+        }
+        if (int e = record(events, 3, s)) return e;
+        ap.opart = cp.opart;
+        ap.ml = cp.ml;
+        ap.nsplit = L.nsplit;
+    } else {
+        if (int e = record(events, 1, s)) return e;
+        if (int e = record(events, 2, s)) return e;
+        if (int e = record(events, 3, s)) return e;
+    }
+    static const int mode_map[4] = {kModeFull, kModeLocalOnly, kModeNoCompression, kModeNoSelection};
+    if (int e = launch_status(launch_attn(ap, mode_map[a->mode], false, waves, s))) return e;
+    return record(events, 4, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mosaic_bsa_workspace_size(const mosaic_bsa_args* args) {
+    if (validate(args) != MOSAIC_OK) return 0;
+    return layout_of(args).total;
+}
+
+int mosaic_bsa_fwd(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes, void* stream) {
+    return bsa_forward(args, workspace, workspace_bytes, stream, nullptr);
+}
+
+int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes, void* stream,
+                            void* const* events) {
+    return bsa_forward(args, workspace, workspace_bytes, stream, events);
+}
+
+int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const int64_t* block_indices,
+                           int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t block_size, int32_t block_count, float softmax_scale,
+                           void* out, float* lse, void* stream) {
+    if (batch <= 0 || seq_len <= 0 || block_count <= 0) return block_count <= 0 ? MOSAIC_ERR_BLOCK_COUNT : MOSAIC_ERR_SHAPE;
+    if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
+    if (int e = check_heads(num_q_heads, num_kv_heads)) return e;
+    if (int e = check_bnhd(q)) return e;
+    if (int e = check_bnhd(k)) return e;
+    if (int e = check_bnhd(v)) return e;
+    if (block_indices == nullptr || out == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(out)) return MOSAIC_ERR_ALIGNMENT;
+    if (block_size <= 0 || block_size % kTile || seq_len % block_size) return MOSAIC_ERR_BLOCK_SIZE;
+    AttnParams ap = attn_params(q, k, v, batch, seq_len, num_q_heads, num_kv_heads,
+                                resolve_scale(softmax_scale, head_dim));
+    ap.out = static_cast<bf16_t*>(out);
+    ap.lse = lse;
+    ap.idx = block_indices;
+    ap.bs = block_size;
+    ap.bs_l = block_size;
+    ap.K = block_count;
+    ap.nb = seq_len / block_size;
+    return launch_status(launch_attn(ap, kModeSelectedOnly, true, attn_waves(ap.G), static_cast<hipStream_t>(stream)));
+}
+
+int mosaic_block_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, int32_t batch, int32_t seq_len,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          float softmax_scale, void* out, void* stream) {
+    mosaic_bsa_args a{};
+    a.batch = batch; a.seq_len = seq_len; a.num_q_heads = num_q_heads; a.num_kv_heads = num_kv_heads;
+    a.head_dim = head_dim; a.block_attn_size = block_size; a.mode = MOSAIC_BSA_LOCAL_ONLY;
+    a.softmax_scale = softmax_scale; a.q = q; a.k = k; a.v = v; a.out = out;
+    return bsa_forward(&a, nullptr, 0, stream, nullptr);
+}
+
+int mosaic_dense_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, int32_t batch, int32_t seq_len,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float softmax_scale,
+                          void* out, void* stream) {
+    return mosaic_block_attn_fwd(q, k, v, batch, seq_len, num_q_heads, num_kv_heads, head_dim, seq_len,
+                                 softmax_scale, out, stream);
+}
+
+int mosaic_pool_mean_fwd(mosaic_bnhd x, int32_t batch, int32_t seq_len, int32_t num_heads, int32_t head_dim,
+                         int32_t block_size, void* out, void* stream) {
+    if (batch <= 0 || seq_len <= 0 || num_heads <= 0) return MOSAIC_ERR_SHAPE;
+    if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
+    if (int e = check_bnhd(x)) return e;
+    if (out == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(out)) return MOSAIC_ERR_ALIGNMENT;
+    if (block_size <= 0 || block_size % 8 || seq_len % block_size) return MOSAIC_ERR_BLOCK_SIZE;
+    PoolParams pp{};
+    pp.x[0] = static_cast<const bf16_t*>(x.ptr);
+    pp.sb[0] = x.stride_b; pp.sn[0] = x.stride_n; pp.sh[0] = x.stride_h; pp.heads[0] = num_heads;
+    pp.out_bnhd[0] = static_cast<bf16_t*>(out);
+    pp.B = batch; pp.nb = seq_len / block_size; pp.nb_pad = pp.nb; pp.bs = block_size;
+    return launch_status(launch_pool(pp, static_cast<hipStream_t>(stream)));
+}
+
+size_t mosaic_attn_topk_workspace_size(int32_t batch, int32_t num_blocks, int32_t num_kv_heads) {
+    if (batch <= 0 || num_blocks <= 0 || num_kv_heads <= 0) return 0;
+    const size_t nbp = (size_t)(num_blocks + 31) / 32 * 32;
+    return align_up((size_t)batch * num_kv_heads * num_blocks * nbp * 2);
+}
+
+int mosaic_attn_topk_fwd(mosaic_bnhd q_cmp, mosaic_bnhd k_cmp, int32_t batch, int32_t num_blocks,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_count,
+                         int64_t* indices_out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (batch <= 0 || num_blocks <= 0) return MOSAIC_ERR_SHAPE;
+    if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
+    if (int e = check_heads(num_q_heads, num_kv_heads)) return e;
+    if (int e = check_bnhd(q_cmp)) return e;
+    if (int e = check_bnhd(k_cmp)) return e;
+    if (indices_out == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (block_count <= 0 || block_count > num_blocks) return MOSAIC_ERR_BLOCK_COUNT;
+    if (num_blocks > kMaxBlocksTopk) return MOSAIC_ERR_UNSUPPORTED;
+    const size_t need = mosaic_attn_topk_workspace_size(batch, num_blocks, num_kv_heads);
+    if (workspace == nullptr || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & (kAlign - 1)))
+        return MOSAIC_ERR_WORKSPACE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int nb_pad = (num_blocks + 31) / 32 * 32;
+    CmpParams cp{};
+    cp.qc = static_cast<const bf16_t*>(q_cmp.ptr); cp.q_sb = q_cmp.stride_b; cp.q_sn = q_cmp.stride_n; cp.q_sh = q_cmp.stride_h;
+    cp.kc = static_cast<const bf16_t*>(k_cmp.ptr); cp.k_sb = k_cmp.stride_b; cp.k_sn = k_cmp.stride_n; cp.k_sh = k_cmp.stride_h;
+    cp.sbar = static_cast<bf16_t*>(workspace);
+    cp.B = batch; cp.nb = num_blocks; cp.nb_pad = nb_pad; cp.Hq = num_q_heads; cp.Hk = num_kv_heads;
+    cp.G = num_q_heads / num_kv_heads;
+    cp.nsplit = choose_splits(batch, num_blocks, num_kv_heads);
+    cp.ut_total = nb_pad / 32;
+    if (int e = launch_status(launch_cmp(cp, true, false, s))) return e;
+    TopkParams tp{};
+    tp.sbar = cp.sbar; tp.idx64 = indices_out;
+    tp.B = batch; tp.nb = num_blocks; tp.nb_pad = nb_pad; tp.Hk = num_kv_heads; tp.K = block_count;
+    tp.rows = batch * num_kv_heads * num_blocks;
+    return launch_status(launch_topk(tp, s));
+}
+
+const char* mosaic_bsa_strerror(int status) {
+    switch (status) {
+        case MOSAIC_OK: return "ok";
+        case MOSAIC_ERR_NULL_POINTER: return "a required pointer is NULL";
+        case MOSAIC_ERR_HEAD_DIM: return "head_dim must be 64";
+        case MOSAIC_ERR_HEADS: return "num_q_heads must be a positive multiple of num_kv_heads";
+        case MOSAIC_ERR_BLOCK_SIZE: return "block sizes must be positive multiples of 64 that divide seq_len";
+        case MOSAIC_ERR_BLOCK_COUNT: return "sparse_block_count out of range";
+        case MOSAIC_ERR_WORKSPACE: return "workspace missing, too small or not 256-byte aligned";
+        case MOSAIC_ERR_ALIGNMENT: return "bf16 rows must be 16-byte aligned (pointer and strides multiples of 8 elements)";
+        case MOSAIC_ERR_SHAPE: return "invalid sizes";
+        case MOSAIC_ERR_LAUNCH: return "kernel launch failed";
+        case MOSAIC_ERR_MODE: return "unknown mode";
+        case MOSAIC_ERR_UNSUPPORTED: return "outside the library's limits (query heads per kv head <= 16, blocks <= 8192)";
+        default: return "unknown status";
+    }
+}
+
+int mosaic_bsa_abi_version(void) { return MOSAIC_BSA_ABI_VERSION; }
+
+}  // extern "C"

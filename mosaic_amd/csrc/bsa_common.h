@@ -1,0 +1,128 @@
+// bsa_common.h -- shared types, bf16 helpers and kernel parameter blocks for the gfx950
+// block-sparse attention kernels.
+//
+// MFMA conventions used throughout (v_mfma_f32_32x32x16_bf16, one wave of 64 lanes):
+//   lane l = 32*hh + r  (hh = l / 32, r = l % 32)
+//   A operand (32 x 16): lane holds A[r][kidx(hh, i)], i = 0..7
+//   B operand (16 x 32): lane holds B[kidx(hh, i)][r], i = 0..7
+//   D (32 x 32, 16 fp32): register jj holds D[8*(jj/4) + 4*hh + jj%4][r]
+// The contraction index kidx(hh, i) is the same function for A and B, so any consistent
+// assignment of contraction elements to (hh, i) is correct.  Attention tiles are computed
+// transposed (S^T = K Q^T, O^T = V^T P^T): a lane then owns one query column, so row
+// statistics of the softmax are per-lane values plus one exchange between the two halves.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mosaic {
+
+typedef uint16_t bf16_t;  // storage type of bfloat16 values
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.44269504089f;  // constant of the selected-branch kernel (ops.py:41)
+constexpr int kHeadDim = 64;
+constexpr int kTile = 64;                  // query rows / keys per attention tile
+
+__device__ __forceinline__ float bf2f(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16 of two values, packed (lo = a, hi = b).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+__device__ __forceinline__ float round_bf16(float a) { return bf_lo(pack_bf16x2(a, 0.f)); }
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
+
+__device__ __forceinline__ float wave_max(float x) {
+    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+
+// Map a linear workgroup id to a logical tile so that each of the 8 XCDs (which receive
+// workgroups round-robin) works on one contiguous range of logical tiles and keeps that
+// range's K/V blocks in its own L2.
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+    const int xcd = id & 7, pos = id >> 3;
+    const int per = total >> 3, rem = total & 7;
+    return xcd * per + min(xcd, rem) + pos;
+}
+
+// ---------------------------------------------------------------------------------------
+// Kernel parameter blocks (passed by value).
+
+struct PoolParams {
+    const bf16_t* x[3];        // q, k, v (x[i] may be null when that tensor is not pooled)
+    int64_t sb[3], sn[3], sh[3];
+    int heads[3];
+    bf16_t* out_bnhd[3];       // [B, nb, H, 64] outputs (null: not written)
+    bf16_t* out_t;             // optional transposed output of tensor 2: [B, H, 64, nb_pad]
+    int B, nb, nb_pad, bs;
+};
+
+struct CmpParams {
+    const bf16_t* qc; int64_t q_sb, q_sn, q_sh;   // pooled queries [B, nb, Hq, 64]
+    const bf16_t* kc; int64_t k_sb, k_sn, k_sh;   // pooled keys    [B, nb, Hk, 64]
+    const bf16_t* vct;                             // pooled values, transposed [B, Hk, 64, nb_pad]
+    bf16_t* sbar;                                  // selection scores [B, Hk, nb, nb_pad]
+    float* opart;                                  // [B, U, nb, Hq, 64] unnormalised O
+    float2* ml;                                    // [B, U, nb, Hq] (running max, sum), log2 units
+    int B, nb, nb_pad, Hq, Hk, G, nsplit, ut_total;
+    float scale_log2;                              // softmax_scale * log2(e)
+};
+
+struct TopkParams {
+    const bf16_t* sbar;  // [B, Hk, nb, nb_pad]
+    int32_t* idx32;      // optional [B, nb, Hk, K]
+    int64_t* idx64;      // optional [B, nb, Hk, K]
+    int B, nb, nb_pad, Hk, K, rows;
+};
+
+enum AttnMode : int {
+    kModeFull = 0,
+    kModeLocalOnly = 1,
+    kModeNoCompression = 2,
+    kModeNoSelection = 3,
+    kModeSelectedOnly = 4,
+};
+
+struct AttnParams {
+    const bf16_t* q; int64_t q_sb, q_sn, q_sh;
+    const bf16_t* k; int64_t k_sb, k_sn, k_sh;
+    const bf16_t* v; int64_t v_sb, v_sn, v_sh;
+    const bf16_t* w; int64_t w_ss, w_sb, w_sn, w_sh;
+    bf16_t* out;             // [B, N, Hq, 64]
+    float* lse;              // [B, N, Hq] (selected-only mode, optional)
+    const void* idx;         // [B, nb, Hk, K] int32 or int64
+    const float* opart;      // compressed partials [B, U, nb, Hq, 64]
+    const float2* ml;        // [B, U, nb, Hq]
+    int B, N, Hq, Hk, G;
+    int bs_l, bs, K, nb, nsplit;
+    int head_groups;         // G / waves-per-workgroup
+    int qtiles;              // N / 64
+    int total_wgs;
+    float scale;             // softmax scale
+    float scale_log2;        // softmax scale * log2(e)
+};
+
+// Host-side launchers (defined next to each kernel).
+hipError_t launch_pool(const PoolParams& p, hipStream_t s);
+hipError_t launch_cmp(const CmpParams& p, bool scores, bool attn, hipStream_t s);
+hipError_t launch_topk(const TopkParams& p, hipStream_t s);
+hipError_t launch_attn(const AttnParams& p, int mode, bool idx64, int waves, hipStream_t s);
+
+}  // namespace mosaic

@@ -1,0 +1,90 @@
+"""Selected-branch attention: the MI355X drop-in for the reference's ops.py forward.
+
+Same names and arguments as the reference:
+  * ``mosaic_sparse_attn(q, k, v, block_indices, block_size, softmax_scale=None)``
+    (ops.py:557-566): ``softmax_scale`` defaults to ``head_dim ** -0.5``.
+  * ``MosaicAttnFunction`` (ops.py:510-554): forward runs the HIP kernel; backward is not
+    implemented (training gradients are outside this library) and raises.
+  * ``mosaic_attn_fwd(q, k, v, block_indices, block_size, softmax_scale)`` (ops.py:137-176)
+    returns ``(output, lse)`` with lse the base-2 log-sum-exp, fp32 [B, N, Hq].
+
+q [B, N, Hq, 64], k/v [B, N, Hk, 64] on a ROCm device; block_indices int64 [B, N/bs, Hk, K].
+Work is enqueued on the current stream.  The computation is bf16 (like the reference kernel,
+which casts q/k/v to bf16, ops.py:92,115-116); other input dtypes are converted to bf16 and
+the output is returned in q's dtype (ops.py:538).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _as_bf16_bnhd(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be [B, N, H, d], got shape {tuple(t.shape)}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a ROCm device, got {t.device}")
+    if t.dtype != torch.bfloat16:
+        t = t.to(torch.bfloat16)
+    if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:3]):
+        t = t.contiguous()
+    return t
+
+
+def bnhd(t: torch.Tensor) -> _lib.Bnhd:
+    return _lib.Bnhd(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    if k.shape != v.shape:
+        raise ValueError(f"k and v shapes differ: {tuple(k.shape)} vs {tuple(v.shape)}")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree on batch/seq/head_dim")
+
+
+def mosaic_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+                    block_size: int, softmax_scale: float):
+    """(output bf16 [B, N, Hq, d], lse fp32 [B, N, Hq]) of the selected-branch attention."""
+    q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    _check_gqa(q, k, v)
+    B, N, Hq, d = q.shape
+    Hk = k.shape[2]
+    if block_indices.dim() != 4:
+        raise ValueError("block_indices must be [B, N/block_size, Hk, K]")
+    idx = block_indices.to(device=q.device, dtype=torch.int64).contiguous()
+    if N % block_size == 0 and tuple(idx.shape[:3]) != (B, N // block_size, Hk):
+        raise ValueError(f"block_indices shape {tuple(idx.shape)} != {(B, N // block_size, Hk, '*')}")
+    out = torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=q.device)
+    lse = torch.empty(B, N, Hq, dtype=torch.float32, device=q.device)
+    st = _lib.lib().mosaic_sparse_attn_fwd(
+        bnhd(q), bnhd(k), bnhd(v), idx.data_ptr(), B, N, Hq, Hk, d, int(block_size), int(idx.shape[-1]),
+        float(softmax_scale), out.data_ptr(), lse.data_ptr(), stream_of(q))
+    _lib.check(st, "mosaic_sparse_attn_fwd")
+    return out, lse
+
+
+class MosaicAttnFunction(torch.autograd.Function):
+    """Autograd wrapper of the selected-branch forward (ops.py:510-554)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, block_indices, block_size, softmax_scale):
+        dtype = q.dtype
+        output, _ = mosaic_attn_fwd(q, k, v, block_indices, block_size, softmax_scale)
+        return output.to(dtype)
+
+    @staticmethod
+    def backward(ctx, grad_o):
+        raise NotImplementedError("mosaic_amd implements the forward pass only")
+
+
+def mosaic_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
+                       block_size: int, softmax_scale: float | None = None) -> torch.Tensor:
+    """Attention of each query block over its selected key blocks (ops.py:557-566)."""
+    softmax_scale = q.shape[-1] ** -0.5 if softmax_scale is None else softmax_scale
+    return MosaicAttnFunction.apply(q, k, v, block_indices, block_size, softmax_scale)

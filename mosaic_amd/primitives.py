@@ -1,0 +1,261 @@
+"""Block-sparse attention primitives: the MI355X drop-in for the reference's primitives.py op.
+
+Same names, arguments and branch logic as the reference:
+  * ``block_attention(q, k, v, block_size)``                       primitives.py:28-32
+  * ``attn_topk(q, k, block_count)``                               primitives.py:35-51
+  * ``mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
+    sparse_block_count, block_attn_only, no_compression=False)``   primitives.py:54-89
+  * ``RoPE`` and ``MosaicAttention`` modules (primitives.py:108-209), the op's caller, with
+    the reference's parameter and buffer names so its state dicts load unchanged.
+
+Every op runs as HIP kernels through the C ABI of libmosaic_bsa.so on the current stream;
+there is no CPU path.  Extras beyond the reference: ``pool_mean`` (the einops mean pooling of
+:65-66 as one kernel), ``dense_attention`` (full-sequence baseline), and the keyword-only
+``return_block_indices`` of ``mosaic_attn_func``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .healpix import rope_tables
+from .ops import _as_bf16_bnhd, _check_gqa, bnhd, mosaic_sparse_attn, stream_of
+
+__all__ = [
+    "block_attention", "dense_attention", "pool_mean", "attn_topk", "mosaic_attn_func",
+    "mosaic_sparse_attn", "RoPE", "MosaicAttention",
+]
+
+
+def _out_like(q: torch.Tensor) -> torch.Tensor:
+    return torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+
+
+def block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Attention inside contiguous blocks of ``block_size`` tokens (primitives.py:28-32)."""
+    dtype = q.dtype
+    q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    _check_gqa(q, k, v)
+    B, N, Hq, d = q.shape
+    out = _out_like(q)
+    st = _lib.lib().mosaic_block_attn_fwd(bnhd(q), bnhd(k), bnhd(v), B, N, Hq, k.shape[2], d, int(block_size),
+                                          0.0, out.data_ptr(), stream_of(q))
+    _lib.check(st, "mosaic_block_attn_fwd")
+    return out.to(dtype)
+
+
+def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+    """Full-sequence attention (flash_attn_func defaults), the dense baseline."""
+    dtype = q.dtype
+    q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    _check_gqa(q, k, v)
+    B, N, Hq, d = q.shape
+    out = _out_like(q)
+    st = _lib.lib().mosaic_dense_attn_fwd(bnhd(q), bnhd(k), bnhd(v), B, N, Hq, k.shape[2], d, 0.0,
+                                          out.data_ptr(), stream_of(q))
+    _lib.check(st, "mosaic_dense_attn_fwd")
+    return out.to(dtype)
+
+
+def pool_mean(x: torch.Tensor, block_size: int) -> torch.Tensor:
+    """reduce(x, 'b (nb bs) h d -> b nb h d', 'mean', bs=block_size) in bf16 (primitives.py:65)."""
+    x = _as_bf16_bnhd(x, "x")
+    B, N, H, d = x.shape
+    if N % block_size:
+        raise ValueError("sequence length must be a multiple of block_size")
+    out = torch.empty(B, N // block_size, H, d, dtype=torch.bfloat16, device=x.device)
+    st = _lib.lib().mosaic_pool_mean_fwd(bnhd(x), B, N, H, d, int(block_size), out.data_ptr(), stream_of(x))
+    _lib.check(st, "mosaic_pool_mean_fwd")
+    return out
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    ws = torch.empty(max(int(nbytes), 256) + 256, dtype=torch.uint8, device=device)
+    off = (-ws.data_ptr()) % 256
+    return ws[off:off + max(int(nbytes), 256)]
+
+
+@torch.no_grad()
+def attn_topk(q: torch.Tensor, k: torch.Tensor, block_count: int) -> torch.Tensor:
+    """Top-``block_count`` key blocks per query block and kv head (primitives.py:35-51).
+
+    q, k are the pooled tensors [B, nb, Hq, d] / [B, nb, Hk, d]; returns int64 [B, nb, Hk, K]
+    sorted by descending score.
+    """
+    q = _as_bf16_bnhd(q, "q")
+    k = _as_bf16_bnhd(k, "k")
+    B, nb, Hq, d = q.shape
+    Hk = k.shape[2]
+    if k.shape[0] != B or k.shape[1] != nb or k.shape[3] != d:
+        raise ValueError(f"q {tuple(q.shape)} and k {tuple(k.shape)} disagree")
+    if not 0 < block_count <= nb:
+        raise ValueError(f"block_count must be in [1, {nb}], got {block_count}")
+    L = _lib.lib()
+    ws = _workspace(L.mosaic_attn_topk_workspace_size(B, nb, Hk), q.device)
+    idx = torch.empty(B, nb, Hk, block_count, dtype=torch.int64, device=q.device)
+    st = L.mosaic_attn_topk_fwd(bnhd(q), bnhd(k), B, nb, Hq, Hk, d, int(block_count), idx.data_ptr(),
+                                ws.data_ptr(), ws.numel(), stream_of(q))
+    _lib.check(st, "mosaic_attn_topk_fwd")
+    return idx
+
+
+def _bsa_args(q, k, v, w, out, block_attn_size, sparse_block_size, sparse_block_count, mode, idx_out):
+    B, N, Hq, d = q.shape
+    a = _lib.BsaArgs()
+    a.batch, a.seq_len, a.num_q_heads, a.num_kv_heads, a.head_dim = B, N, Hq, k.shape[2], d
+    a.block_attn_size = int(block_attn_size)
+    a.sparse_block_size = int(sparse_block_size)
+    a.sparse_block_count = int(sparse_block_count)
+    a.mode = mode
+    a.softmax_scale = 0.0
+    a.q, a.k, a.v = bnhd(q), bnhd(k), bnhd(v)
+    if w is not None:
+        a.weights = w.data_ptr()
+        a.w_stride_s, a.w_stride_b, a.w_stride_n, a.w_stride_h = (w.stride(i) for i in range(4))
+    a.out = out.data_ptr()
+    a.block_indices_out = idx_out.data_ptr() if idx_out is not None else None
+    return a
+
+
+def _weights_view(w: torch.Tensor, B: int, N: int, Hq: int, device) -> torch.Tensor:
+    if w is None:
+        raise ValueError("weight_ba_cmp_slc is required unless block_attn_only")
+    if w.dim() == 5:
+        if w.shape[-1] != 1:
+            raise ValueError("weight_ba_cmp_slc must be [3, B, N, Hq, 1]")
+        w = w[..., 0]
+    if tuple(w.shape) != (3, B, N, Hq):
+        raise ValueError(f"weight_ba_cmp_slc shape {tuple(w.shape)} != (3, {B}, {N}, {Hq}, 1)")
+    if w.device != device:
+        raise ValueError("weight_ba_cmp_slc must be on the same device as q")
+    if w.dtype != torch.bfloat16:
+        w = w.to(torch.bfloat16)
+    return w
+
+
+def mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
+                     block_attn_only, no_compression=False, *, return_block_indices=False):
+    """Three-branch block-sparse attention forward (primitives.py:54-89).
+
+    Branch logic as in the reference: ``block_attn_only`` returns the local branch; with
+    ``no_compression`` the local and selected branches are merged with renormalised weights;
+    ``sparse_block_count == 0`` merges local and compressed with renormalised weights;
+    otherwise ``o_ba*w0 + o_cmp*w1 + o_slc*w2``.  With ``return_block_indices`` the selected
+    block indices (int64 [B, N/sparse_block_size, Hk, K]) are returned as well.
+    """
+    dtype = q.dtype
+    q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    _check_gqa(q, k, v)
+    B, N, Hq, d = q.shape
+    Hk = k.shape[2]
+    if block_attn_only:
+        mode = _lib.MODE_LOCAL_ONLY
+    elif no_compression:
+        if sparse_block_count <= 0:
+            raise ValueError("no_compression needs sparse_block_count >= 1")
+        mode = _lib.MODE_NO_COMPRESSION
+    elif sparse_block_count == 0:
+        mode = _lib.MODE_NO_SELECTION
+    else:
+        mode = _lib.MODE_FULL
+    w = None if block_attn_only else _weights_view(weight_ba_cmp_slc, B, N, Hq, q.device)
+    selects = mode in (_lib.MODE_FULL, _lib.MODE_NO_COMPRESSION)
+    idx = None
+    if return_block_indices and selects:
+        idx = torch.empty(B, N // sparse_block_size, Hk, sparse_block_count, dtype=torch.int64, device=q.device)
+    out = _out_like(q)
+    a = _bsa_args(q, k, v, w, out, block_attn_size, sparse_block_size, sparse_block_count, mode, idx)
+    L = _lib.lib()
+    nbytes = L.mosaic_bsa_workspace_size(ctypes.byref(a))
+    if nbytes == 0 and mode != _lib.MODE_LOCAL_ONLY:
+        # invalid arguments: let the entry point report which
+        _lib.check(L.mosaic_bsa_fwd(ctypes.byref(a), None, 0, stream_of(q)), "mosaic_bsa_fwd")
+    ws = _workspace(nbytes, q.device) if nbytes else None
+    st = L.mosaic_bsa_fwd(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
+                          ws.numel() if ws is not None else 0, stream_of(q))
+    _lib.check(st, "mosaic_bsa_fwd")
+    out = out.to(dtype)
+    if return_block_indices:
+        return out, idx
+    return out
+
+
+class RoPE(nn.Module):
+    """2-D (lon, lat) rotary embedding with the reference's buffers (primitives.py:108-135)."""
+
+    def __init__(self, dim, theta=10000):
+        super().__init__()
+        assert dim % 2 == 0
+        self.dim = dim
+        self.theta = theta
+
+    def initialize_rope(self, positions):
+        cos, sin = rope_tables(positions, self.dim, self.theta)
+        self.register_buffer("cos_freqs", cos, persistent=True)
+        self.register_buffer("sin_freqs", sin, persistent=True)
+
+    def forward(self, x):
+        xf = x.float()
+        c = self.cos_freqs.unsqueeze(0).unsqueeze(2)
+        s = self.sin_freqs.unsqueeze(0).unsqueeze(2)
+        x_even, x_odd = xf[..., 0::2], xf[..., 1::2]
+        out = torch.empty_like(xf)
+        out[..., 0::2] = x_even * c - x_odd * s
+        out[..., 1::2] = x_odd * c + x_even * s
+        return out.to(x.dtype)
+
+
+class MosaicAttention(nn.Module):
+    """The op's caller (primitives.py:138-209): projections, gates, RoPE, block-sparse attention.
+
+    ``config`` needs: block_attn_size, sparse_block_size, sparse_block_count, num_heads,
+    gqa_ratio, dim, qkv_compress_ratio, rope, rope_theta.  x is sequence-first [S, B, dim].
+    """
+
+    def __init__(self, config, block_attn_only: bool, no_compression: bool = False):
+        super().__init__()
+        self.block_attn_only = block_attn_only
+        self.no_compression = no_compression
+        self.block_attn_size = config.block_attn_size
+        self.sparse_block_size = config.sparse_block_size
+        self.sparse_block_count = config.sparse_block_count
+        q_heads = config.num_heads
+        kv_heads = q_heads // config.gqa_ratio
+        head_dim = int(config.dim // q_heads // config.qkv_compress_ratio)
+        self.q_heads, self.kv_heads = q_heads, kv_heads
+        self.to_q = nn.Linear(config.dim, q_heads * head_dim, bias=False)
+        self.to_k = nn.Linear(config.dim, kv_heads * head_dim, bias=False)
+        self.to_v = nn.Linear(config.dim, kv_heads * head_dim, bias=False)
+        self.to_o = nn.Linear(q_heads * head_dim, config.dim, bias=False)
+        self.q_rope = RoPE(head_dim, config.rope_theta) if config.rope else None
+        self.k_rope = RoPE(head_dim, config.rope_theta) if config.rope else None
+        self.to_strategy_combine_mlp = None if block_attn_only else nn.Linear(config.dim, 3 * q_heads, bias=False)
+
+    def generate_strategy_weights(self, x):
+        """Softmax over the 3 branch logits per head, channel index h*3 + s (primitives.py:173-180)."""
+        if self.block_attn_only:
+            return None
+        logits = self.to_strategy_combine_mlp(x)                      # [S, B, Hq*3]
+        S_, B_ = logits.shape[:2]
+        logits = logits.view(S_, B_, self.q_heads, 3).permute(3, 1, 0, 2)   # [3, B, S, Hq]
+        return torch.softmax(logits.float(), dim=0).type_as(x).unsqueeze(-1)
+
+    def forward(self, x):
+        S_, B_ = x.shape[:2]
+        q = self.to_q(x).view(S_, B_, self.q_heads, -1).transpose(0, 1)
+        k = self.to_k(x).view(S_, B_, self.kv_heads, -1).transpose(0, 1)
+        v = self.to_v(x).view(S_, B_, self.kv_heads, -1).transpose(0, 1)
+        w = self.generate_strategy_weights(x)
+        if self.q_rope is not None:
+            q = self.q_rope(q)
+            k = self.k_rope(k)
+        out = mosaic_attn_func(q=q, k=k, v=v, weight_ba_cmp_slc=w, block_attn_size=self.block_attn_size,
+                               sparse_block_size=self.sparse_block_size,
+                               sparse_block_count=self.sparse_block_count,
+                               block_attn_only=self.block_attn_only, no_compression=self.no_compression)
+        out = out.transpose(0, 1).reshape(S_, B_, -1)
+        return self.to_o(out)

@@ -1,0 +1,109 @@
+"""C-ABI checks that need no GPU: the library loads, exports every declared symbol, and rejects
+invalid arguments on the host before any launch (CPU only)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from mosaic_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mosaic_bsa.h")
+
+pytestmark = pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH),
+                                reason="libmosaic_bsa.so not built (python -m mosaic_amd.build)")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"MOSAIC_API\s+[\w\s\*]+?\b(mosaic_\w+)\s*\(", text)))
+
+
+def test_header_declarations_match_binding_list():
+    assert declared_symbols() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    handle = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_symbols():
+        assert hasattr(handle, name), name
+
+
+def test_abi_version_and_strerror():
+    L = _lib.lib()
+    assert L.mosaic_bsa_abi_version() == _lib.ABI_VERSION
+    assert _lib.strerror(0) == "ok"
+    for code in range(1, 12):
+        assert _lib.strerror(code) not in ("ok", "unknown status")
+    assert _lib.strerror(999) == "unknown status"
+
+
+FAKE = 1 << 20  # non-null, 16-byte aligned host address; never dereferenced (validation fails first)
+
+
+def _args(**kw):
+    a = _lib.BsaArgs()
+    a.batch, a.seq_len, a.num_q_heads, a.num_kv_heads, a.head_dim = 1, 3072, 20, 5, 64
+    a.block_attn_size, a.sparse_block_size, a.sparse_block_count = 64, 64, 4
+    a.mode = _lib.MODE_FULL
+    for name in ("q", "k", "v"):
+        setattr(a, name, _lib.Bnhd(FAKE, 3072 * 20 * 64, 20 * 64, 64))
+    a.weights, a.out = FAKE, FAKE
+    a.w_stride_s, a.w_stride_b, a.w_stride_n, a.w_stride_h = 3072 * 20, 3072 * 20, 20, 1
+    for key, val in kw.items():
+        setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize("change,status", [
+    (dict(head_dim=32), 2),
+    (dict(num_q_heads=21), 3),
+    (dict(num_q_heads=5 * 17), 11),
+    (dict(sparse_block_size=96), 4),
+    (dict(block_attn_size=100), 4),
+    (dict(sparse_block_count=49), 5),
+    (dict(sparse_block_count=0), 5),
+    (dict(mode=7), 10),
+    (dict(batch=0), 8),
+    (dict(out=None), 1),
+    (dict(weights=None), 1),
+    (dict(q=_lib.Bnhd(FAKE + 2, 0, 1280, 64)), 7),
+    (dict(q=_lib.Bnhd(FAKE, 0, 1281, 64)), 7),
+])
+def test_bsa_fwd_validation(change, status):
+    L = _lib.lib()
+    a = _args(**change)
+    assert L.mosaic_bsa_workspace_size(ctypes.byref(a)) == 0
+    assert L.mosaic_bsa_fwd(ctypes.byref(a), None, 0, None) == status
+
+
+def test_workspace_size_and_missing_workspace():
+    L = _lib.lib()
+    a = _args()
+    n = L.mosaic_bsa_workspace_size(ctypes.byref(a))
+    # q_cmp + k_cmp + v_cmp^T + compressed partials + scores + indices, each 256-aligned
+    nb, nbp, Hq, Hk, K = 48, 64, 20, 5, 4
+    assert n >= nb * Hq * 64 * 2 + nb * Hk * 64 * 2 + Hk * 64 * nbp * 2 + nb * Hq * 64 * 4 + Hk * nb * nbp * 2 + nb * Hk * K * 4
+    assert n % 256 == 0
+    assert L.mosaic_bsa_fwd(ctypes.byref(a), None, 0, None) == 6
+    assert L.mosaic_bsa_fwd(ctypes.byref(a), FAKE + 16, n, None) == 6   # misaligned
+    assert L.mosaic_bsa_fwd(ctypes.byref(a), FAKE, n - 1, None) == 6    # too small
+    local = _args(mode=_lib.MODE_LOCAL_ONLY, weights=None)
+    assert L.mosaic_bsa_workspace_size(ctypes.byref(local)) == 0
+
+
+def test_other_entry_points_validate():
+    L = _lib.lib()
+    t = _lib.Bnhd(FAKE, 0, 64 * 4, 64)
+    assert L.mosaic_sparse_attn_fwd(t, t, t, FAKE, 1, 256, 4, 1, 64, 64, 0, 0.0, FAKE, None, None) == 5
+    assert L.mosaic_sparse_attn_fwd(t, t, t, FAKE, 1, 256, 4, 3, 64, 64, 1, 0.0, FAKE, None, None) == 3
+    assert L.mosaic_sparse_attn_fwd(t, t, t, None, 1, 256, 4, 1, 64, 64, 1, 0.0, FAKE, None, None) == 1
+    assert L.mosaic_block_attn_fwd(t, t, t, 1, 256, 4, 1, 64, 96, 0.0, FAKE, None) == 4
+    assert L.mosaic_dense_attn_fwd(t, t, t, 1, 100, 4, 1, 64, 0.0, FAKE, None) == 4
+    assert L.mosaic_pool_mean_fwd(t, 1, 256, 4, 48, 64, FAKE, None) == 2
+    assert L.mosaic_attn_topk_fwd(t, t, 1, 48, 4, 1, 64, 49, FAKE, FAKE, 1 << 20, None) == 5
+    assert L.mosaic_attn_topk_fwd(t, t, 1, 48, 4, 1, 64, 4, FAKE, FAKE, 16, None) == 6
+    assert L.mosaic_attn_topk_fwd(t, t, 1, 9000, 4, 1, 64, 4, FAKE, FAKE, 1 << 30, None) == 11
+    assert L.mosaic_attn_topk_workspace_size(1, 48, 5) == ((5 * 48 * 64 * 2 + 255) // 256) * 256

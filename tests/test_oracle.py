@@ -1,0 +1,263 @@
+"""Pin the CPU oracle against checks that are independent of its own formulas (CPU only)."""
+
+import einops
+import pytest
+import torch
+
+from oracle import bsa_oracle as O
+
+bf16 = torch.bfloat16
+
+
+def _rand(*shape, seed=0, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(bf16)
+
+
+# ----------------------------------------------------------------------------- pooling
+def test_pool_mean_closed_form():
+    B, N, H, d, bs = 2, 256, 3, 64, 64
+    # value = token index (exact in bf16 up to 256); block mean = i*bs + (bs-1)/2
+    x = torch.arange(N, dtype=torch.float32).view(1, N, 1, 1).expand(B, N, H, d).to(bf16)
+    m = O.pool_mean(x, bs).float()
+    expect = torch.tensor([i * bs + (bs - 1) / 2 for i in range(N // bs)])
+    expect_bf = expect.to(bf16).float()
+    assert torch.equal(m[0, :, 0, 0], expect_bf)
+    assert m.shape == (B, N // bs, H, d)
+
+
+def test_pool_mean_matches_float64_rounding():
+    x = _rand(1, 1024, 4, 64, seed=1)
+    ref = x.double().reshape(1, 16, 64, 4, 64).mean(2).to(bf16)
+    got = O.pool_mean(x, 64)
+    mismatch = (ref != got).float().mean().item()
+    assert mismatch < 1e-3  # fp32 summation order may flip a rare bf16 rounding
+
+
+# ----------------------------------------------------------------------------- scores / top-k
+def _scores_by_einops(q_cmp, k_cmp):
+    """The reference's expression evaluated by einops (primitives.py:37-47)."""
+    Hq, Hk = q_cmp.shape[2], k_cmp.shape[2]
+    G = Hq // Hk
+    k = k_cmp.repeat_interleave(G, dim=2)
+    s = torch.matmul(einops.rearrange(q_cmp, "b t h d -> b h t d"),
+                     einops.rearrange(k, "b t h d -> b h d t"))
+    return einops.reduce(s, "b (g h) t k -> b h t k", "mean", g=G)
+
+
+@pytest.mark.parametrize("Hq,Hk", [(12, 3), (20, 5), (16, 4), (4, 4)])
+def test_topk_scores_equal_einops(Hq, Hk):
+    q_cmp = _rand(2, 48, Hq, 64, seed=2, scale=0.125)
+    k_cmp = _rand(2, 48, Hk, 64, seed=3, scale=0.125)
+    assert torch.equal(O.topk_scores(q_cmp, k_cmp), _scores_by_einops(q_cmp, k_cmp))
+
+
+def test_strided_group_is_not_contiguous_group():
+    """A contiguous '(h g)' mean would be a plausible mistake: it must give different scores."""
+    Hq, Hk = 12, 3
+    G = Hq // Hk
+    q_cmp = _rand(1, 32, Hq, 64, seed=4, scale=0.125)
+    k_cmp = _rand(1, 32, Hk, 64, seed=5, scale=0.125)
+    k = k_cmp.repeat_interleave(G, dim=2)
+    s = torch.matmul(q_cmp.permute(0, 2, 1, 3), k.permute(0, 2, 3, 1))
+    wrong = einops.reduce(s, "b (h g) t k -> b h t k", "mean", g=G)
+    assert not torch.equal(O.topk_scores(q_cmp, k_cmp), wrong)
+
+
+def test_topk_scores_golden_fixture():
+    data = torch.load(O_GOLDEN, weights_only=True)
+    got = O.topk_scores(data["q_cmp"], data["k_cmp"])
+    assert torch.equal(got, data["scores"])
+    idx = O.attn_topk(data["q_cmp"], data["k_cmp"], int(data["block_count"]))
+    bad, _, _ = O.selection_band_check(got.permute(0, 2, 1, 3), idx, int(data["block_count"]))
+    assert bad == 0
+    bad, _, _ = O.selection_band_check(got.permute(0, 2, 1, 3), data["indices"], int(data["block_count"]))
+    assert bad == 0
+
+
+O_GOLDEN = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "topk_scores_small.pt")
+
+
+def test_attn_topk_brute_force():
+    q_cmp = _rand(1, 24, 8, 64, seed=6, scale=0.125)
+    k_cmp = _rand(1, 24, 2, 64, seed=7, scale=0.125)
+    K = 5
+    idx = O.attn_topk(q_cmp, k_cmp, K)
+    s = O.topk_scores(q_cmp, k_cmp).float()  # B h t u
+    for t in range(24):
+        for h in range(2):
+            row = s[0, h, t]
+            order = sorted(range(24), key=lambda u: (-row[u].item(), u))
+            kth = row[order[K - 1]].item()
+            chosen = set(idx[0, t, h].tolist())
+            assert len(chosen) == K
+            assert {u for u in range(24) if row[u].item() > kth} <= chosen
+            assert all(row[u].item() >= kth for u in chosen)
+            # sorted descending
+            vals = [row[u].item() for u in idx[0, t, h].tolist()]
+            assert vals == sorted(vals, reverse=True)
+
+
+def test_attn_topk_planted_winners():
+    """k_cmp rows aligned with every query head's q_cmp make chosen blocks known analytically."""
+    B, nb, Hq, Hk, d, K = 1, 32, 8, 2, 64, 4
+    g = torch.Generator().manual_seed(8)
+    q_cmp = (torch.randn(B, nb, Hq, d, generator=g) * 0.01).to(bf16)
+    q_cmp[..., 0] = 1.0                     # all query heads share a large component on dim 0
+    k_cmp = (torch.randn(B, nb, Hk, d, generator=g) * 0.01).to(bf16)
+    winners = {0: [3, 17, 29, 8], 1: [30, 1, 12, 22]}
+    for c, blocks in winners.items():
+        for rank, u in enumerate(blocks):
+            k_cmp[0, u, c, 0] = 4.0 - rank * 0.5   # distinct margins >> noise
+    # row h averages query heads h, h+2, h+4, h+6 -> kv heads (h//4, (h+2)//4, ...) = mix of both
+    # kv heads; with G=4, query heads {0,2,4,6} -> kv {0,0,1,1}: both kv heads' winners count
+    # half each, so the row's top-4 are the blocks with the largest mean planted value.
+    idx = O.attn_topk(q_cmp, k_cmp, K)
+    planted = torch.zeros(nb)
+    for c, blocks in winners.items():
+        for rank, u in enumerate(blocks):
+            planted[u] += (4.0 - rank * 0.5) / 2
+    expect = planted.topk(K).indices.tolist()
+    for h in range(Hk):
+        for t in range(nb):
+            assert set(idx[0, t, h].tolist()) == set(expect)
+
+
+# ----------------------------------------------------------------------------- dense / local
+def test_dense_attention_matches_sdpa():
+    q = _rand(2, 96, 8, 64, seed=9)
+    k = _rand(2, 96, 2, 64, seed=10)
+    v = _rand(2, 96, 2, 64, seed=11)
+    got = O.dense_attention(q, k, v).float()
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.float().transpose(1, 2), k.float().transpose(1, 2), v.float().transpose(1, 2),
+        enable_gqa=True).transpose(1, 2)
+    assert (got - ref).abs().max().item() < 1e-2  # bf16 output rounding only
+
+
+def _brute_masked_attention(q, k, v, mask, scale, prescale_bf16=False):
+    """float64 softmax attention with an explicit [B, Hq, N, N] boolean mask."""
+    Hq, Hk = q.shape[2], k.shape[2]
+    G = Hq // Hk
+    qd = q.double()
+    if prescale_bf16:
+        qd = ((q.float() * scale) * O.LOG2E).to(bf16).double()
+        s = torch.einsum("bnhd,bmhd->bhnm", qd, k.double().repeat_interleave(G, 2)) / O.LOG2E
+    else:
+        s = torch.einsum("bnhd,bmhd->bhnm", qd, k.double().repeat_interleave(G, 2)) * scale
+    s = s.masked_fill(~mask, float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    return torch.einsum("bhnm,bmhd->bnhd", p, v.double().repeat_interleave(G, 2))
+
+
+def test_block_attention_equals_block_diagonal_mask():
+    B, N, Hq, Hk, d, bs = 1, 192, 4, 1, 64, 64
+    q, k, v = _rand(B, N, Hq, d, seed=12), _rand(B, N, Hk, d, seed=13), _rand(B, N, Hk, d, seed=14)
+    blk = torch.arange(N) // bs
+    mask = (blk[:, None] == blk[None, :]).expand(B, Hq, N, N)
+    ref = _brute_masked_attention(q, k, v, mask, d ** -0.5)
+    got = O.block_attention(q, k, v, bs).double()
+    assert (got - ref).abs().max().item() < 1e-2
+    # one block covering the whole sequence is plain dense attention
+    full = O.block_attention(q, k, v, N).double()
+    ref_full = _brute_masked_attention(q, k, v, torch.ones(B, Hq, N, N, dtype=torch.bool), d ** -0.5)
+    assert (full - ref_full).abs().max().item() < 1e-2
+
+
+# ----------------------------------------------------------------------------- selected branch
+def _selected_mask(idx, N, bs, Hq, Hk):
+    B, nb, _, K = idx.shape
+    G = Hq // Hk
+    mask = torch.zeros(B, Hq, N, N, dtype=torch.bool)
+    for b in range(B):
+        for i in range(nb):
+            for j in range(Hq):
+                for u in idx[b, i, j // G].tolist():
+                    mask[b, j, i * bs:(i + 1) * bs, u * bs:(u + 1) * bs] = True
+    return mask
+
+
+def test_sparse_attn_equals_masked_dense():
+    B, N, Hq, Hk, d, bs, K = 1, 512, 4, 2, 64, 64, 3
+    q, k, v = _rand(B, N, Hq, d, seed=15), _rand(B, N, Hk, d, seed=16), _rand(B, N, Hk, d, seed=17)
+    g = torch.Generator().manual_seed(18)
+    nb = N // bs
+    idx = torch.stack([torch.randperm(nb, generator=g)[:K] for _ in range(B * nb * Hk)]).view(B, nb, Hk, K)
+    o, lse = O.sparse_attn_fwd(q, k, v, idx, bs)
+    mask = _selected_mask(idx, N, bs, Hq, Hk)
+    ref = _brute_masked_attention(q, k, v, mask, d ** -0.5, prescale_bf16=True)
+    err = (o.double() - ref).abs().max().item()
+    assert err < 2e-2
+    # LSE (base 2) of the pre-scaled logits, brute force
+    G = Hq // Hk
+    qs = ((q.float() * d ** -0.5) * O.LOG2E).to(bf16).double()
+    s = torch.einsum("bnhd,bmhd->bhnm", qs, k.double().repeat_interleave(G, 2)).masked_fill(~mask, float("-inf"))
+    lse_ref = torch.logsumexp(s * torch.log(torch.tensor(2.0, dtype=torch.float64)), -1) / torch.log(torch.tensor(2.0, dtype=torch.float64))
+    assert (lse.double() - lse_ref.transpose(1, 2)).abs().max().item() < 1e-4
+
+
+def test_sparse_attn_all_blocks_is_dense_and_own_block_is_local():
+    B, N, Hq, Hk, d, bs = 1, 256, 4, 1, 64, 64
+    q, k, v = _rand(B, N, Hq, d, seed=19), _rand(B, N, Hk, d, seed=20), _rand(B, N, Hk, d, seed=21)
+    nb = N // bs
+    all_idx = torch.arange(nb).view(1, 1, 1, nb).expand(B, nb, Hk, nb).contiguous()
+    o, _ = O.sparse_attn_fwd(q, k, v, all_idx, bs)
+    dense = O.dense_attention(q, k, v).float()
+    assert (o.float() - dense).abs().max().item() < 2e-2
+    own = torch.arange(nb).view(1, nb, 1, 1).expand(B, nb, Hk, 1).contiguous()
+    o2, _ = O.sparse_attn_fwd(q, k, v, own, bs)
+    local = O.block_attention(q, k, v, bs).float()
+    assert (o2.float() - local).abs().max().item() < 2e-2
+
+
+def test_sparse_attn_q_block_subset_matches_full():
+    B, N, Hq, Hk, d, bs, K = 1, 512, 4, 1, 64, 64, 2
+    q, k, v = _rand(B, N, Hq, d, seed=22), _rand(B, N, Hk, d, seed=23), _rand(B, N, Hk, d, seed=24)
+    nb = N // bs
+    idx = torch.stack([torch.arange(K) + i % (nb - K) for i in range(nb)]).view(1, nb, 1, K)
+    full, lse_full = O.sparse_attn_fwd(q, k, v, idx, bs)
+    sub = torch.tensor([1, 5, 6])
+    part, lse_part = O.sparse_attn_fwd(q, k, v, idx, bs, q_blocks=sub)
+    for i in sub.tolist():
+        sl = slice(i * bs, (i + 1) * bs)
+        assert torch.equal(part[:, sl], full[:, sl])
+        assert torch.equal(lse_part[:, sl], lse_full[:, sl])
+
+
+# ----------------------------------------------------------------------------- merge / variants
+def test_merge_closed_forms():
+    B, N, Hq, Hk, d = 1, 256, 4, 1, 64
+    q, k, v = _rand(B, N, Hq, d, seed=25), _rand(B, N, Hk, d, seed=26), _rand(B, N, Hk, d, seed=27)
+    one = torch.ones(B, N, Hq, 1, dtype=bf16)
+    zero = torch.zeros_like(one)
+    out, parts = O.mosaic_attn_func(q, k, v, torch.stack([one, zero, zero]), 64, 64, 2, False, return_parts=True)
+    assert torch.equal(out, parts["o_ba"])
+    out, parts = O.mosaic_attn_func(q, k, v, torch.stack([zero, one, zero]), 64, 64, 2, False, return_parts=True)
+    assert torch.equal(out, parts["o_cmp_blk"].repeat_interleave(64, dim=1))
+    out, parts = O.mosaic_attn_func(q, k, v, torch.stack([zero, zero, one]), 64, 64, 2, False, return_parts=True)
+    assert torch.equal(out, parts["o_slc"])
+    # no_compression with equal weights: the average of local and selected
+    half = torch.full_like(one, 0.5)
+    out, parts = O.mosaic_attn_func(q, k, v, torch.stack([half, half, half]), 64, 64, 2, False,
+                                    no_compression=True, return_parts=True)
+    avg = (parts["o_ba"].float() + parts["o_slc"].float()) / 2
+    assert (out.float() - avg).abs().max().item() < 1e-2
+    # K == 0: local and compressed renormalised
+    out, parts = O.mosaic_attn_func(q, k, v, torch.stack([half, half, half]), 64, 64, 0, False, return_parts=True)
+    avg = (parts["o_ba"].float() + parts["o_cmp_blk"].repeat_interleave(64, 1).float()) / 2
+    assert (out.float() - avg).abs().max().item() < 1e-2
+    # block_attn_only returns the local branch
+    assert torch.equal(O.mosaic_attn_func(q, k, v, None, 64, 64, 2, True), parts["o_ba"])
+
+
+# ----------------------------------------------------------------------------- band rule
+def test_band_check_catches_wrong_selection():
+    s = torch.tensor([[[[0.9, 0.8, 0.1, 0.05, 0.7]]]])
+    good = torch.tensor([[[[0, 1, 4]]]])
+    assert O.selection_band_check(s, good, 3)[0] == 0
+    bad = torch.tensor([[[[0, 1, 2]]]])
+    assert O.selection_band_check(s, bad, 3)[0] == 1
+    dup = torch.tensor([[[[0, 0, 1]]]])
+    assert O.selection_band_check(s, dup, 3)[0] == 1
+    tie = torch.tensor([[[[0.9, 0.8, 0.5, 0.5, 0.1]]]])
+    assert O.selection_band_check(tie, torch.tensor([[[[0, 1, 3]]]]), 3)[:2] == (0, 1)
