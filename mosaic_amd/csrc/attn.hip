@@ -1,8 +1,8 @@
 // attn.hip -- fused local + selected-block attention with the gated merge (gfx950).
 //
 // One workgroup = (batch b, kv head c, 64-token query tile, group of NW query heads).
-// Each wave owns one query head j = c*G + ... of the GQA group and all 64 query rows of the
-// tile; the K/V tiles of 64 keys are loaded once into LDS and read by all NW waves.
+// Each wave owns one query head j of the GQA group and all 64 query rows of the tile; the
+// K/V tiles of 64 keys are loaded once into LDS and read by all NW waves.
 //
 //   local branch     block_attention / flash_attn_func (primitives.py:28-32): the keys of
 //                    the query's block_attn_size block, logits q.k * scale, fp32 online
@@ -11,8 +11,21 @@
 //                    and rounded to bf16 (:92), the sparse_block_size blocks named by the
 //                    top-k indices in order (:94-95), base-2 online softmax (:120-128),
 //                    P -> bf16 before PV (:128), O / l and LSE = m + log2(l) (:130-131).
-//   merge            primitives.py:62-89 in fp32 in the epilogue, with the compressed branch
-//                    read from the partial results of the compressed-attention kernel.
+//   merge            primitives.py:62-89 in fp32 in the epilogue; the compressed branch is
+//                    read from the split partial results of the compressed-attention kernel.
+//
+// Tiles of both branches form one sequence [local tiles..., selected tiles...] streamed
+// through a double-buffered LDS ring with one barrier per tile: tile t+1 is written to the
+// other buffer after tile t's compute, from registers loaded one tile earlier.
+//
+// The softmax rescale is lazy: a row's reference max only moves when a tile's max exceeds
+// it by more than kTau (log2 units), so P = exp2(s - m) <= 2^kTau and, after the first tile,
+// the O accumulators are touched by MFMA only.  The result is the same softmax: numerator
+// and denominator share the reference max.  Row sums are taken from the bf16-rounded P with
+// v_dot2c_f32_bf16, i.e. from the same values that enter the PV product.
+//
+// Two workgroups share a CU (2 waves per SIMD): one wave's softmax VALU work overlaps the
+// other's MFMA work.  The local branch's partial merge (w0 * o_ba) waits in LDS as bf16.
 //
 // S^T = K Q^T and O^T = V^T P^T are computed so a lane owns one query column (see
 // bsa_common.h).  K is kept row-major in LDS (A operand rows = keys); V is transposed while
@@ -24,6 +37,10 @@ namespace {
 
 constexpr int KS = 72;  // K tile row stride in bf16 (144 B): 16-lane b128 reads hit distinct banks
 constexpr int VS = 68;  // V^T tile row stride in bf16 (136 B): 32-lane b64 reads hit distinct banks
+constexpr int PS = 68;  // merge-partial row stride in bf16
+constexpr int kKTile = 64 * KS;
+constexpr int kVTile = 64 * VS;
+constexpr float kTau = 8.0f;
 
 template <int NW>
 struct TileLoader {
@@ -33,8 +50,8 @@ struct TileLoader {
     uint4 kr[KCH];
     uint4 v0[VCH], v1[VCH];
 
-    __device__ __forceinline__ void load(const bf16_t* kb, const bf16_t* vb, int64_t ksn,
-                                         int64_t vsn, int key0, int tid) {
+    __device__ __forceinline__ void load(const bf16_t* kb, const bf16_t* vb, int64_t ksn, int64_t vsn, int key0,
+                                         int tid) {
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
             const int c = tid + i * NT, row = c >> 3, ch = c & 7;
@@ -76,45 +93,18 @@ struct TileLoader {
     }
 };
 
-struct WaveState {
-    f32x16 o[2][2];  // O^T accumulators [d tile][query tile]
-    float m[2];      // running max of the logits (log2 units) per query tile
-    float l[2];      // this lane's partial softmax denominator per query tile
-
-    __device__ __forceinline__ void reset() {
+__device__ __forceinline__ void zero(f32x16 (&x)[2][2]) {
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+        for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) o[dt][qt][e] = 0.f;
-        m[0] = m[1] = -INFINITY;
-        l[0] = l[1] = 0.f;
-    }
-};
-
-__device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
-    uint4 u;
-    u.x = pack_bf16x2(s[base + 0], s[base + 1]);
-    u.y = pack_bf16x2(s[base + 2], s[base + 3]);
-    u.z = pack_bf16x2(s[base + 4], s[base + 5]);
-    u.w = pack_bf16x2(s[base + 6], s[base + 7]);
-    return as_bf16x8(u);
+            for (int e = 0; e < 16; ++e) x[a][b][e] = 0.f;
 }
 
-// One 64-key tile: S^T = K Q^T, online softmax update, O^T += V^T P^T.
-// SCALED: logits = S * c (local branch, unscaled q); otherwise logits = S (q pre-scaled).
-template <bool SCALED>
-__device__ __forceinline__ void attend_tile(const bf16_t* Ks, const bf16_t* Vt, const bf16x8 (&qf)[2][4],
-                                            WaveState& st, float c, int r, int hh) {
-    f32x16 s[2][2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) s[kt][qt][e] = 0.f;
-
+// S^T = K Q^T for one 64-key tile: s[key tile][query tile]
+__device__ __forceinline__ void s_tile(const bf16_t* Ks, const bf16x8 (&qf)[2][4], f32x16 (&s)[2][2], int r, int hh) {
+    zero(s);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
@@ -124,64 +114,97 @@ __device__ __forceinline__ void attend_tile(const bf16_t* Ks, const bf16_t* Vt, 
             for (int qt = 0; qt < 2; ++qt) s[kt][qt] = mfma32(a, qf[qt][ds], s[kt][qt]);
         }
     }
+}
 
-    bf16x8 pb[2][2][2];  // [query tile][key tile][16-key step]
+// O^T += V^T P^T for one 64-key tile
+__device__ __forceinline__ void pv_tile(const bf16_t* Vt, const bf16x8 (&pb)[2][2][2], f32x16 (&o)[2][2], int r,
+                                        int hh) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) {
+                const bf16_t* vp = Vt + (32 * dt + r) * VS + 32 * kt + 16 * s2 + 4 * hh;
+                const uint2 lo = ld8(vp), hi = ld8(vp + 8);
+                const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma32(a, pb[qt][kt][s2], o[dt][qt]);
+            }
+}
+
+// Online softmax of one tile with lazy rescaling.  Logits are s * c when SCALED, else s.
+// m: reference max per query tile (log2 units); l: this lane's partial denominators.
+template <bool SCALED>
+__device__ __forceinline__ void softmax_tile(f32x16 (&s)[2][2], float (&m)[2], float (&l)[2], f32x16 (&o)[2][2],
+                                             bf16x8 (&pb)[2][2][2], float c) {
+    float mt[2];
+    bool need = false;
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-        float mx = -INFINITY;
+        float mx = s[0][qt][0];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][qt][e]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(st.m[qt], SCALED ? mx * c : mx);
-        const float alpha = __builtin_amdgcn_exp2f(st.m[qt] - mnew);
-        float sum = 0.f;
+        mt[qt] = SCALED ? mx * c : mx;
+        need |= mt[qt] > m[qt] + kTau;
+    }
+    if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform; rare after a row's first tile
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int qt = 0; qt < 2; ++qt) {
+            const float mnew = mt[qt] > m[qt] + kTau ? mt[qt] : m[qt];
+            const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);  // 0 on a row's first tile
+            l[qt] *= alpha;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float x = SCALED ? fmaf(s[kt][qt][e], c, -mnew) : s[kt][qt][e] - mnew;
-                const float pe = __builtin_amdgcn_exp2f(x);
-                s[kt][qt][e] = pe;
-                sum += pe;
-            }
-        st.l[qt] = st.l[qt] * alpha + sum;
-        st.m[qt] = mnew;
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) st.o[dt][qt] *= alpha;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            pb[qt][kt][0] = pack8(s[kt][qt], 0);
-            pb[qt][kt][1] = pack8(s[kt][qt], 8);
+            for (int dt = 0; dt < 2; ++dt) o[dt][qt] *= alpha;
+            m[qt] = mnew;
         }
     }
-
+    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+    for (int qt = 0; qt < 2; ++qt) {
+        const float mm = m[qt];
+        float lsum[2] = {0.f, 0.f};
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
-                const bf16_t* vp = Vt + (32 * dt + r) * VS + 32 * kt + 16 * s2 + 4 * hh;
-                const uint2 lo = ld8(vp), hi = ld8(vp + 8);
-                const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+                uint32_t w[4];
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) st.o[dt][qt] = mfma32(a, pb[qt][kt][s2], st.o[dt][qt]);
+                for (int i = 0; i < 4; ++i) {
+                    const float x0 = s[kt][qt][8 * s2 + 2 * i], x1 = s[kt][qt][8 * s2 + 2 * i + 1];
+                    const float p0 = __builtin_amdgcn_exp2f(SCALED ? fmaf(x0, c, -mm) : x0 - mm);
+                    const float p1 = __builtin_amdgcn_exp2f(SCALED ? fmaf(x1, c, -mm) : x1 - mm);
+                    w[i] = pack_bf16x2(p0, p1);
+                    lsum[kt] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), ones, lsum[kt], false);
+                }
+                pb[qt][kt][s2] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
             }
+        l[qt] += lsum[0] + lsum[1];
+    }
 }
 
 __device__ __forceinline__ float load_bf16(const bf16_t* p) { return bf2f(*p); }
 
-template <int NW, int MODE, typename IdxT>
-__global__ __launch_bounds__(NW * 64) void bsa_attn_kernel(AttnParams p) {
-    __shared__ __attribute__((aligned(16))) bf16_t Ks[64 * KS];
-    __shared__ __attribute__((aligned(16))) bf16_t Vt[64 * VS];
+template <int MODE>
+struct AttnLds {
+    static constexpr bool kPartial = MODE == kModeFull || MODE == kModeNoCompression;
+};
 
+template <int NW, int MODE, typename IdxT>
+__global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(2, 2)))
+void bsa_attn_kernel(AttnParams p) {
     constexpr bool kLocal = MODE != kModeSelectedOnly;
     constexpr bool kSel = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeSelectedOnly;
     constexpr bool kCmp = MODE == kModeFull || MODE == kModeNoSelection;
     constexpr bool kWeights = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeNoSelection;
+    constexpr bool kPartial = AttnLds<MODE>::kPartial;
+
+    __shared__ __attribute__((aligned(16))) bf16_t Ks[2 * kKTile];
+    __shared__ __attribute__((aligned(16))) bf16_t Vt[2 * kVTile];
+    __shared__ __attribute__((aligned(16))) bf16_t Part[kPartial ? NW * 64 * PS : 8];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, hh = lane >> 5;
     const int L = xcd_remap(blockIdx.x, p.total_wgs);
@@ -198,6 +221,24 @@ __global__ __launch_bounds__(NW * 64) void bsa_attn_kernel(AttnParams p) {
     const bf16_t* kb = p.k + b * p.k_sb + (int64_t)c * p.k_sh;
     const bf16_t* vb = p.v + b * p.v_sb + (int64_t)c * p.v_sh;
 
+    // tile sequence: [local tiles][selected tiles]
+    const int tl_count = kLocal ? p.bs_l / kTile : 0;
+    const int lstart = (n0 / p.bs_l) * p.bs_l;
+    const int sub = p.bs / kTile;
+    const int ts_count = kSel ? p.K * sub : 0;
+    const IdxT* ip = reinterpret_cast<const IdxT*>(p.idx) + ((int64_t)(b * p.nb + n0 / p.bs) * p.Hk + c) * p.K;
+    auto tile_key0 = [&](int t, bool& valid) -> int {
+        if (kLocal && t < tl_count) {
+            valid = true;
+            return lstart + kTile * t;
+        }
+        const int ts = t - tl_count;
+        const int64_t blk = (int64_t)ip[ts / sub];
+        valid = blk >= 0 && blk < p.nb;
+        return (int)((valid ? blk : 0) * p.bs) + (ts % sub) * kTile;
+    };
+    const int total_tiles = tl_count + ts_count;
+
     bf16x8 qf[2][4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt)
@@ -205,115 +246,94 @@ __global__ __launch_bounds__(NW * 64) void bsa_attn_kernel(AttnParams p) {
         for (int ds = 0; ds < 4; ++ds)
             qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
 
-    // gate weights of this lane's two query rows
-    float wgt[2][3];
-    if constexpr (kWeights) {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-            for (int sidx = 0; sidx < 3; ++sidx)
-                wgt[qt][sidx] = load_bf16(p.w + sidx * p.w_ss + b * p.w_sb + (int64_t)(n0 + 32 * qt + r) * p.w_sn +
-                                          (int64_t)j * p.w_sh);
+    TileLoader<NW> tl;
+    bool valid_cur, valid_next = false;
+    {
+        int key0 = tile_key0(0, valid_cur);
+        tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
+        tl.store(Ks, Vt, tid);
+        if (total_tiles > 1) {
+            key0 = tile_key0(1, valid_next);
+            tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
+        }
     }
 
-    TileLoader<NW> tl;
-    WaveState st;
-    f32x16 acc[2][2];  // merge accumulator (fp32), same layout as st.o
+    f32x16 o[2][2], s[2][2];
+    bf16x8 pb[2][2][2];
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    zero(o);
+
+    auto advance = [&](int t) {
+        // after tile t's compute: publish tile t+1 into the other buffer, prefetch tile t+2
+        if (t + 1 < total_tiles) {
+            tl.store(Ks + ((t + 1) & 1) * kKTile, Vt + ((t + 1) & 1) * kVTile, tid);
+            valid_cur = valid_next;
+            if (t + 2 < total_tiles) {
+                const int key0 = tile_key0(t + 2, valid_next);
+                tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
+            }
+        }
+    };
 
     bf16_t* outp = p.out + ((int64_t)b * p.N + n0) * p.Hq * kHeadDim + (int64_t)j * kHeadDim;
-    auto store_out = [&](const f32x16 (&val)[2][2]) {
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    uint2 w2;
-                    w2.x = pack_bf16x2(val[dt][qt][4 * g4 + 0], val[dt][qt][4 * g4 + 1]);
-                    w2.y = pack_bf16x2(val[dt][qt][4 * g4 + 2], val[dt][qt][4 * g4 + 3]);
-                    *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
-                }
-    };
 
     // ------------------------------------------------------------------ local branch
     if constexpr (kLocal) {
-        st.reset();
-        const int lstart = (n0 / p.bs_l) * p.bs_l;
-        const int ntiles = p.bs_l / kTile;
-        tl.load(kb, vb, p.k_sn, p.v_sn, lstart, tid);
-        for (int t = 0; t < ntiles; ++t) {
+        for (int t = 0; t < tl_count; ++t) {
             __syncthreads();
-            tl.store(Ks, Vt, tid);
-            __syncthreads();
-            if (t + 1 < ntiles) tl.load(kb, vb, p.k_sn, p.v_sn, lstart + kTile * (t + 1), tid);
-            attend_tile<true>(Ks, Vt, qf, st, p.scale_log2, r, hh);
+            const int buf = t & 1;
+            s_tile(Ks + buf * kKTile, qf, s, r, hh);
+            softmax_tile<true>(s, m, l, o, pb, p.scale_log2);
+            pv_tile(Vt + buf * kVTile, pb, o, r, hh);
+            advance(t);
         }
         float inv[2];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) inv[qt] = 1.f / (st.l[qt] + __shfl_xor(st.l[qt], 32));
+        for (int qt = 0; qt < 2; ++qt) inv[qt] = 1.f / (l[qt] + __shfl_xor(l[qt], 32));
 
-        if constexpr (MODE == kModeLocalOnly) {
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) acc[dt][qt] = st.o[dt][qt] * inv[qt];
-            store_out(acc);
-            return;
-        } else {
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) acc[dt][qt] = st.o[dt][qt] * (inv[qt] * wgt[qt][0]);
-        }
-    }
-
-    // ------------------------------------------------------------------ compressed branch
-    if constexpr (kCmp) {
-        // Combine the split partial results of block tq for head j: each split holds an
-        // unnormalised O and its (max, sum) in log2 units.
-        const int tq = n0 / p.bs;
-        const int64_t row0 = ((int64_t)b * p.nsplit * p.nb + tq) * p.Hq + j;  // split 0
-        const int64_t split_stride = (int64_t)p.nb * p.Hq;
-        float M = -INFINITY;
-        for (int sp = 0; sp < p.nsplit; ++sp) M = fmaxf(M, p.ml[row0 + sp * split_stride].x);
-        f32x16 oc[2];
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) oc[dt][e] = 0.f;
-        float Lsum = 0.f;
-        for (int sp = 0; sp < p.nsplit; ++sp) {
-            const float2 mlv = p.ml[row0 + sp * split_stride];
-            const float a = __builtin_amdgcn_exp2f(mlv.x - M);
-            Lsum += a * mlv.y;
-            const float* op = p.opart + (row0 + sp * split_stride) * kHeadDim;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const float4 v4 = *reinterpret_cast<const float4*>(op + 32 * dt + 8 * g4 + 4 * hh);
-                    oc[dt][4 * g4 + 0] += a * v4.x;
-                    oc[dt][4 * g4 + 1] += a * v4.y;
-                    oc[dt][4 * g4 + 2] += a * v4.z;
-                    oc[dt][4 * g4 + 3] += a * v4.w;
-                }
-        }
-        const float linv = 1.f / Lsum;
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            const float w1 = wgt[qt][1] * linv;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) acc[dt][qt] += oc[dt] * w1;
-        }
-        if constexpr (MODE == kModeNoSelection) {
+        if constexpr (MODE == kModeLocalOnly || MODE == kModeNoSelection || kPartial) {
+            float f[2];
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
-                const float nrm = 1.f / (wgt[qt][0] + wgt[qt][1] + 1e-8f);
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt) acc[dt][qt] *= nrm;
+                f[qt] = inv[qt];
+                if constexpr (kWeights) {
+                    const float w0 = load_bf16(p.w + b * p.w_sb + (int64_t)(n0 + 32 * qt + r) * p.w_sn + (int64_t)j * p.w_sh);
+                    f[qt] *= w0;
+                }
             }
-            store_out(acc);
-            return;
+            if constexpr (MODE == kModeLocalOnly) {
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; ++g4) {
+                            uint2 w2;
+                            w2.x = pack_bf16x2(o[dt][qt][4 * g4 + 0] * f[qt], o[dt][qt][4 * g4 + 1] * f[qt]);
+                            w2.y = pack_bf16x2(o[dt][qt][4 * g4 + 2] * f[qt], o[dt][qt][4 * g4 + 3] * f[qt]);
+                            *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                        }
+                return;
+            } else if constexpr (kPartial) {
+                // w0 * o_ba waits in LDS (bf16) while the selected branch runs
+                bf16_t* pp = Part + wave * 64 * PS;
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                        for (int g4 = 0; g4 < 4; ++g4) {
+                            uint2 w2;
+                            w2.x = pack_bf16x2(o[dt][qt][4 * g4 + 0] * f[qt], o[dt][qt][4 * g4 + 1] * f[qt]);
+                            w2.y = pack_bf16x2(o[dt][qt][4 * g4 + 2] * f[qt], o[dt][qt][4 * g4 + 3] * f[qt]);
+                            *reinterpret_cast<uint2*>(pp + (32 * qt + r) * PS + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                        }
+            } else {  // no selection: keep w0 * o_ba in registers for the epilogue
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                    for (int dt = 0; dt < 2; ++dt) o[dt][qt] *= f[qt];
+            }
         }
     }
 
@@ -328,70 +348,122 @@ __global__ __launch_bounds__(NW * 64) void bsa_attn_kernel(AttnParams p) {
                 const uint32_t w[4] = {u.x, u.y, u.z, u.w};
                 uint32_t o4[4];
 #pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    o4[m] = pack_bf16x2((bf_lo(w[m]) * p.scale) * kLog2e, (bf_hi(w[m]) * p.scale) * kLog2e);
+                for (int mm = 0; mm < 4; ++mm)
+                    o4[mm] = pack_bf16x2((bf_lo(w[mm]) * p.scale) * kLog2e, (bf_hi(w[mm]) * p.scale) * kLog2e);
                 qf[qt][ds] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
             }
-        st.reset();
-        const int qblk = n0 / p.bs;
-        const IdxT* ip = reinterpret_cast<const IdxT*>(p.idx) + ((int64_t)(b * p.nb + qblk) * p.Hk + c) * p.K;
-        const int sub = p.bs / kTile;
-        const int ntiles = p.K * sub;
-        auto tile_key0 = [&](int t, bool& valid) {
-            const int64_t blk = (int64_t)ip[t / sub];
-            valid = blk >= 0 && blk < p.nb;
-            return (int)((valid ? blk : 0) * p.bs) + (t % sub) * kTile;
-        };
-        bool valid_next;
-        int key0 = tile_key0(0, valid_next);
-        tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
-        for (int t = 0; t < ntiles; ++t) {
-            const bool valid = valid_next;
+        zero(o);
+        m[0] = m[1] = -INFINITY;
+        l[0] = l[1] = 0.f;
+        for (int t = tl_count; t < total_tiles; ++t) {
             __syncthreads();
-            tl.store(Ks, Vt, tid);
-            __syncthreads();
-            if (t + 1 < ntiles) {
-                key0 = tile_key0(t + 1, valid_next);
-                tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
+            const int buf = t & 1;
+            if (valid_cur) {
+                s_tile(Ks + buf * kKTile, qf, s, r, hh);
+                softmax_tile<false>(s, m, l, o, pb, 1.f);
+                pv_tile(Vt + buf * kVTile, pb, o, r, hh);
             }
-            if (valid) attend_tile<false>(Ks, Vt, qf, st, 1.f, r, hh);
+            advance(t);
         }
+    }
+
+    // ------------------------------------------------------------------ epilogue
+    if constexpr (MODE == kModeSelectedOnly) {
         float ltot[2], inv[2];
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            ltot[qt] = st.l[qt] + __shfl_xor(st.l[qt], 32);
+            ltot[qt] = l[qt] + __shfl_xor(l[qt], 32);
             inv[qt] = 1.f / ltot[qt];
         }
-        if constexpr (MODE == kModeSelectedOnly) {
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) acc[dt][qt] = st.o[dt][qt] * inv[qt];
-            store_out(acc);
-            if (p.lse != nullptr && hh == 0) {
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    uint2 w2;
+                    w2.x = pack_bf16x2(o[dt][qt][4 * g4 + 0] * inv[qt], o[dt][qt][4 * g4 + 1] * inv[qt]);
+                    w2.y = pack_bf16x2(o[dt][qt][4 * g4 + 2] * inv[qt], o[dt][qt][4 * g4 + 3] * inv[qt]);
+                    *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                }
+        if (p.lse != nullptr && hh == 0) {
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt)
-                    p.lse[((int64_t)b * p.N + n0 + 32 * qt + r) * p.Hq + j] = st.m[qt] + __log2f(ltot[qt]);
-            }
-            return;
-        } else if constexpr (MODE == kModeFull) {
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                const float w2 = wgt[qt][2] * inv[qt];
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt) acc[dt][qt] += st.o[dt][qt] * w2;
-            }
-            store_out(acc);
-        } else {  // no compression: (o_ba*w0 + o_slc*w2) / (w0 + w2 + 1e-8)
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                const float nrm = 1.f / (wgt[qt][0] + wgt[qt][2] + 1e-8f);
-                const float w2 = wgt[qt][2] * inv[qt];
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt) acc[dt][qt] = (acc[dt][qt] + st.o[dt][qt] * w2) * nrm;
-            }
-            store_out(acc);
+            for (int qt = 0; qt < 2; ++qt)
+                p.lse[((int64_t)b * p.N + n0 + 32 * qt + r) * p.Hq + j] = m[qt] + __log2f(ltot[qt]);
         }
+        return;
+    } else if constexpr (kWeights) {
+        // per-row weights of the selected and compressed branches and the renormalisation
+        float fs[2], fc[2], nrm[2];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const int64_t woff = b * p.w_sb + (int64_t)(n0 + 32 * qt + r) * p.w_sn + (int64_t)j * p.w_sh;
+            const float w0 = load_bf16(p.w + woff);
+            const float w1 = load_bf16(p.w + p.w_ss + woff);
+            const float w2 = load_bf16(p.w + 2 * p.w_ss + woff);
+            if constexpr (kSel) fs[qt] = w2 / (l[qt] + __shfl_xor(l[qt], 32));
+            fc[qt] = w1;
+            nrm[qt] = MODE == kModeNoCompression ? 1.f / (w0 + w2 + 1e-8f)
+                    : MODE == kModeNoSelection ? 1.f / (w0 + w1 + 1e-8f) : 1.f;
+        }
+        f32x16 oc[2];  // compressed-branch output of block n0 / bs for head j (same for all rows)
+        if constexpr (kCmp) {
+            const int tq = n0 / p.bs;
+            const int64_t row0 = ((int64_t)b * p.nsplit * p.nb + tq) * p.Hq + j;
+            const int64_t split_stride = (int64_t)p.nb * p.Hq;
+            float M = -INFINITY;
+            for (int sp = 0; sp < p.nsplit; ++sp) M = fmaxf(M, p.ml[row0 + sp * split_stride].x);
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oc[dt][e] = 0.f;
+            float Lsum = 0.f;
+            for (int sp = 0; sp < p.nsplit; ++sp) {
+                const float2 mlv = p.ml[row0 + sp * split_stride];
+                const float a = __builtin_amdgcn_exp2f(mlv.x - M);
+                Lsum += a * mlv.y;
+                const float* op = p.opart + (row0 + sp * split_stride) * kHeadDim;
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        const float4 v4 = *reinterpret_cast<const float4*>(op + 32 * dt + 8 * g4 + 4 * hh);
+                        oc[dt][4 * g4 + 0] += a * v4.x;
+                        oc[dt][4 * g4 + 1] += a * v4.y;
+                        oc[dt][4 * g4 + 2] += a * v4.z;
+                        oc[dt][4 * g4 + 3] += a * v4.w;
+                    }
+            }
+            const float linv = 1.f / Lsum;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) oc[dt] *= linv;
+        }
+        const bf16_t* pp = Part + wave * 64 * PS;
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    float v[4];
+                    if constexpr (kPartial) {
+                        const uint2 pw = *reinterpret_cast<const uint2*>(pp + (32 * qt + r) * PS + 32 * dt + 8 * g4 + 4 * hh);
+                        v[0] = bf_lo(pw.x); v[1] = bf_hi(pw.x); v[2] = bf_lo(pw.y); v[3] = bf_hi(pw.y);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int jj = 4 * g4 + e;
+                        float x;
+                        if constexpr (kPartial) x = v[e] + o[dt][qt][jj] * fs[qt];
+                        else x = o[dt][qt][jj];  // no selection: o holds w0 * o_ba
+                        if constexpr (kCmp) x += oc[dt][jj] * fc[qt];
+                        v[e] = x * nrm[qt];
+                    }
+                    uint2 w2;
+                    w2.x = pack_bf16x2(v[0], v[1]);
+                    w2.y = pack_bf16x2(v[2], v[3]);
+                    *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                }
     }
 }
 

@@ -76,7 +76,9 @@ def test_sparse_attn_and_lse(B, N, Hq, Hk, bs, K):
     out, lse = M.mosaic_attn_fwd(*dev(q, k, v), idx.to(DEV), bs, 64 ** -0.5)
     ref, ref_lse = O.sparse_attn_fwd(q, k, v, idx, bs)
     close(out, ref)
-    assert (lse.cpu() - ref_lse).abs().max().item() < 1e-3
+    # The kernel's denominator sums the bf16-rounded probabilities (the values that multiply
+    # V); each carries <= 2^-9 relative rounding, so |log2(l'/l)| <= 2^-9 / ln 2 = 2.8e-3.
+    assert (lse.cpu() - ref_lse).abs().max().item() < 3e-3
     # the autograd wrapper returns the same output
     out2 = M.mosaic_sparse_attn(*dev(q, k, v), idx.to(DEV), bs)
     assert torch.equal(out2.cpu(), out.cpu())
