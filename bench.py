@@ -11,7 +11,8 @@ W warm-up steps, then K timed steps bracketed by device synchronisation; per-ker
 come from HIP events recorded between the kernels of every timed step, on the launch stream.
 
 Prints one JSON line.  Options: --gpus (only 1 is supported: the op runs on one GPU),
---steps, --warmup, --workload {nside64, nside32_b24, nside16, nside128}, --no-cpu-baseline.
+--steps, --warmup, --workload {nside64, nside32_b24, nside16, nside128}, --no-cpu-baseline,
+--calibration-copy-mb.
 """
 
 from __future__ import annotations
@@ -102,6 +103,9 @@ def main():
     ap.add_argument("--workload", default="nside64", choices=sorted(WORKLOADS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibration-copy-mb", type=int, default=0,
+                    help="after timing, run one device-to-device copy of this many MiB (a known-size "
+                         "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -218,6 +222,13 @@ def main():
         },
         "unet_24_member_step_ms": None,
     }
+    if args.calibration_copy_mb:
+        n = args.calibration_copy_mb << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = n
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, q_c, k_c, v_c, w_c)
     print(json.dumps(result))

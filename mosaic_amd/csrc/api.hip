@@ -8,7 +8,7 @@
 #include <cmath>
 
 #include "bsa_common.h"
-#include "../../include/mosaic_bsa.h"
+#include "mosaic_bsa.h"
 
 using namespace mosaic;
 
@@ -17,7 +17,7 @@ namespace {
 constexpr size_t kAlign = 256;
 constexpr int kMaxBlocksTopk = 8192;  // selection rows live in registers: 128 keys per lane
 constexpr int kMaxGroup = 16;         // query heads per kv head (one wave each in cmp_kernel)
-constexpr int kMaxSplits = 4;
+constexpr int kMaxSplits = 4;  // <= kMaxSplitsCombine
 
 size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 
@@ -56,7 +56,7 @@ int choose_splits(int B, int nb, int Hk) {
 
 struct Layout {
     int nb = 0, nb_pad = 0, nsplit = 1;
-    size_t qc = 0, kc = 0, vct = 0, sbar = 0, idx = 0, opart = 0, ml = 0, total = 0;
+    size_t qc = 0, kc = 0, vct = 0, sbar = 0, idx = 0, opart = 0, ml = 0, ocmp = 0, total = 0;
 };
 
 bool uses_selection(int mode) { return mode == MOSAIC_BSA_FULL || mode == MOSAIC_BSA_NO_COMPRESSION; }
@@ -85,6 +85,7 @@ int validate(const mosaic_bsa_args* a) {
     if (uses_selection(a->mode)) {
         if (a->sparse_block_count == 0) return MOSAIC_ERR_BLOCK_COUNT;
         if (nb > kMaxBlocksTopk || nb > 65535) return MOSAIC_ERR_UNSUPPORTED;
+        if (a->sparse_block_count > kMaxSelected) return MOSAIC_ERR_UNSUPPORTED;
     }
     return MOSAIC_OK;
 }
@@ -104,6 +105,7 @@ Layout layout_of(const mosaic_bsa_args* a) {
         L.vct = off; off = align_up(off + B * Hk * kHeadDim * nbp * 2);
         L.opart = off; off = align_up(off + B * U * nb * Hq * kHeadDim * 4);
         L.ml = off; off = align_up(off + B * U * nb * Hq * 8);
+        L.ocmp = off; off = align_up(off + B * nb * Hq * kHeadDim * 2);
     }
     if (uses_selection(a->mode)) {
         L.sbar = off; off = align_up(off + B * Hk * nb * nbp * 2);
@@ -126,7 +128,6 @@ AttnParams attn_params(const mosaic_bnhd& q, const mosaic_bnhd& k, const mosaic_
     p.total_wgs = B * Hk * p.head_groups * p.qtiles;
     p.scale = scale;
     p.scale_log2 = scale * kLog2e;
-    p.nsplit = 1;
     return p;
 }
 
@@ -191,8 +192,13 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         if (int e = launch_status(launch_cmp(cp, sel, cmp, s))) return e;
         if (int e = record(events, 2, s)) return e;
 
+        CombineParams cb{};
+        cb.opart = cp.opart; cb.ml = cp.ml; cb.nsplit = L.nsplit; cb.Hq = Hq;
+        cb.ocmp = cmp ? reinterpret_cast<bf16_t*>(w + L.ocmp) : nullptr;
         if (sel) {
             TopkParams tp{};
+            tp.G = Hq / Hk;
+            tp.cmb = cb;
             tp.sbar = cp.sbar;
             tp.idx32 = reinterpret_cast<int32_t*>(w + L.idx);
             tp.idx64 = a->block_indices_out;
@@ -200,11 +206,11 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
             tp.rows = B * Hk * L.nb;
             if (int e = launch_status(launch_topk(tp, s))) return e;
             ap.idx = tp.idx32;
+        } else if (cmp) {
+            if (int e = launch_status(launch_combine(cb, B, L.nb, s))) return e;
         }
         if (int e = record(events, 3, s)) return e;
-        ap.opart = cp.opart;
-        ap.ml = cp.ml;
-        ap.nsplit = L.nsplit;
+        ap.ocmp = cb.ocmp;
     } else {
         if (int e = record(events, 1, s)) return e;
         if (int e = record(events, 2, s)) return e;
@@ -246,6 +252,7 @@ int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const in
     if (block_indices == nullptr || out == nullptr) return MOSAIC_ERR_NULL_POINTER;
     if (!aligned16(out)) return MOSAIC_ERR_ALIGNMENT;
     if (block_size <= 0 || block_size % kTile || seq_len % block_size) return MOSAIC_ERR_BLOCK_SIZE;
+    if (block_count > kMaxSelected) return MOSAIC_ERR_UNSUPPORTED;
     AttnParams ap = attn_params(q, k, v, batch, seq_len, num_q_heads, num_kv_heads,
                                 resolve_scale(softmax_scale, head_dim));
     ap.out = static_cast<bf16_t*>(out);
@@ -326,6 +333,7 @@ int mosaic_attn_topk_fwd(mosaic_bnhd q_cmp, mosaic_bnhd k_cmp, int32_t batch, in
     tp.sbar = cp.sbar; tp.idx64 = indices_out;
     tp.B = batch; tp.nb = num_blocks; tp.nb_pad = nb_pad; tp.Hk = num_kv_heads; tp.K = block_count;
     tp.rows = batch * num_kv_heads * num_blocks;
+    tp.G = cp.G;
     return launch_status(launch_topk(tp, s));
 }
 
@@ -342,7 +350,7 @@ const char* mosaic_bsa_strerror(int status) {
         case MOSAIC_ERR_SHAPE: return "invalid sizes";
         case MOSAIC_ERR_LAUNCH: return "kernel launch failed";
         case MOSAIC_ERR_MODE: return "unknown mode";
-        case MOSAIC_ERR_UNSUPPORTED: return "outside the library's limits (query heads per kv head <= 16, blocks <= 8192)";
+        case MOSAIC_ERR_UNSUPPORTED: return "outside the library's limits (query heads per kv head <= 16, blocks <= 8192, selected blocks <= 1024)";
         default: return "unknown status";
     }
 }

@@ -205,6 +205,8 @@ void bsa_attn_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) bf16_t Ks[2 * kKTile];
     __shared__ __attribute__((aligned(16))) bf16_t Vt[2 * kVTile];
     __shared__ __attribute__((aligned(16))) bf16_t Part[kPartial ? NW * 64 * PS : 8];
+    __shared__ int sel_key0[kSel ? kMaxSelected : 1];  // first key of each in-range selected block
+    __shared__ int sel_count;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, hh = lane >> 5;
     const int L = xcd_remap(blockIdx.x, p.total_wgs);
@@ -221,23 +223,42 @@ void bsa_attn_kernel(AttnParams p) {
     const bf16_t* kb = p.k + b * p.k_sb + (int64_t)c * p.k_sh;
     const bf16_t* vb = p.v + b * p.v_sb + (int64_t)c * p.v_sh;
 
-    // tile sequence: [local tiles][selected tiles]
+    // tile sequence: [local tiles][tiles of the in-range selected blocks, in top-k order]
     const int tl_count = kLocal ? p.bs_l / kTile : 0;
     const int lstart = (n0 / p.bs_l) * p.bs_l;
     const int sub = p.bs / kTile;
-    const int ts_count = kSel ? p.K * sub : 0;
     const IdxT* ip = reinterpret_cast<const IdxT*>(p.idx) + ((int64_t)(b * p.nb + n0 / p.bs) * p.Hk + c) * p.K;
-    auto tile_key0 = [&](int t, bool& valid) -> int {
-        if (kLocal && t < tl_count) {
-            valid = true;
-            return lstart + kTile * t;
+    // Selected blocks: wave 0 compacts the in-range indices (top-k order kept) into LDS once,
+    // so the tile loop reads block offsets from LDS instead of waiting on a global load.
+    if constexpr (kSel) {
+        if (wave == 0) {
+            int count = 0;
+            for (int base = 0; base < p.K; base += 64) {
+                const int i = base + lane;
+                const int64_t blk = i < p.K ? (int64_t)ip[i] : -1;
+                const bool ok = blk >= 0 && blk < p.nb;
+                const uint64_t mask = __builtin_amdgcn_ballot_w64(ok);
+                const int pos = count + (int)__builtin_popcountll(mask & ((1ull << lane) - 1ull));
+                if (ok) sel_key0[pos] = (int)(blk * p.bs);
+                count += (int)__builtin_popcountll(mask);
+            }
+            if (lane == 0) sel_count = count;
         }
-        const int ts = t - tl_count;
-        const int64_t blk = (int64_t)ip[ts / sub];
-        valid = blk >= 0 && blk < p.nb;
-        return (int)((valid ? blk : 0) * p.bs) + (ts % sub) * kTile;
+        __syncthreads();
+    }
+    const int nvalid = kSel ? sel_count : 0;
+    const int total_tiles = tl_count + nvalid * sub;
+    // The loader asks for tiles in order 0, 1, 2, ...
+    int cur_k = 0, cur_s = 0;
+    auto next_key0 = [&](int t) -> int {
+        if (kLocal && t < tl_count) return lstart + kTile * t;
+        const int key0 = sel_key0[cur_k] + cur_s * kTile;
+        if (++cur_s == sub) {
+            cur_s = 0;
+            ++cur_k;
+        }
+        return key0;
     };
-    const int total_tiles = tl_count + ts_count;
 
     bf16x8 qf[2][4];
 #pragma unroll
@@ -246,16 +267,21 @@ void bsa_attn_kernel(AttnParams p) {
         for (int ds = 0; ds < 4; ++ds)
             qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
 
+    // compressed-branch output of this block and head (bf16), consumed in the epilogue
+    uint2 ocw[2][4];
+    if constexpr (kCmp) {
+        const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim + 4 * hh;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) ocw[dt][g4] = ld8(ocp + 32 * dt + 8 * g4);
+    }
+
     TileLoader<NW> tl;
-    bool valid_cur, valid_next = false;
-    {
-        int key0 = tile_key0(0, valid_cur);
-        tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
+    if (total_tiles > 0) {
+        tl.load(kb, vb, p.k_sn, p.v_sn, next_key0(0), tid);
         tl.store(Ks, Vt, tid);
-        if (total_tiles > 1) {
-            key0 = tile_key0(1, valid_next);
-            tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
-        }
+        if (total_tiles > 1) tl.load(kb, vb, p.k_sn, p.v_sn, next_key0(1), tid);
     }
 
     f32x16 o[2][2], s[2][2];
@@ -267,11 +293,7 @@ void bsa_attn_kernel(AttnParams p) {
         // after tile t's compute: publish tile t+1 into the other buffer, prefetch tile t+2
         if (t + 1 < total_tiles) {
             tl.store(Ks + ((t + 1) & 1) * kKTile, Vt + ((t + 1) & 1) * kVTile, tid);
-            valid_cur = valid_next;
-            if (t + 2 < total_tiles) {
-                const int key0 = tile_key0(t + 2, valid_next);
-                tl.load(kb, vb, p.k_sn, p.v_sn, key0, tid);
-            }
+            if (t + 2 < total_tiles) tl.load(kb, vb, p.k_sn, p.v_sn, next_key0(t + 2), tid);
         }
     };
 
@@ -358,11 +380,9 @@ void bsa_attn_kernel(AttnParams p) {
         for (int t = tl_count; t < total_tiles; ++t) {
             __syncthreads();
             const int buf = t & 1;
-            if (valid_cur) {
-                s_tile(Ks + buf * kKTile, qf, s, r, hh);
-                softmax_tile<false>(s, m, l, o, pb, 1.f);
-                pv_tile(Vt + buf * kVTile, pb, o, r, hh);
-            }
+            s_tile(Ks + buf * kKTile, qf, s, r, hh);
+            softmax_tile<false>(s, m, l, o, pb, 1.f);
+            pv_tile(Vt + buf * kVTile, pb, o, r, hh);
             advance(t);
         }
     }
@@ -408,35 +428,15 @@ void bsa_attn_kernel(AttnParams p) {
         }
         f32x16 oc[2];  // compressed-branch output of block n0 / bs for head j (same for all rows)
         if constexpr (kCmp) {
-            const int tq = n0 / p.bs;
-            const int64_t row0 = ((int64_t)b * p.nsplit * p.nb + tq) * p.Hq + j;
-            const int64_t split_stride = (int64_t)p.nb * p.Hq;
-            float M = -INFINITY;
-            for (int sp = 0; sp < p.nsplit; ++sp) M = fmaxf(M, p.ml[row0 + sp * split_stride].x);
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) oc[dt][e] = 0.f;
-            float Lsum = 0.f;
-            for (int sp = 0; sp < p.nsplit; ++sp) {
-                const float2 mlv = p.ml[row0 + sp * split_stride];
-                const float a = __builtin_amdgcn_exp2f(mlv.x - M);
-                Lsum += a * mlv.y;
-                const float* op = p.opart + (row0 + sp * split_stride) * kHeadDim;
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-                    for (int g4 = 0; g4 < 4; ++g4) {
-                        const float4 v4 = *reinterpret_cast<const float4*>(op + 32 * dt + 8 * g4 + 4 * hh);
-                        oc[dt][4 * g4 + 0] += a * v4.x;
-                        oc[dt][4 * g4 + 1] += a * v4.y;
-                        oc[dt][4 * g4 + 2] += a * v4.z;
-                        oc[dt][4 * g4 + 3] += a * v4.w;
-                    }
-            }
-            const float linv = 1.f / Lsum;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) oc[dt] *= linv;
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    oc[dt][4 * g4 + 0] = bf_lo(ocw[dt][g4].x);
+                    oc[dt][4 * g4 + 1] = bf_hi(ocw[dt][g4].x);
+                    oc[dt][4 * g4 + 2] = bf_lo(ocw[dt][g4].y);
+                    oc[dt][4 * g4 + 3] = bf_hi(ocw[dt][g4].y);
+                }
         }
         const bf16_t* pp = Part + wave * 64 * PS;
 #pragma unroll

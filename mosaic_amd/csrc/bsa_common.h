@@ -85,11 +85,23 @@ struct CmpParams {
     float scale_log2;                              // softmax_scale * log2(e)
 };
 
+// Combination of the compressed-attention split partials into the final compressed-branch
+// output of one (batch, block) for all query heads (done by the top-k kernel, or by a
+// combine-only kernel when there is no selection).
+struct CombineParams {
+    const float* opart;  // [B, U, nb, Hq, 64] unnormalised O per split
+    const float2* ml;    // [B, U, nb, Hq] (max, sum) per split, log2 units
+    bf16_t* ocmp;        // [B, nb, Hq, 64] compressed-branch output
+    int nsplit, Hq;
+};
+
 struct TopkParams {
     const bf16_t* sbar;  // [B, Hk, nb, nb_pad]
     int32_t* idx32;      // optional [B, nb, Hk, K]
     int64_t* idx64;      // optional [B, nb, Hk, K]
     int B, nb, nb_pad, Hk, K, rows;
+    int G;               // query heads per kv head (heads g*Hk + h of row h are combined)
+    CombineParams cmb;   // cmb.ocmp == nullptr: no compressed-branch combine
 };
 
 enum AttnMode : int {
@@ -108,10 +120,9 @@ struct AttnParams {
     bf16_t* out;             // [B, N, Hq, 64]
     float* lse;              // [B, N, Hq] (selected-only mode, optional)
     const void* idx;         // [B, nb, Hk, K] int32 or int64
-    const float* opart;      // compressed partials [B, U, nb, Hq, 64]
-    const float2* ml;        // [B, U, nb, Hq]
+    const bf16_t* ocmp;      // compressed-branch output [B, nb, Hq, 64]
     int B, N, Hq, Hk, G;
-    int bs_l, bs, K, nb, nsplit;
+    int bs_l, bs, K, nb;
     int head_groups;         // G / waves-per-workgroup
     int qtiles;              // N / 64
     int total_wgs;
@@ -123,6 +134,50 @@ struct AttnParams {
 hipError_t launch_pool(const PoolParams& p, hipStream_t s);
 hipError_t launch_cmp(const CmpParams& p, bool scores, bool attn, hipStream_t s);
 hipError_t launch_topk(const TopkParams& p, hipStream_t s);
+hipError_t launch_combine(const CombineParams& c, int B, int nb, hipStream_t s);
 hipError_t launch_attn(const AttnParams& p, int mode, bool idx64, int waves, hipStream_t s);
+
+// Maximum number of selected blocks per query block (block indices are staged in LDS).
+constexpr int kMaxSelected = 1024;
+
+// The compressed-branch output at block t of NH heads j0, j0 + jstep, ..., combined over the
+// splits: lane owns dimension d = lane.  exp2 weights are relative to the largest split max.
+// All loads of all heads and splits are issued before any arithmetic (one memory round trip).
+constexpr int kMaxSplitsCombine = 8;
+template <int NH>
+__device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int nb, int t, int j0, int jstep, int lane) {
+    const int64_t stride = (int64_t)nb * c.Hq;
+    float2 mlv[NH][kMaxSplitsCombine];
+    float ov[NH][kMaxSplitsCombine];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        const int64_t row0 = ((int64_t)b * c.nsplit * nb + t) * c.Hq + j0 + h * jstep;
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplitsCombine; ++sp) {
+            if (sp < c.nsplit) {
+                mlv[h][sp] = c.ml[row0 + sp * stride];
+                ov[h][sp] = c.opart[(row0 + sp * stride) * kHeadDim + lane];
+            }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplitsCombine; ++sp)
+            if (sp < c.nsplit) M = fmaxf(M, mlv[h][sp].x);
+        float L = 0.f, acc = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < kMaxSplitsCombine; ++sp) {
+            if (sp < c.nsplit) {
+                const float a = __builtin_amdgcn_exp2f(mlv[h][sp].x - M);
+                L += a * mlv[h][sp].y;
+                acc += a * ov[h][sp];
+            }
+        }
+        const int j = j0 + h * jstep;
+        c.ocmp[(((int64_t)b * nb + t) * c.Hq + j) * kHeadDim + lane] = (bf16_t)(pack_bf16x2(acc / L, 0.f) & 0xffffu);
+    }
+}
 
 }  // namespace mosaic
