@@ -64,6 +64,25 @@ def byte_counts(wl):
     return {"pool": pool, "selected_gather": gather, "op_io": io}
 
 
+def profiled_traffic(workload_name):
+    """HBM-side bytes per attention launch from the committed rocprofv3 counter summary.
+
+    The two counter passes (FETCH_SIZE, WRITE_SIZE), scaled by a copy kernel of known size,
+    cannot run inside this process; their result is read from profiles/ when the summary
+    covers this workload, else None.
+    """
+    path = os.path.join(ROOT, "profiles", "bsa_attn_nside64_hbm_traffic.md")
+    key = f"traffic_bytes_per_launch bsa_attn_kernel {workload_name}:"
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(key):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(wl, q, k, v, w):
     """The CPU oracle (torch restatement of the reference path) on the full workload."""
     from oracle import bsa_oracle as O
@@ -217,7 +236,8 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(wl.name),
+            "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)",
             "flops_per_launch": fl["attn"],
         },
         "unet_24_member_step_ms": None,
