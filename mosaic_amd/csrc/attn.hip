@@ -2,7 +2,7 @@
 //
 // One workgroup = (batch b, kv head c, 64-token query tile, group of NW query heads).
 // Each wave owns one query head j of the GQA group and all 64 query rows of the tile; the
-// K/V tiles of 64 keys are loaded once into LDS and read by all NW waves.
+// K/V tiles of 64 keys are staged once in LDS and read by all NW waves.
 //
 //   local branch     block_attention / flash_attn_func (primitives.py:28-32): the keys of
 //                    the query's block_attn_size block, logits q.k * scale, fp32 online
@@ -12,86 +12,71 @@
 //                    top-k indices in order (:94-95), base-2 online softmax (:120-128),
 //                    P -> bf16 before PV (:128), O / l and LSE = m + log2(l) (:130-131).
 //   merge            primitives.py:62-89 in fp32 in the epilogue; the compressed branch is
-//                    read from the split partial results of the compressed-attention kernel.
+//                    read from the combined compressed-attention output (one row per block).
 //
-// Tiles of both branches form one sequence [local tiles..., selected tiles...] streamed
-// through a double-buffered LDS ring with one barrier per tile: tile t+1 is written to the
-// other buffer after tile t's compute, from registers loaded one tile earlier.
+// Staging.  Tiles of both branches form one sequence [local tiles..., selected tiles...]
+// streamed through two LDS buffers with one barrier per tile.  K and V rows go from global
+// memory straight into LDS (global_load_lds_dwordx4: lane L of an instruction lands at
+// byte 16*L of a 1 KB run), issued for tile t+1 right after the barrier of tile t, so no
+// registers hold staged data.  Both keep 128-byte rows with the 16-byte chunks of a row
+// permuted (XOR swizzle, chosen per tensor for its read pattern):
+//   K  chunk c of key k at position c ^ (k & 7): the 8 lanes of a b128 read that fetch
+//      chunk c of 8 consecutive keys hit 8 different positions;
+//   V  chunk c of key k at position c ^ 2(k & 3): the 16 lanes of a transposing read that
+//      fetch 2 chunks of 4 consecutive keys hit 8 different positions.
+// The PV operand needs V^T (8 consecutive keys of one dimension per lane); it is read from
+// the row-major tile with ds_read_b64_tr_b16, which hands lane 4a+b of each 16-lane group
+// element b of the 8-byte rows addressed by lanes a, a+4, a+8, a+12.
 //
-// The softmax rescale is lazy: a row's reference max only moves when a tile's max exceeds
-// it by more than kTau (log2 units), so P = exp2(s - m) <= 2^kTau and, after the first tile,
-// the O accumulators are touched by MFMA only.  The result is the same softmax: numerator
-// and denominator share the reference max.  Row sums are taken from the bf16-rounded P with
-// v_dot2c_f32_bf16, i.e. from the same values that enter the PV product.
+// Softmax.  Local tiles: exact row max per tile with a lazy reference (a row's reference
+// only moves when a tile's max exceeds it by more than kTau).  Selected tiles: the first
+// tile's row max, rounded to bf16, is the reference m; later tiles get -m as one extra
+// contraction step of the QK^T MFMA (A = ones, B = -m), so P = exp2(S - m) is taken without
+// a max pass, and a tile whose row sums exceed kSumLimit (or are not finite) is recomputed
+// from LDS with the reference moved up to its row max.  Numerator and denominator share the
+// reference, so the result is the same softmax.  Row sums are taken from the bf16-rounded P
+// with v_dot2c_f32_bf16, i.e. from the values that enter the PV product.
 //
 // Two workgroups share a CU (2 waves per SIMD): one wave's softmax VALU work overlaps the
 // other's MFMA work.  The local branch's partial merge (w0 * o_ba) waits in LDS as bf16.
 //
 // S^T = K Q^T and O^T = V^T P^T are computed so a lane owns one query column (see
-// bsa_common.h).  K is kept row-major in LDS (A operand rows = keys); V is transposed while
-// being written to LDS so the PV A operand reads 8-byte runs of consecutive keys.
+// bsa_common.h).
+#include <type_traits>
+
 #include "bsa_common.h"
 
 namespace mosaic {
 namespace {
 
-constexpr int KS = 72;  // K tile row stride in bf16 (144 B): 16-lane b128 reads hit distinct banks
-constexpr int VS = 68;  // V^T tile row stride in bf16 (136 B): 32-lane b64 reads hit distinct banks
-constexpr int PS = 68;  // merge-partial row stride in bf16
-constexpr int kKTile = 64 * KS;
-constexpr int kVTile = 64 * VS;
+constexpr int kTileElems = 64 * 64;  // one K or V tile: 64 keys x 64 dims, 128-byte rows
+constexpr int PS = 68;               // merge-partial row stride in bf16
 constexpr float kTau = 8.0f;
+// Largest accepted partial row sum of a selected tile under the reference max: every P is
+// then <= 2^16, far from fp32 / bf16 overflow.
+constexpr float kSumLimit = 65536.0f;
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Issue the direct-to-LDS loads of one 64-key tile (K and V rows key0 .. key0+63): NW waves,
+// 8/NW 1 KB runs per wave and tensor.  wave_u is the wave index as a wave-uniform value.
 template <int NW>
-struct TileLoader {
-    static constexpr int NT = NW * 64;
-    static constexpr int KCH = 512 / NT;               // 16-byte K chunks per thread
-    static constexpr int VCH = (256 + NT - 1) / NT;    // (key pair, 8 dims) V chunks per thread
-    uint4 kr[KCH];
-    uint4 v0[VCH], v1[VCH];
-
-    __device__ __forceinline__ void load(const bf16_t* kb, const bf16_t* vb, int64_t ksn, int64_t vsn, int key0,
-                                         int tid) {
+__device__ __forceinline__ void issue_tile(const bf16_t* kb, const bf16_t* vb, int64_t ksn, int64_t vsn, int key0,
+                                           bf16_t* Kd, bf16_t* Vd, int wave_u, int lane) {
+    constexpr int PER = 8 / NW;
 #pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = tid + i * NT, row = c >> 3, ch = c & 7;
-            kr[i] = ld16(kb + (int64_t)(key0 + row) * ksn + ch * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-            const int c = tid + i * NT;
-            if (VCH * NT == 256 || c < 256) {
-                const int pr = c & 31, ch = c >> 5;
-                const bf16_t* src = vb + (int64_t)(key0 + 2 * pr) * vsn + ch * 8;
-                v0[i] = ld16(src);
-                v1[i] = ld16(src + vsn);
-            }
-        }
+    for (int i = 0; i < PER; ++i) {
+        const int row0 = 8 * (wave_u * PER + i);
+        const int row = row0 + (lane >> 3), pos = lane & 7;
+        const int ck = pos ^ (row & 7);          // global chunk stored at position pos
+        const int cv = pos ^ ((row & 3) << 1);
+        __builtin_amdgcn_global_load_lds(kb + (int64_t)(key0 + row) * ksn + 8 * ck, (lds_void*)(Kd + row0 * 64), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vb + (int64_t)(key0 + row) * vsn + 8 * cv, (lds_void*)(Vd + row0 * 64), 16, 0, 0);
     }
-
-    __device__ __forceinline__ void store(bf16_t* Ks, bf16_t* Vt, int tid) const {
-#pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = tid + i * NT, row = c >> 3, ch = c & 7;
-            *reinterpret_cast<uint4*>(Ks + row * KS + ch * 8) = kr[i];
-        }
-#pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-            const int c = tid + i * NT;
-            if (VCH * NT == 256 || c < 256) {
-                const int pr = c & 31, ch = c >> 5;
-                const uint32_t a[4] = {v0[i].x, v0[i].y, v0[i].z, v0[i].w};
-                const uint32_t b[4] = {v1[i].x, v1[i].y, v1[i].z, v1[i].w};
-                bf16_t* dst = Vt + (ch * 8) * VS + 2 * pr;
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    *reinterpret_cast<uint32_t*>(dst + (2 * m) * VS) = (a[m] & 0xffffu) | (b[m] << 16);
-                    *reinterpret_cast<uint32_t*>(dst + (2 * m + 1) * VS) = (a[m] >> 16) | (b[m] & 0xffff0000u);
-                }
-            }
-        }
-    }
-};
+}
 
 __device__ __forceinline__ void zero(f32x16 (&x)[2][2]) {
 #pragma unroll
@@ -102,71 +87,106 @@ __device__ __forceinline__ void zero(f32x16 (&x)[2][2]) {
             for (int e = 0; e < 16; ++e) x[a][b][e] = 0.f;
 }
 
-// S^T = K Q^T for one 64-key tile: s[key tile][query tile]
-__device__ __forceinline__ void s_tile(const bf16_t* Ks, const bf16x8 (&qf)[2][4], f32x16 (&s)[2][2], int r, int hh) {
-    zero(s);
+// Per-lane element offsets of the operand reads (constant over tiles).
+struct ReadOffsets {
+    int k[4];  // K row r, chunk 2*ds + hh (swizzled), for ds = 0..3; + 32*kt*64 per key tile
+    int v[2];  // V transposing read for dim tile dt; + (32*kt + 16*s2 + 8*sec)*64
+    __device__ __forceinline__ void init(int lane) {
+        const int r = lane & 31, hh = lane >> 5;
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds) k[ds] = r * 64 + 8 * ((2 * ds + hh) ^ (r & 7));
+        const int s = lane & 15, half = (lane >> 4) & 1;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+            v[dt] = (4 * hh + (s >> 2)) * 64 + 8 * ((4 * dt + 2 * half + ((s & 3) >> 1)) ^ (2 * (s >> 2))) + 4 * (s & 1);
+    }
+};
+
+// S^T = K Q^T for one 64-key tile: s[key tile][query tile].  With BIAS the per-query
+// reference m (bf16-representable) enters as one extra contraction step (A = ones at
+// contraction element (hh=0, i=0), B = -m at the same element), so s = S^T - m.
+template <bool BIAS>
+__device__ __forceinline__ void s_tile(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[2][4],
+                                       const float (&m)[2], f32x16 (&s)[2][2], int hh) {
+    if constexpr (BIAS) {
+        f32x16 z;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) z[e] = 0.f;
+        const bf16x8 kbias = as_bf16x8(make_uint4(hh == 0 ? 0x3f80u : 0u, 0u, 0u, 0u));
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const bf16x8 qbias = as_bf16x8(make_uint4(hh == 0 ? pack_bf16x2(-m[qt], 0.f) : 0u, 0u, 0u, 0u));
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) s[kt][qt] = mfma32(kbias, qbias, z);
+        }
+    } else {
+        zero(s);
+    }
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(Ks + (32 * kt + r) * KS + 16 * ds + 8 * hh));
+            const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(Ks + 32 * kt * 64 + ro.k[ds]));
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) s[kt][qt] = mfma32(a, qf[qt][ds], s[kt][qt]);
         }
     }
 }
 
-// O^T += V^T P^T for one 64-key tile
-__device__ __forceinline__ void pv_tile(const bf16_t* Vt, const bf16x8 (&pb)[2][2][2], f32x16 (&o)[2][2], int r,
-                                        int hh) {
+// One query tile of s_tile<BIAS> (rare recompute path), as s[key tile].
+template <bool BIAS>
+__device__ __forceinline__ void s_half(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[4], float m,
+                                       f32x16 (&s)[2], int hh) {
+    f32x16 z;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) z[e] = 0.f;
+    if constexpr (BIAS) {
+        const bf16x8 kbias = as_bf16x8(make_uint4(hh == 0 ? 0x3f80u : 0u, 0u, 0u, 0u));
+        const bf16x8 qbias = as_bf16x8(make_uint4(hh == 0 ? pack_bf16x2(-m, 0.f) : 0u, 0u, 0u, 0u));
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s[kt] = mfma32(kbias, qbias, z);
+    } else {
+        s[0] = s[1] = z;
+    }
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+            s[kt] = mfma32(as_bf16x8(*reinterpret_cast<const uint4*>(Ks + 32 * kt * 64 + ro.k[ds])), qf[ds], s[kt]);
+}
+
+// O^T += V^T P^T for one 64-key tile; V^T operands come from transposing reads of the
+// row-major tile (keys 4hh + 0..3 and 8 + 4hh + 0..3 of each 16-key step, matching the
+// packing of P in exp_pack).
+__device__ __forceinline__ void pv_tile(const bf16_t* Vs, const ReadOffsets& ro, const bf16x8 (&pb)[2][2][2],
+                                        f32x16 (&o)[2][2]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
-                const bf16_t* vp = Vt + (32 * dt + r) * VS + 32 * kt + 16 * s2 + 4 * hh;
-                const uint2 lo = ld8(vp), hi = ld8(vp + 8);
+                const bf16_t* vp = Vs + (32 * kt + 16 * s2) * 64 + ro.v[dt];
+                const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                               (__attribute__((address_space(3))) v4i16*)(vp)));
+                const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                               (__attribute__((address_space(3))) v4i16*)(vp + 8 * 64)));
                 const bf16x8 a = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) o[dt][qt] = mfma32(a, pb[qt][kt][s2], o[dt][qt]);
             }
 }
 
-// Online softmax of one tile with lazy rescaling.  Logits are s * c when SCALED, else s.
-// m: reference max per query tile (log2 units); l: this lane's partial denominators.
-template <bool SCALED>
-__device__ __forceinline__ void softmax_tile(f32x16 (&s)[2][2], float (&m)[2], float (&l)[2], f32x16 (&o)[2][2],
-                                             bf16x8 (&pb)[2][2][2], float c) {
-    float mt[2];
-    bool need = false;
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-        float mx = s[0][qt][0];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][qt][e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        mt[qt] = SCALED ? mx * c : mx;
-        need |= mt[qt] > m[qt] + kTau;
-    }
-    if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform; rare after a row's first tile
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            const float mnew = mt[qt] > m[qt] + kTau ? mt[qt] : m[qt];
-            const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);  // 0 on a row's first tile
-            l[qt] *= alpha;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) o[dt][qt] *= alpha;
-            m[qt] = mnew;
-        }
-    }
+// P = exp2(s * c - m[qt]) (SCALED), exp2(s - m[qt]) (SHIFT) or exp2(s), packed to bf16 for
+// the PV product; lt = this lane's partial row sums of the rounded P.
+template <bool SCALED, bool SHIFT>
+__device__ __forceinline__ void exp_pack(const f32x16 (&s)[2][2], const float (&m)[2], float c, bf16x8 (&pb)[2][2][2],
+                                         float (&lt)[2]) {
     const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-        const float mm = m[qt];
         float lsum[2] = {0.f, 0.f};
+        const float mm = m[qt];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -175,23 +195,60 @@ __device__ __forceinline__ void softmax_tile(f32x16 (&s)[2][2], float (&m)[2], f
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float x0 = s[kt][qt][8 * s2 + 2 * i], x1 = s[kt][qt][8 * s2 + 2 * i + 1];
-                    const float p0 = __builtin_amdgcn_exp2f(SCALED ? fmaf(x0, c, -mm) : x0 - mm);
-                    const float p1 = __builtin_amdgcn_exp2f(SCALED ? fmaf(x1, c, -mm) : x1 - mm);
-                    w[i] = pack_bf16x2(p0, p1);
+                    const float a0 = SCALED ? fmaf(x0, c, -mm) : (SHIFT ? x0 - mm : x0);
+                    const float a1 = SCALED ? fmaf(x1, c, -mm) : (SHIFT ? x1 - mm : x1);
+                    w[i] = pack_bf16x2(__builtin_amdgcn_exp2f(a0), __builtin_amdgcn_exp2f(a1));
                     lsum[kt] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), ones, lsum[kt], false);
                 }
                 pb[qt][kt][s2] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
             }
-        l[qt] += lsum[0] + lsum[1];
+        lt[qt] = lsum[0] + lsum[1];
     }
+}
+
+// exp_pack<false, true> of one query tile
+__device__ __forceinline__ void exp_pack_half(const f32x16 (&s)[2], float m, bf16x8 (&pb)[2][2], float& lt) {
+    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
+    float lsum[2] = {0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                w[i] = pack_bf16x2(__builtin_amdgcn_exp2f(s[kt][8 * s2 + 2 * i] - m),
+                                   __builtin_amdgcn_exp2f(s[kt][8 * s2 + 2 * i + 1] - m));
+                lsum[kt] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), ones, lsum[kt], false);
+            }
+            pb[kt][s2] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
+        }
+    lt = lsum[0] + lsum[1];
+}
+
+// Row max of a tile (both lane halves) for query tile qt.
+__device__ __forceinline__ float tile_max(const f32x16 (&s)[2][2], int qt) {
+    float mx = s[0][qt][0];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][qt][e]);
+    return fmaxf(mx, __shfl_xor(mx, 32));
+}
+
+__device__ __forceinline__ float half_max(const f32x16 (&s)[2]) {
+    float mx = s[0][0];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
+    return fmaxf(mx, __shfl_xor(mx, 32));
 }
 
 __device__ __forceinline__ float load_bf16(const bf16_t* p) { return bf2f(*p); }
 
-template <int MODE>
-struct AttnLds {
-    static constexpr bool kPartial = MODE == kModeFull || MODE == kModeNoCompression;
-};
+using Buf0 = std::integral_constant<int, 0>;
+using Buf1 = std::integral_constant<int, 1>;
 
 template <int NW, int MODE, typename IdxT>
 __global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(2, 2)))
@@ -200,15 +257,20 @@ void bsa_attn_kernel(AttnParams p) {
     constexpr bool kSel = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeSelectedOnly;
     constexpr bool kCmp = MODE == kModeFull || MODE == kModeNoSelection;
     constexpr bool kWeights = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeNoSelection;
-    constexpr bool kPartial = AttnLds<MODE>::kPartial;
+    constexpr bool kPartial = MODE == kModeFull || MODE == kModeNoCompression;
 
-    __shared__ __attribute__((aligned(16))) bf16_t Ks[2 * kKTile];
-    __shared__ __attribute__((aligned(16))) bf16_t Vt[2 * kVTile];
+    // two staging buffers as separate objects, so the compiler can tell the loads in flight
+    // into one buffer from the reads of the other
+    __shared__ __attribute__((aligned(1024))) bf16_t Ks0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t Ks1[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t Vs0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t Vs1[kTileElems];
     __shared__ __attribute__((aligned(16))) bf16_t Part[kPartial ? NW * 64 * PS : 8];
     __shared__ int sel_key0[kSel ? kMaxSelected : 1];  // first key of each in-range selected block
     __shared__ int sel_count;
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r = lane & 31, hh = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int L = xcd_remap(blockIdx.x, p.total_wgs);
     const int qtile = L % p.qtiles;
     const int rest = L / p.qtiles;
@@ -227,11 +289,11 @@ void bsa_attn_kernel(AttnParams p) {
     const int tl_count = kLocal ? p.bs_l / kTile : 0;
     const int lstart = (n0 / p.bs_l) * p.bs_l;
     const int sub = p.bs / kTile;
-    const IdxT* ip = reinterpret_cast<const IdxT*>(p.idx) + ((int64_t)(b * p.nb + n0 / p.bs) * p.Hk + c) * p.K;
     // Selected blocks: wave 0 compacts the in-range indices (top-k order kept) into LDS once,
-    // so the tile loop reads block offsets from LDS instead of waiting on a global load.
+    // so tile addresses never wait on a global load inside the loop.
     if constexpr (kSel) {
         if (wave == 0) {
+            const IdxT* ip = reinterpret_cast<const IdxT*>(p.idx) + ((int64_t)(b * p.nb + n0 / p.bs) * p.Hk + c) * p.K;
             int count = 0;
             for (int base = 0; base < p.K; base += 64) {
                 const int i = base + lane;
@@ -248,7 +310,7 @@ void bsa_attn_kernel(AttnParams p) {
     }
     const int nvalid = kSel ? sel_count : 0;
     const int total_tiles = tl_count + nvalid * sub;
-    // The loader asks for tiles in order 0, 1, 2, ...
+    // first key of tile t; tiles are requested in order 0, 1, 2, ...
     int cur_k = 0, cur_s = 0;
     auto next_key0 = [&](int t) -> int {
         if (kLocal && t < tl_count) return lstart + kTile * t;
@@ -260,6 +322,11 @@ void bsa_attn_kernel(AttnParams p) {
         return key0;
     };
 
+    ReadOffsets ro;
+    ro.init(lane);
+
+    if (total_tiles > 0) issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, next_key0(0), Ks0, Vs0, wave, lane);
+
     bf16x8 qf[2][4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt)
@@ -267,48 +334,62 @@ void bsa_attn_kernel(AttnParams p) {
         for (int ds = 0; ds < 4; ++ds)
             qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
 
-    // compressed-branch output of this block and head (bf16), consumed in the epilogue
-    uint2 ocw[2][4];
-    if constexpr (kCmp) {
-        const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim + 4 * hh;
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) ocw[dt][g4] = ld8(ocp + 32 * dt + 8 * g4);
-    }
-
-    TileLoader<NW> tl;
-    if (total_tiles > 0) {
-        tl.load(kb, vb, p.k_sn, p.v_sn, next_key0(0), tid);
-        tl.store(Ks, Vt, tid);
-        if (total_tiles > 1) tl.load(kb, vb, p.k_sn, p.v_sn, next_key0(1), tid);
-    }
-
     f32x16 o[2][2], s[2][2];
     bf16x8 pb[2][2][2];
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
     zero(o);
 
-    auto advance = [&](int t) {
-        // after tile t's compute: publish tile t+1 into the other buffer, prefetch tile t+2
-        if (t + 1 < total_tiles) {
-            tl.store(Ks + ((t + 1) & 1) * kKTile, Vt + ((t + 1) & 1) * kVTile, tid);
-            if (t + 2 < total_tiles) tl.load(kb, vb, p.k_sn, p.v_sn, next_key0(t + 2), tid);
-        }
+    // Start of tile t in buffer BUF: wait for this wave's loads of tile t, then the barrier
+    // makes every wave's loads visible and guarantees the other buffer (tile t-1) is no
+    // longer read; the loads of tile t+1 go there.
+    auto begin_tile = [&](auto bufc, int t) {
+        constexpr int BUF = decltype(bufc)::value;
+        wait_vmem();
+        __syncthreads();
+        if (t + 1 < total_tiles)
+            issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, next_key0(t + 1), BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, wave, lane);
     };
 
     bf16_t* outp = p.out + ((int64_t)b * p.N + n0) * p.Hq * kHeadDim + (int64_t)j * kHeadDim;
 
     // ------------------------------------------------------------------ local branch
     if constexpr (kLocal) {
-        for (int t = 0; t < tl_count; ++t) {
-            __syncthreads();
-            const int buf = t & 1;
-            s_tile(Ks + buf * kKTile, qf, s, r, hh);
-            softmax_tile<true>(s, m, l, o, pb, p.scale_log2);
-            pv_tile(Vt + buf * kVTile, pb, o, r, hh);
-            advance(t);
+        auto local_step = [&](auto bufc, int t) {
+            constexpr int BUF = decltype(bufc)::value;
+            const bf16_t* Kc = BUF ? Ks1 : Ks0;
+            const bf16_t* Vc = BUF ? Vs1 : Vs0;
+            begin_tile(bufc, t);
+            s_tile<false>(Kc, ro, qf, m, s, hh);
+            float mt[2];
+            bool need = false;
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                mt[qt] = tile_max(s, qt) * p.scale_log2;
+                need |= mt[qt] > m[qt] + kTau;
+            }
+            if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform; rare after a row's first tile
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    const float mnew = mt[qt] > m[qt] + kTau ? mt[qt] : m[qt];
+                    const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);  // 0 on a row's first tile
+                    l[qt] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < 2; ++dt) o[dt][qt] *= alpha;
+                    m[qt] = mnew;
+                }
+            }
+            float lt[2];
+            exp_pack<true, true>(s, m, p.scale_log2, pb, lt);
+            l[0] += lt[0];
+            l[1] += lt[1];
+            pv_tile(Vc, ro, pb, o);
+        };
+        int t = 0;
+        for (; t + 1 < tl_count; t += 2) {
+            local_step(Buf0{}, t);
+            local_step(Buf1{}, t + 1);
         }
+        if (t < tl_count) local_step(Buf0{}, t);
         float inv[2];
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) inv[qt] = 1.f / (l[qt] + __shfl_xor(l[qt], 32));
@@ -375,16 +456,68 @@ void bsa_attn_kernel(AttnParams p) {
                 qf[qt][ds] = as_bf16x8(make_uint4(o4[0], o4[1], o4[2], o4[3]));
             }
         zero(o);
-        m[0] = m[1] = -INFINITY;
         l[0] = l[1] = 0.f;
-        for (int t = tl_count; t < total_tiles; ++t) {
-            __syncthreads();
-            const int buf = t & 1;
-            s_tile(Ks + buf * kKTile, qf, s, r, hh);
-            softmax_tile<false>(s, m, l, o, pb, 1.f);
-            pv_tile(Vt + buf * kVTile, pb, o, r, hh);
-            advance(t);
+
+        // first selected tile: exact row max, rounded to bf16, becomes the reference
+        auto first_step = [&](auto bufc, int t) {
+            constexpr int BUF = decltype(bufc)::value;
+            const bf16_t* Kc = BUF ? Ks1 : Ks0;
+            const bf16_t* Vc = BUF ? Vs1 : Vs0;
+            begin_tile(bufc, t);
+            s_tile<false>(Kc, ro, qf, m, s, hh);
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) m[qt] = round_bf16(tile_max(s, qt));
+            float lt[2];
+            exp_pack<false, true>(s, m, 1.f, pb, lt);
+            l[0] += lt[0];
+            l[1] += lt[1];
+            pv_tile(Vc, ro, pb, o);
+        };
+        auto sel_step = [&](auto bufc, int t) {
+            constexpr int BUF = decltype(bufc)::value;
+            const bf16_t* Kc = BUF ? Ks1 : Ks0;
+            const bf16_t* Vc = BUF ? Vs1 : Vs0;
+            begin_tile(bufc, t);
+            s_tile<true>(Kc, ro, qf, m, s, hh);
+            float lt[2];
+            exp_pack<false, false>(s, m, 1.f, pb, lt);
+            if (__builtin_amdgcn_ballot_w64(!(lt[0] <= kSumLimit && lt[1] <= kSumLimit))) {
+                // rare: recompute one query tile at a time with the reference moved up to
+                // the tile's row max (K of this tile stays in LDS until the next barrier)
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    f32x16 sh[2];
+                    s_half<true>(Kc, ro, qf[qt], m[qt], sh, hh);
+                    const float mx = half_max(sh);
+                    const float mnew = mx > 0.f ? round_bf16(m[qt] + mx) : m[qt];
+                    const float dl = mnew - m[qt];
+                    const float alpha = __builtin_amdgcn_exp2f(-dl);
+                    l[qt] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < 2; ++dt) o[dt][qt] *= alpha;
+                    m[qt] = mnew;
+                    exp_pack_half(sh, dl, pb[qt], lt[qt]);
+                }
+            }
+            l[0] += lt[0];
+            l[1] += lt[1];
+            pv_tile(Vc, ro, pb, o);
+        };
+        int t = tl_count;
+        if (t < total_tiles) {
+            if (t & 1) first_step(Buf1{}, t);
+            else first_step(Buf0{}, t);
+            ++t;
         }
+        if ((t & 1) && t < total_tiles) {
+            sel_step(Buf1{}, t);
+            ++t;
+        }
+        for (; t + 1 < total_tiles; t += 2) {
+            sel_step(Buf0{}, t);
+            sel_step(Buf1{}, t + 1);
+        }
+        if (t < total_tiles) sel_step(Buf0{}, t);
     }
 
     // ------------------------------------------------------------------ epilogue
@@ -428,6 +561,12 @@ void bsa_attn_kernel(AttnParams p) {
         }
         f32x16 oc[2];  // compressed-branch output of block n0 / bs for head j (same for all rows)
         if constexpr (kCmp) {
+            uint2 ocw[2][4];
+            const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim + 4 * hh;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) ocw[dt][g4] = ld8(ocp + 32 * dt + 8 * g4);
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
