@@ -20,8 +20,9 @@
 // byte 16*L of a 1 KB run), issued for tile t+1 right after the barrier of tile t, so no
 // registers hold staged data.  Both keep 128-byte rows with the 16-byte chunks of a row
 // permuted (XOR swizzle, chosen per tensor for its read pattern):
-//   K  chunk c of key k at position c ^ (k & 7): the 8 lanes of a b128 read that fetch
-//      chunk c of 8 consecutive keys hit 8 different positions;
+//   K  chunk c of key k at position c ^ ((k >> 1) & 7): a b128 read is served 16 lanes
+//      (256 bytes, all 64 banks) at a time, and the 16 lanes that fetch chunk c of 16
+//      consecutive keys then cover both 128-byte halves of the banks at 8 positions each;
 //   V  chunk c of key k at position c ^ 2(k & 3): the 16 lanes of a transposing read that
 //      fetch 2 chunks of 4 consecutive keys hit 8 different positions.
 // The PV operand needs V^T (8 consecutive keys of one dimension per lane); it is read from
@@ -71,7 +72,7 @@ __device__ __forceinline__ void issue_tile(const bf16_t* kb, const bf16_t* vb, i
     for (int i = 0; i < PER; ++i) {
         const int row0 = 8 * (wave_u * PER + i);
         const int row = row0 + (lane >> 3), pos = lane & 7;
-        const int ck = pos ^ (row & 7);          // global chunk stored at position pos
+        const int ck = pos ^ ((row >> 1) & 7);   // global chunk stored at position pos
         const int cv = pos ^ ((row & 3) << 1);
         __builtin_amdgcn_global_load_lds(kb + (int64_t)(key0 + row) * ksn + 8 * ck, (lds_void*)(Kd + row0 * 64), 16, 0, 0);
         __builtin_amdgcn_global_load_lds(vb + (int64_t)(key0 + row) * vsn + 8 * cv, (lds_void*)(Vd + row0 * 64), 16, 0, 0);
@@ -94,7 +95,7 @@ struct ReadOffsets {
     __device__ __forceinline__ void init(int lane) {
         const int r = lane & 31, hh = lane >> 5;
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds) k[ds] = r * 64 + 8 * ((2 * ds + hh) ^ (r & 7));
+        for (int ds = 0; ds < 4; ++ds) k[ds] = r * 64 + 8 * ((2 * ds + hh) ^ ((r >> 1) & 7));
         const int s = lane & 15, half = (lane >> 4) & 1;
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
