@@ -35,8 +35,10 @@
 // contraction step of the QK^T MFMA (A = ones, B = -m), so P = exp2(S - m) is taken without
 // a max pass, and a tile whose row sums exceed kSumLimit (or are not finite) is recomputed
 // from LDS with the reference moved up to its row max.  Numerator and denominator share the
-// reference, so the result is the same softmax.  Row sums are taken from the bf16-rounded P
-// with v_dot2c_f32_bf16, i.e. from the values that enter the PV product.
+// reference, so the result is the same softmax.  Row sums add the fp32 P before its bf16
+// rounding, as the selected-branch kernel does (ops.py:125), with plain fp32 adds: on gfx950
+// v_dot2c_f32_bf16 shares the matrix pipe and stalls behind the other wave's MFMAs, while
+// fp32 VALU work overlaps them.
 //
 // Two workgroups share a CU (2 waves per SIMD): one wave's softmax VALU work overlaps the
 // other's MFMA work.  The local branch's partial merge (w0 * o_ba) waits in LDS as bf16.
@@ -179,14 +181,13 @@ __device__ __forceinline__ void pv_tile(const bf16_t* Vs, const ReadOffsets& ro,
 }
 
 // P = exp2(s * c - m[qt]) (SCALED), exp2(s - m[qt]) (SHIFT) or exp2(s), packed to bf16 for
-// the PV product; lt = this lane's partial row sums of the rounded P.
+// the PV product; lt = this lane's partial row sums of P (fp32, before rounding).
 template <bool SCALED, bool SHIFT>
 __device__ __forceinline__ void exp_pack(const f32x16 (&s)[2][2], const float (&m)[2], float c, bf16x8 (&pb)[2][2][2],
                                          float (&lt)[2]) {
-    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-        float lsum[2] = {0.f, 0.f};
+        float lsum[4] = {0.f, 0.f, 0.f, 0.f};
         const float mm = m[qt];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
@@ -198,18 +199,18 @@ __device__ __forceinline__ void exp_pack(const f32x16 (&s)[2][2], const float (&
                     const float x0 = s[kt][qt][8 * s2 + 2 * i], x1 = s[kt][qt][8 * s2 + 2 * i + 1];
                     const float a0 = SCALED ? fmaf(x0, c, -mm) : (SHIFT ? x0 - mm : x0);
                     const float a1 = SCALED ? fmaf(x1, c, -mm) : (SHIFT ? x1 - mm : x1);
-                    w[i] = pack_bf16x2(__builtin_amdgcn_exp2f(a0), __builtin_amdgcn_exp2f(a1));
-                    lsum[kt] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), ones, lsum[kt], false);
+                    const float p0 = __builtin_amdgcn_exp2f(a0), p1 = __builtin_amdgcn_exp2f(a1);
+                    w[i] = pack_bf16x2(p0, p1);
+                    lsum[2 * kt + s2] += p0 + p1;
                 }
                 pb[qt][kt][s2] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
             }
-        lt[qt] = lsum[0] + lsum[1];
+        lt[qt] = (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     }
 }
 
 // exp_pack<false, true> of one query tile
 __device__ __forceinline__ void exp_pack_half(const f32x16 (&s)[2], float m, bf16x8 (&pb)[2][2], float& lt) {
-    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3f803f80u);
     float lsum[2] = {0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -218,9 +219,10 @@ __device__ __forceinline__ void exp_pack_half(const f32x16 (&s)[2], float m, bf1
             uint32_t w[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                w[i] = pack_bf16x2(__builtin_amdgcn_exp2f(s[kt][8 * s2 + 2 * i] - m),
-                                   __builtin_amdgcn_exp2f(s[kt][8 * s2 + 2 * i + 1] - m));
-                lsum[kt] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), ones, lsum[kt], false);
+                const float p0 = __builtin_amdgcn_exp2f(s[kt][8 * s2 + 2 * i] - m);
+                const float p1 = __builtin_amdgcn_exp2f(s[kt][8 * s2 + 2 * i + 1] - m);
+                w[i] = pack_bf16x2(p0, p1);
+                lsum[kt] += p0 + p1;
             }
             pb[kt][s2] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
         }
@@ -267,6 +269,7 @@ void bsa_attn_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(1024))) bf16_t Vs0[kTileElems];
     __shared__ __attribute__((aligned(1024))) bf16_t Vs1[kTileElems];
     __shared__ __attribute__((aligned(16))) bf16_t Part[kPartial ? NW * 64 * PS : 8];
+    __shared__ __attribute__((aligned(16))) bf16_t Ocmp[kCmp ? NW * 64 : 8];  // compressed-branch rows
     __shared__ int sel_key0[kSel ? kMaxSelected : 1];  // first key of each in-range selected block
     __shared__ int sel_count;
 
@@ -290,6 +293,31 @@ void bsa_attn_kernel(AttnParams p) {
     const int tl_count = kLocal ? p.bs_l / kTile : 0;
     const int lstart = (n0 / p.bs_l) * p.bs_l;
     const int sub = p.bs / kTile;
+    // Prologue.  The Q rows, the gate weights, the compressed-branch row and (with a local
+    // branch) the first tile do not depend on the top-k indices: their loads are issued
+    // first, so they are in flight while wave 0 stages the indices.
+    bf16x8 qf[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds)
+            qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
+    // gate weights of rows n0 + 32*qt + r: branch 0 is needed when the local branch ends,
+    // branches 1 and 2 are loaded in the epilogue
+    auto gate = [&](int sidx, int qt) -> float {
+        return load_bf16(p.w + sidx * p.w_ss + b * p.w_sb + (int64_t)(n0 + 32 * qt + r) * p.w_sn + (int64_t)j * p.w_sh);
+    };
+    float w0r[2] = {0.f, 0.f};
+    if constexpr (kWeights) {
+        w0r[0] = gate(0, 0);
+        w0r[1] = gate(0, 1);
+    }
+    if constexpr (kCmp) {  // compressed-branch output row of (block, head j): 128 bytes into LDS
+        const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim;
+        if (lane < 32) __builtin_amdgcn_global_load_lds(ocp + 2 * lane, (lds_void*)(Ocmp + wave * 64), 4, 0, 0);
+    }
+    if constexpr (kLocal) issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, lstart, Ks0, Vs0, wave, lane);
+
     // Selected blocks: wave 0 compacts the in-range indices (top-k order kept) into LDS once,
     // so tile addresses never wait on a global load inside the loop.
     if constexpr (kSel) {
@@ -311,7 +339,8 @@ void bsa_attn_kernel(AttnParams p) {
     }
     const int nvalid = kSel ? sel_count : 0;
     const int total_tiles = tl_count + nvalid * sub;
-    // first key of tile t; tiles are requested in order 0, 1, 2, ...
+    // first key of tile t >= 1 (tile 0 of a local branch is issued above); tiles are
+    // requested in order
     int cur_k = 0, cur_s = 0;
     auto next_key0 = [&](int t) -> int {
         if (kLocal && t < tl_count) return lstart + kTile * t;
@@ -322,18 +351,10 @@ void bsa_attn_kernel(AttnParams p) {
         }
         return key0;
     };
+    if (!kLocal && total_tiles > 0) issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, next_key0(0), Ks0, Vs0, wave, lane);
 
     ReadOffsets ro;
     ro.init(lane);
-
-    if (total_tiles > 0) issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, next_key0(0), Ks0, Vs0, wave, lane);
-
-    bf16x8 qf[2][4];
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-        for (int ds = 0; ds < 4; ++ds)
-            qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
 
     f32x16 o[2][2], s[2][2];
     bf16x8 pb[2][2][2];
@@ -400,10 +421,7 @@ void bsa_attn_kernel(AttnParams p) {
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
                 f[qt] = inv[qt];
-                if constexpr (kWeights) {
-                    const float w0 = load_bf16(p.w + b * p.w_sb + (int64_t)(n0 + 32 * qt + r) * p.w_sn + (int64_t)j * p.w_sh);
-                    f[qt] *= w0;
-                }
+                if constexpr (kWeights) f[qt] *= w0r[qt];
             }
             if constexpr (MODE == kModeLocalOnly) {
 #pragma unroll
@@ -551,10 +569,7 @@ void bsa_attn_kernel(AttnParams p) {
         float fs[2], fc[2], nrm[2];
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            const int64_t woff = b * p.w_sb + (int64_t)(n0 + 32 * qt + r) * p.w_sn + (int64_t)j * p.w_sh;
-            const float w0 = load_bf16(p.w + woff);
-            const float w1 = load_bf16(p.w + p.w_ss + woff);
-            const float w2 = load_bf16(p.w + 2 * p.w_ss + woff);
+            const float w0 = w0r[qt], w1 = gate(1, qt), w2 = gate(2, qt);
             if constexpr (kSel) fs[qt] = w2 / (l[qt] + __shfl_xor(l[qt], 32));
             fc[qt] = w1;
             nrm[qt] = MODE == kModeNoCompression ? 1.f / (w0 + w2 + 1e-8f)
@@ -563,11 +578,12 @@ void bsa_attn_kernel(AttnParams p) {
         f32x16 oc[2];  // compressed-branch output of block n0 / bs for head j (same for all rows)
         if constexpr (kCmp) {
             uint2 ocw[2][4];
-            const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim + 4 * hh;
+            wait_vmem();  // the row was requested in the prologue; the wave reads its own bytes
+            const bf16_t* ocp = Ocmp + wave * 64 + 4 * hh;
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) ocw[dt][g4] = ld8(ocp + 32 * dt + 8 * g4);
+                for (int g4 = 0; g4 < 4; ++g4) ocw[dt][g4] = *reinterpret_cast<const uint2*>(ocp + 32 * dt + 8 * g4);
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
 #pragma unroll

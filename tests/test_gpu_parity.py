@@ -76,9 +76,10 @@ def test_sparse_attn_and_lse(B, N, Hq, Hk, bs, K):
     out, lse = M.mosaic_attn_fwd(*dev(q, k, v), idx.to(DEV), bs, 64 ** -0.5)
     ref, ref_lse = O.sparse_attn_fwd(q, k, v, idx, bs)
     close(out, ref)
-    # The kernel's denominator sums the bf16-rounded probabilities (the values that multiply
-    # V); each carries <= 2^-9 relative rounding, so |log2(l'/l)| <= 2^-9 / ln 2 = 2.8e-3.
-    assert (lse.cpu() - ref_lse).abs().max().item() < 3e-3
+    # Both sum the fp32 probabilities (ops.py:125); they differ by the fp32 accumulation order
+    # of the 64-term logits (|ds| <~ 64 * 2^-24 * |s|, about 4e-5 for |s| ~ 10) and of the row
+    # sums, so the base-2 LSE agrees to well within 2e-4.
+    assert (lse.cpu() - ref_lse).abs().max().item() < 2e-4
     # the autograd wrapper returns the same output
     out2 = M.mosaic_sparse_attn(*dev(q, k, v), idx.to(DEV), bs)
     assert torch.equal(out2.cpu(), out.cpu())
