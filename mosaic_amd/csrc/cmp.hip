@@ -9,34 +9,37 @@
 //   attention   flash_attn_func(q_cmp, k_cmp, v_cmp) (primitives.py:77): logits S*scale,
 //               online softmax in base 2 over this split's range of key blocks, P -> bf16,
 //               O^T += v_cmp^T P^T.  Each split writes its unnormalised O and (max, sum);
-//               the attention kernel combines the splits in its epilogue.
+//               the top-k kernel combines the splits.
 //
 // Grid: (query-block tiles of 32, selection row h, batch * splits).  Workgroup: G waves;
 // wave g handles query head j = g*Hk + h against kv head j / G, so the G heads averaged by
-// selection row h sit in one workgroup and are reduced through LDS.
+// selection row h sit in one workgroup and are reduced through LDS (bf16 tiles, 8-byte
+// reads and stores).
 //
-// The loop over key-block tiles is latency-bound (little arithmetic per tile), so the next
-// tile's K and V^T fragments are loaded into registers while the current one is computed,
-// and the per-head score exchange is double-buffered (one barrier per tile).
+// The loop over key-block tiles is latency-bound (little arithmetic per tile): the K and
+// V^T fragments of the next tile are loaded into registers while the current one is
+// computed (two register sets, unrolled by two).  All loads are unconditional (rows past the last block are clamped and their
+// results masked or never read), so the compiler's wait counts stay exact and a wait for
+// the prefetched fragments never waits for the score stores issued after them.
 #include "bsa_common.h"
 
 namespace mosaic {
 namespace {
 
-constexpr int XS = 36;  // row stride (floats) of the per-head score exchange buffer
+constexpr int XSB = 40;  // row stride (bf16) of the per-head score exchange tile [32 t][32 u]
+constexpr float kTau = 8.0f;
 
 struct CmpFrags {
-    uint4 k[4];      // A operand of S^T = K Q^T: k_cmp[u0 + r][16*ds + 8*hh ..]
+    uint4 k[4];        // A operand of S^T = K Q^T: k_cmp[u0 + r][16*ds + 8*hh ..]
     uint2 v[2][2][2];  // A operand of O^T += V^T P^T: [dt][s2][lo/hi]
 };
 
 template <bool ATTN>
 __device__ __forceinline__ void load_frags(CmpFrags& f, const CmpParams& p, const bf16_t* kp0, const bf16_t* vtp,
                                            int u0, int r, int hh) {
-    const bool uvalid = u0 + r < p.nb;
+    const int urow = min(u0 + r, p.nb - 1);  // rows past the last block: clamped, masked later
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds)
-        f.k[ds] = uvalid ? ld16(kp0 + (int64_t)(u0 + r) * p.k_sn + 16 * ds) : make_uint4(0, 0, 0, 0);
+    for (int ds = 0; ds < 4; ++ds) f.k[ds] = ld16(kp0 + (int64_t)urow * p.k_sn + 16 * ds);
     if constexpr (ATTN) {
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
@@ -49,28 +52,85 @@ __device__ __forceinline__ void load_frags(CmpFrags& f, const CmpParams& p, cons
     }
 }
 
-template <bool SCORES, bool ATTN, int MAXT>
-__global__ __launch_bounds__(MAXT) void cmp_kernel(CmpParams p) {
-    extern __shared__ float xs[];  // [2][G][32 t][XS] bf16-rounded scores per head (SCORES)
+// Mean over the G heads of one 32x32 tile of bf16 scores in LDS, rounded to bf16 and stored
+// (rows past the last block are skipped; columns up to nb_pad are written, the padding is
+// never read).  Thread tid handles 16/G consecutive columns of row (tid * 16/G) / 32.
+template <int G>
+__device__ __forceinline__ void store_mean(const bf16_t* xb, bf16_t* dst_row0, int64_t row_stride, int rows_left,
+                                           int tid, int gcount) {
+    if constexpr (G == 0) {  // head count not a power of two: one element at a time
+        for (int e = tid; e < 32 * 32; e += gcount * 64) {
+            const int t = e >> 5, u = e & 31;
+            if (t >= rows_left) break;
+            float sum = 0.f;
+            for (int gg = 0; gg < gcount; ++gg) sum += bf2f(xb[(gg * 32 + t) * XSB + u]);
+            dst_row0[t * row_stride + u] = (bf16_t)(pack_bf16x2(sum / (float)gcount, 0.f) & 0xffffu);
+        }
+        return;
+    }
+    constexpr int GG = G > 0 ? G : 1;
+    constexpr int EPT = 16 / GG;            // elements per thread
+    constexpr int CH = EPT >= 4 ? 4 : EPT;  // elements per LDS read / global store
+    const int e0 = tid * EPT, t = e0 >> 5, u = e0 & 31;
+    if (t >= rows_left) return;
+#pragma unroll
+    for (int c0 = 0; c0 < EPT; c0 += CH) {
+        float acc[CH];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) acc[i] = 0.f;
+#pragma unroll
+        for (int g = 0; g < GG; ++g) {
+            const bf16_t* src = xb + (g * 32 + t) * XSB + u + c0;
+            if constexpr (CH == 4) {
+                const uint2 w = *reinterpret_cast<const uint2*>(src);
+                acc[0] += bf_lo(w.x); acc[1] += bf_hi(w.x); acc[2] += bf_lo(w.y); acc[3] += bf_hi(w.y);
+            } else if constexpr (CH == 2) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
+                acc[0] += bf_lo(w); acc[1] += bf_hi(w);
+            } else {
+                acc[0] += bf2f(*src);
+            }
+        }
+        bf16_t* dst = dst_row0 + t * row_stride + u + c0;
+        constexpr float kInvG = 1.f / GG;  // exact: GG is a power of two
+        if constexpr (CH == 4) {
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(pack_bf16x2(acc[0] * kInvG, acc[1] * kInvG), pack_bf16x2(acc[2] * kInvG, acc[3] * kInvG));
+        } else if constexpr (CH == 2) {
+            *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0] * kInvG, acc[1] * kInvG);
+        } else {
+            *dst = (bf16_t)(pack_bf16x2(acc[0] * kInvG, 0.f) & 0xffffu);
+        }
+    }
+}
+
+// G > 0: query heads per kv head as a compile-time constant (a power of two); G == 0: any
+// head count (p.G waves, at most 16).
+template <bool SCORES, bool ATTN, int G>
+__global__ __attribute__((amdgpu_flat_work_group_size(1, G > 0 ? G * 64 : 1024), amdgpu_waves_per_eu(1, 2)))
+void cmp_kernel(CmpParams p) {
+    constexpr int kMaxG = G > 0 ? G : 16;
+    __shared__ __attribute__((aligned(16))) bf16_t xs[SCORES ? 2 * kMaxG * 32 * XSB : 8];  // [2][G][32 t][XSB]
+    const int ng = G > 0 ? G : p.G;
 
     const int tid = threadIdx.x, g = tid >> 6, lane = tid & 63, r = lane & 31, hh = lane >> 5;
     const int t0 = blockIdx.x * 32, h = blockIdx.y;
     const int b = blockIdx.z / p.nsplit, split = blockIdx.z % p.nsplit;
     const int j = g * p.Hk + h;
-    const int c = j / p.G;
+    const int c = j / ng;
     const int ut0 = split * p.ut_total / p.nsplit, ut1 = (split + 1) * p.ut_total / p.nsplit;
-    const int nthreads = blockDim.x;
-    const int xs_half = p.G * 32 * XS;
 
     const bool tvalid = t0 + r < p.nb;
     bf16x8 qf[4];
     {
-        const bf16_t* qp = p.qc + b * p.q_sb + (int64_t)(t0 + r) * p.q_sn + (int64_t)j * p.q_sh + 8 * hh;
+        const int trow = min(t0 + r, p.nb - 1);  // rows past the last block: clamped, never stored
+        const bf16_t* qp = p.qc + b * p.q_sb + (int64_t)trow * p.q_sn + (int64_t)j * p.q_sh + 8 * hh;
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds) qf[ds] = as_bf16x8(tvalid ? ld16(qp + 16 * ds) : make_uint4(0, 0, 0, 0));
+        for (int ds = 0; ds < 4; ++ds) qf[ds] = as_bf16x8(ld16(qp + 16 * ds));
     }
     const bf16_t* kp0 = p.kc + b * p.k_sb + (int64_t)c * p.k_sh + 8 * hh;
     const bf16_t* vtp = ATTN ? p.vct + ((int64_t)(b * p.Hk + c) * kHeadDim) * p.nb_pad : nullptr;
+    bf16_t* srow0 = SCORES ? p.sbar + ((int64_t)(b * p.Hk + h) * p.nb + t0) * p.nb_pad : nullptr;
 
     f32x16 o[2];
 #pragma unroll
@@ -79,14 +139,9 @@ __global__ __launch_bounds__(MAXT) void cmp_kernel(CmpParams p) {
         for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
     float m = -INFINITY, l = 0.f;
 
-    CmpFrags cur, nxt;
-    if (ut0 < ut1) load_frags<ATTN>(nxt, p, kp0, vtp, ut0 * 32, r, hh);
-
-    for (int ut = ut0; ut < ut1; ++ut) {
+    // one key-block tile: S, the score mean, the online softmax and PV
+    auto step = [&](const CmpFrags& cur, int ut) __attribute__((always_inline)) {
         const int u0 = ut * 32;
-        cur = nxt;
-        if (ut + 1 < ut1) load_frags<ATTN>(nxt, p, kp0, vtp, u0 + 32, r, hh);
-
         f32x16 s;
 #pragma unroll
         for (int e = 0; e < 16; ++e) s[e] = 0.f;
@@ -94,51 +149,44 @@ __global__ __launch_bounds__(MAXT) void cmp_kernel(CmpParams p) {
         for (int ds = 0; ds < 4; ++ds) s = mfma32(as_bf16x8(cur.k[ds]), qf[ds], s);
 
         if constexpr (SCORES) {
-            // lane holds S^T[u0 + 8*(e/4) + 4*hh + e%4][t0 + r]
-            float* xb = xs + ((ut - ut0) & 1) * xs_half;
+            // lane holds S^T[u0 + 8*(e/4) + 4*hh + e%4][t0 + r]: bf16(S) of this head to LDS
+            bf16_t* xb = xs + ((ut - ut0) & 1) * (kMaxG * 32 * XSB);
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4) {
-                float4 v4;
-                v4.x = round_bf16(s[4 * g4 + 0]);
-                v4.y = round_bf16(s[4 * g4 + 1]);
-                v4.z = round_bf16(s[4 * g4 + 2]);
-                v4.w = round_bf16(s[4 * g4 + 3]);
-                *reinterpret_cast<float4*>(xb + (g * 32 + r) * XS + 8 * g4 + 4 * hh) = v4;
-            }
+            for (int g4 = 0; g4 < 4; ++g4)
+                *reinterpret_cast<uint2*>(xb + (g * 32 + r) * XSB + 8 * g4 + 4 * hh) =
+                    make_uint2(pack_bf16x2(s[4 * g4 + 0], s[4 * g4 + 1]), pack_bf16x2(s[4 * g4 + 2], s[4 * g4 + 3]));
             __syncthreads();  // buffer (ut & 1) is next written two tiles later, after another barrier
-            for (int e = tid; e < 32 * 32; e += nthreads) {
-                const int tl = e >> 5, ul = e & 31;
-                float sum = 0.f;
-                for (int gg = 0; gg < p.G; ++gg) sum += xb[(gg * 32 + tl) * XS + ul];
-                const float mean = sum / (float)p.G;
-                if (t0 + tl < p.nb && u0 + ul < p.nb)
-                    p.sbar[((int64_t)(b * p.Hk + h) * p.nb + t0 + tl) * p.nb_pad + u0 + ul] =
-                        (bf16_t)(pack_bf16x2(mean, 0.f) & 0xffffu);
-            }
+            store_mean<G>(xb, srow0 + u0, p.nb_pad, p.nb - t0, tid, ng);
         }
 
         if constexpr (ATTN) {
-            float mx = -INFINITY;
+            if (u0 + 32 > p.nb) {  // last, partial tile: blocks past the end get no weight
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int u = u0 + 8 * (e >> 2) + 4 * hh + (e & 3);
-                if (u >= p.nb) s[e] = -INFINITY;
-                mx = fmaxf(mx, s[e]);
+                for (int e = 0; e < 16; ++e)
+                    if (u0 + 8 * (e >> 2) + 4 * hh + (e & 3) >= p.nb) s[e] = -INFINITY;
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew = fmaxf(m, mx * p.scale_log2);
-            const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+            float mx = s[0];
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.scale_log2;
+            // lazy reference: moves only when a tile's max exceeds it by more than kTau (the
+            // first tile always moves it), so P <= 2^kTau and O is rarely rescaled
+            if (__builtin_amdgcn_ballot_w64(mx > m + kTau)) {
+                const float mnew = mx > m + kTau ? mx : m;
+                const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+                l *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) o[dt] *= alpha;
+                m = mnew;
+            }
             float sum = 0.f;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float pe = __builtin_amdgcn_exp2f(fmaf(s[e], p.scale_log2, -mnew));
+                const float pe = __builtin_amdgcn_exp2f(fmaf(s[e], p.scale_log2, -m));
                 s[e] = pe;
                 sum += pe;
             }
-            l = l * alpha + sum;
-            m = mnew;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt) o[dt] *= alpha;
+            l += sum;
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
                 uint4 pu;
@@ -153,6 +201,20 @@ __global__ __launch_bounds__(MAXT) void cmp_kernel(CmpParams p) {
                     o[dt] = mfma32(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb, o[dt]);
                 }
             }
+        }
+    };
+    // Two fragment sets swap roles; the next tile is always requested (past the last tile,
+    // the last one again, never used), so every wait targets exactly the set about to be used.
+    if (ut0 < ut1) {
+        CmpFrags f0, f1;
+        load_frags<ATTN>(f0, p, kp0, vtp, ut0 * 32, r, hh);
+        for (int ut = ut0;; ut += 2) {
+            load_frags<ATTN>(f1, p, kp0, vtp, min(ut + 1, ut1 - 1) * 32, r, hh);
+            step(f0, ut);
+            if (ut + 1 >= ut1) break;
+            load_frags<ATTN>(f0, p, kp0, vtp, min(ut + 2, ut1 - 1) * 32, r, hh);
+            step(f1, ut + 1);
+            if (ut + 2 >= ut1) break;
         }
     }
 
@@ -172,32 +234,30 @@ __global__ __launch_bounds__(MAXT) void cmp_kernel(CmpParams p) {
     }
 }
 
+template <int G>
+const void* pick(bool scores, bool attn) {
+    if (scores && attn) return (const void*)cmp_kernel<true, true, G>;
+    if (scores) return (const void*)cmp_kernel<true, false, G>;
+    if (attn) return (const void*)cmp_kernel<false, true, G>;
+    return nullptr;
+}
+
 }  // namespace
 
 hipError_t launch_cmp(const CmpParams& p, bool scores, bool attn, hipStream_t s) {
     const dim3 grid((p.nb + 31) / 32, p.Hk, p.B * p.nsplit), block(p.G * 64);
-    const size_t shmem = scores ? (size_t)2 * p.G * 32 * XS * sizeof(float) : 0;
     void* args[] = {const_cast<CmpParams*>(&p)};
     const void* fn = nullptr;
-    const int nt = p.G * 64;
-#define MOSAIC_CMP_PICK(MAXT)                                                    \
-    if (scores && attn) fn = (const void*)cmp_kernel<true, true, MAXT>;          \
-    else if (scores) fn = (const void*)cmp_kernel<true, false, MAXT>;            \
-    else if (attn) fn = (const void*)cmp_kernel<false, true, MAXT>;              \
-    else return hipSuccess;
-    if (nt <= 256) {
-        MOSAIC_CMP_PICK(256)
-    } else if (nt <= 512) {
-        MOSAIC_CMP_PICK(512)
-    } else {
-        MOSAIC_CMP_PICK(1024)
+    switch (p.G) {
+        case 1: fn = pick<1>(scores, attn); break;
+        case 2: fn = pick<2>(scores, attn); break;
+        case 4: fn = pick<4>(scores, attn); break;
+        case 8: fn = pick<8>(scores, attn); break;
+        case 16: fn = pick<16>(scores, attn); break;
+        default: fn = pick<0>(scores, attn); break;
     }
-#undef MOSAIC_CMP_PICK
-    if (shmem > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem);
-        if (e != hipSuccess) return e;
-    }
-    return hipLaunchKernel(fn, grid, block, args, shmem, s);
+    if (fn == nullptr) return hipSuccess;
+    return hipLaunchKernel(fn, grid, block, args, 0, s);
 }
 
 }  // namespace mosaic
