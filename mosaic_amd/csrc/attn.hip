@@ -64,20 +64,29 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Issue the direct-to-LDS loads of one 64-key tile (K and V rows key0 .. key0+63): NW waves,
-// 8/NW 1 KB runs per wave and tensor.  wave_u is the wave index as a wave-uniform value.
+// Direct-to-LDS loads of one 64-key tile (K and V rows key0 .. key0+63): NW waves, 8/NW
+// 1 KB runs per wave and tensor.  The per-lane element offsets (key row * stride + swizzled
+// chunk) do not change between tiles and are computed once; a tile only adds key0 * stride.
 template <int NW>
-__device__ __forceinline__ void issue_tile(const bf16_t* kb, const bf16_t* vb, int64_t ksn, int64_t vsn, int key0,
-                                           bf16_t* Kd, bf16_t* Vd, int wave_u, int lane) {
-    constexpr int PER = 8 / NW;
+__device__ __forceinline__ void dma_init(int* dk, int* dv, int wave_u, int lane, int64_t ksn, int64_t vsn) {
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int row0 = 8 * (wave_u * PER + i);
-        const int row = row0 + (lane >> 3), pos = lane & 7;
-        const int ck = pos ^ ((row >> 1) & 7);   // global chunk stored at position pos
-        const int cv = pos ^ ((row & 3) << 1);
-        __builtin_amdgcn_global_load_lds(kb + (int64_t)(key0 + row) * ksn + 8 * ck, (lds_void*)(Kd + row0 * 64), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vb + (int64_t)(key0 + row) * vsn + 8 * cv, (lds_void*)(Vd + row0 * 64), 16, 0, 0);
+    for (int i = 0; i < 8 / NW; ++i) {
+        const int row = 8 * (wave_u * (8 / NW) + i) + (lane >> 3), pos = lane & 7;
+        dk[i] = (int)(row * ksn) + 8 * (pos ^ ((row >> 1) & 7));  // global chunk stored at position pos
+        dv[i] = (int)(row * vsn) + 8 * (pos ^ ((row & 3) << 1));
+    }
+}
+template <int NW>
+__device__ __forceinline__ void dma_issue(const int* dk, const int* dv, const bf16_t* kb, const bf16_t* vb,
+                                          int64_t ksn, int64_t vsn, int key0, bf16_t* Kd, bf16_t* Vd, int wave_u) {
+    const int k0 = __builtin_amdgcn_readfirstlane(key0);
+    const bf16_t* kt = kb + (int64_t)k0 * ksn;
+    const bf16_t* vt = vb + (int64_t)k0 * vsn;
+#pragma unroll
+    for (int i = 0; i < 8 / NW; ++i) {
+        const int row0 = 8 * (wave_u * (8 / NW) + i);
+        __builtin_amdgcn_global_load_lds(kt + dk[i], (lds_void*)(Kd + row0 * 64), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vt + dv[i], (lds_void*)(Vd + row0 * 64), 16, 0, 0);
     }
 }
 
@@ -316,7 +325,9 @@ void bsa_attn_kernel(AttnParams p) {
         const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim;
         if (lane < 32) __builtin_amdgcn_global_load_lds(ocp + 2 * lane, (lds_void*)(Ocmp + wave * 64), 4, 0, 0);
     }
-    if constexpr (kLocal) issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, lstart, Ks0, Vs0, wave, lane);
+    int dk[8 / NW], dv[8 / NW];
+    dma_init<NW>(dk, dv, wave, lane, p.k_sn, p.v_sn);
+    if constexpr (kLocal) dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, lstart, Ks0, Vs0, wave);
 
     // Selected blocks: wave 0 compacts the in-range indices (top-k order kept) into LDS once,
     // so tile addresses never wait on a global load inside the loop.
@@ -351,7 +362,7 @@ void bsa_attn_kernel(AttnParams p) {
         }
         return key0;
     };
-    if (!kLocal && total_tiles > 0) issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, next_key0(0), Ks0, Vs0, wave, lane);
+    if (!kLocal && total_tiles > 0) dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(0), Ks0, Vs0, wave);
 
     ReadOffsets ro;
     ro.init(lane);
@@ -369,7 +380,7 @@ void bsa_attn_kernel(AttnParams p) {
         wait_vmem();
         __syncthreads();
         if (t + 1 < total_tiles)
-            issue_tile<NW>(kb, vb, p.k_sn, p.v_sn, next_key0(t + 1), BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, wave, lane);
+            dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(t + 1), BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, wave);
     };
 
     bf16_t* outp = p.out + ((int64_t)b * p.N + n0) * p.Hq * kHeadDim + (int64_t)j * kHeadDim;
@@ -485,7 +496,7 @@ void bsa_attn_kernel(AttnParams p) {
             begin_tile(bufc, t);
             s_tile<false>(Kc, ro, qf, m, s, hh);
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) m[qt] = round_bf16(tile_max(s, qt));
+            for (int qt = 0; qt < 2; ++qt) m[qt] = tile_max(s, qt);
             float lt[2];
             exp_pack<false, true>(s, m, 1.f, pb, lt);
             l[0] += lt[0];
@@ -497,25 +508,24 @@ void bsa_attn_kernel(AttnParams p) {
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
             const bf16_t* Vc = BUF ? Vs1 : Vs0;
             begin_tile(bufc, t);
-            s_tile<true>(Kc, ro, qf, m, s, hh);
+            s_tile<false>(Kc, ro, qf, m, s, hh);
             float lt[2];
-            exp_pack<false, false>(s, m, 1.f, pb, lt);
+            exp_pack<false, true>(s, m, 1.f, pb, lt);
             if (__builtin_amdgcn_ballot_w64(!(lt[0] <= kSumLimit && lt[1] <= kSumLimit))) {
                 // rare: recompute one query tile at a time with the reference moved up to
                 // the tile's row max (K of this tile stays in LDS until the next barrier)
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) {
                     f32x16 sh[2];
-                    s_half<true>(Kc, ro, qf[qt], m[qt], sh, hh);
+                    s_half<false>(Kc, ro, qf[qt], m[qt], sh, hh);
                     const float mx = half_max(sh);
-                    const float mnew = mx > 0.f ? round_bf16(m[qt] + mx) : m[qt];
-                    const float dl = mnew - m[qt];
-                    const float alpha = __builtin_amdgcn_exp2f(-dl);
+                    const float mnew = mx > m[qt] ? mx : m[qt];
+                    const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);
                     l[qt] *= alpha;
 #pragma unroll
                     for (int dt = 0; dt < 2; ++dt) o[dt][qt] *= alpha;
                     m[qt] = mnew;
-                    exp_pack_half(sh, dl, pb[qt], lt[qt]);
+                    exp_pack_half(sh, mnew, pb[qt], lt[qt]);
                 }
             }
             l[0] += lt[0];
