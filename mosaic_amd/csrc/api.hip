@@ -56,7 +56,7 @@ int choose_splits(int B, int nb, int Hk) {
 
 struct Layout {
     int nb = 0, nb_pad = 0, nsplit = 1;
-    size_t qc = 0, kc = 0, vct = 0, sbar = 0, idx = 0, opart = 0, ml = 0, ocmp = 0, total = 0;
+    size_t qc = 0, kc = 0, vct = 0, sbar = 0, idx = 0, kbnd = 0, opart = 0, ml = 0, ocmp = 0, total = 0;
 };
 
 bool uses_selection(int mode) { return mode == MOSAIC_BSA_FULL || mode == MOSAIC_BSA_NO_COMPRESSION; }
@@ -110,6 +110,7 @@ Layout layout_of(const mosaic_bsa_args* a) {
     if (uses_selection(a->mode)) {
         L.sbar = off; off = align_up(off + B * Hk * nb * nbp * 2);
         L.idx = off; off = align_up(off + B * nb * Hk * K * 4);
+        L.kbnd = off; off = align_up(off + B * nb * Hk * 8 * 4);
     }
     L.total = off;
     return L;
@@ -176,6 +177,7 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
             pp.out_t = reinterpret_cast<bf16_t*>(w + L.vct);
         }
         pp.B = B; pp.nb = L.nb; pp.nb_pad = L.nb_pad; pp.bs = a->sparse_block_size;
+        if (sel) pp.kbnd = reinterpret_cast<float*>(w + L.kbnd);
         if (int e = launch_status(launch_pool(pp, s))) return e;
         if (int e = record(events, 1, s)) return e;
 
@@ -206,6 +208,7 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
             tp.rows = B * Hk * L.nb;
             if (int e = launch_status(launch_topk(tp, s))) return e;
             ap.idx = tp.idx32;
+            ap.kbnd = pp.kbnd;
         } else if (cmp) {
             if (int e = launch_status(launch_combine(cb, B, L.nb, s))) return e;
         }

@@ -58,6 +58,10 @@ constexpr float kTau = 8.0f;
 // Largest accepted partial row sum of a selected tile under the reference max: every P is
 // then <= 2^16, far from fp32 / bf16 overflow.
 constexpr float kSumLimit = 65536.0f;
+// Bounded-logit path of the selected branch: largest |s| (base-2 logit) it accepts, and the
+// most selected blocks whose key-norm bounds are staged.
+constexpr float kLogitBound = 64.0f;
+constexpr int kMaxBounded = 64;
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -238,6 +242,46 @@ __device__ __forceinline__ void exp_pack_half(const f32x16 (&s)[2], float m, bf1
     lt = lsum[0] + lsum[1];
 }
 
+// P = exp2(s) packed to bf16 for the PV product; the row sums are taken on the matrix pipe
+// (row_sums).
+__device__ __forceinline__ void exp_pack_raw(const f32x16 (&s)[2][2], bf16x8 (&pb)[2][2][2]) {
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                uint32_t w[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    w[i] = pack_bf16x2(__builtin_amdgcn_exp2f(s[kt][qt][8 * s2 + 2 * i]),
+                                       __builtin_amdgcn_exp2f(s[kt][qt][8 * s2 + 2 * i + 1]));
+                pb[qt][kt][s2] = as_bf16x8(make_uint4(w[0], w[1], w[2], w[3]));
+            }
+}
+
+// Selector A of the row-sum product D = A B on v_mfma_f32_16x16x32_bf16, where B is a PV
+// operand pb[qt][kt][s2] (lane l: 8 keys of query l % 32 from key half l / 32).  Lane l of B
+// lands in column l % 16, contraction chunk c = l / 16, so chunks 0 and 2 carry queries
+// 0..15 and chunks 1 and 3 queries 16..31.  A[i][chunk c] = 1 when (c & 1) == ((i >> 2) & 1):
+// output lane l (rows 4*(l/16)..+3, column l % 16) then receives the 16-key sum of P for
+// query l % 32, both key halves included.
+__device__ __forceinline__ bf16x8 row_sum_selector(int lane) {
+    const uint32_t h = ((((lane & 15) >> 2) ^ (lane >> 4)) & 1) ? 0u : 0x3f80u;
+    const uint32_t w = h | (h << 16);
+    return as_bf16x8(make_uint4(w, w, w, w));
+}
+
+// acc[qt] += row sums of the bf16 P of one tile (every lane of a query column holds its total)
+__device__ __forceinline__ void row_sums(const bf16x8& sel, const bf16x8 (&pb)[2][2][2], f32x4 (&acc)[2]) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) acc[qt] = mfma16(sel, pb[qt][kt][s2], acc[qt]);
+}
+
 // Row max of a tile (both lane halves) for query tile qt.
 __device__ __forceinline__ float tile_max(const f32x16 (&s)[2][2], int qt) {
     float mx = s[0][qt][0];
@@ -270,6 +314,8 @@ void bsa_attn_kernel(AttnParams p) {
     constexpr bool kCmp = MODE == kModeFull || MODE == kModeNoSelection;
     constexpr bool kWeights = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeNoSelection;
     constexpr bool kPartial = MODE == kModeFull || MODE == kModeNoCompression;
+    // selected tiles may take the bounded-logit path (key-norm bounds come with the pooling)
+    constexpr bool kFastSel = MODE == kModeFull || MODE == kModeNoCompression;
 
     // two staging buffers as separate objects, so the compiler can tell the loads in flight
     // into one buffer from the reads of the other
@@ -281,6 +327,7 @@ void bsa_attn_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) bf16_t Ocmp[kCmp ? NW * 64 : 8];  // compressed-branch rows
     __shared__ int sel_key0[kSel ? kMaxSelected : 1];  // first key of each in-range selected block
     __shared__ int sel_count;
+    __shared__ __attribute__((aligned(16))) float sel_kbnd[kFastSel ? kMaxBounded * 8 : 4];  // key-norm bounds
 
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, hh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -381,6 +428,20 @@ void bsa_attn_kernel(AttnParams p) {
         __syncthreads();
         if (t + 1 < total_tiles)
             dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(t + 1), BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, wave);
+        if constexpr (kFastSel) {
+            // with the first selected tile, the key-norm bounds of the selected blocks (32 bytes
+            // each) go to LDS; they arrive with that tile
+            if (t + 1 == tl_count && wave == 0 && p.kbnd != nullptr && nvalid <= kMaxBounded) {
+                for (int i0 = 0; i0 < nvalid; i0 += 32) {
+                    const int i = i0 + (lane >> 1);
+                    if (i < nvalid) {
+                        const int64_t blk = sel_key0[i] / p.bs;
+                        const float* src = p.kbnd + ((b * p.nb + blk) * p.Hk + c) * 8 + 4 * (lane & 1);
+                        __builtin_amdgcn_global_load_lds(src, (lds_void*)(sel_kbnd + 8 * i0), 16, 0, 0);
+                    }
+                }
+            }
+        }
     };
 
     bf16_t* outp = p.out + ((int64_t)b * p.N + n0) * p.Hq * kHeadDim + (int64_t)j * kHeadDim;
@@ -488,26 +549,56 @@ void bsa_attn_kernel(AttnParams p) {
         zero(o);
         l[0] = l[1] = 0.f;
 
-        // first selected tile: exact row max, rounded to bf16, becomes the reference
-        auto first_step = [&](auto bufc, int t) {
+        // Bounded-logit path.  |s| <= |q'| * |k|; with the pooled key-norm bounds of the
+        // selected blocks, a wave whose rows all have |s| <= kLogitBound takes P = exp2(s)
+        // directly (reference 0: P stays within [2^-64, 2^64], far from fp32 / bf16 limits)
+        // and sums the bf16 P on the matrix pipe.  Otherwise the running-reference path below.
+        float qn2[2] = {0.f, 0.f};  // |q'|^2 of this lane's rows
+        if constexpr (kFastSel) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+#pragma unroll
+                for (int ds = 0; ds < 4; ++ds) {
+                    const uint4 u = __builtin_bit_cast(uint4, qf[qt][ds]);
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int mm = 0; mm < 4; ++mm) {
+                        qn2[qt] = fmaf(bf_lo(w[mm]), bf_lo(w[mm]), qn2[qt]);
+                        qn2[qt] = fmaf(bf_hi(w[mm]), bf_hi(w[mm]), qn2[qt]);
+                    }
+                }
+                qn2[qt] += __shfl_xor(qn2[qt], 32);
+            }
+        }
+        // after the barrier of the first selected tile: every row of this wave bounded?
+        auto bounded = [&]() -> bool {
+            if (p.kbnd == nullptr || nvalid > kMaxBounded) return false;
+            float kb2 = 0.f;
+            for (int i = lane; i < nvalid; i += 64) {
+                const float4 a = *reinterpret_cast<const float4*>(sel_kbnd + 8 * i);
+                const float4 c4 = *reinterpret_cast<const float4*>(sel_kbnd + 8 * i + 4);
+                kb2 = fmaxf(kb2, ((a.x + a.y) + (a.z + a.w)) + ((c4.x + c4.y) + (c4.z + c4.w)));
+            }
+            kb2 = wave_max(kb2);
+            const float lim = kLogitBound * kLogitBound;
+            return !__builtin_amdgcn_ballot_w64(!(qn2[0] * kb2 <= lim && qn2[1] * kb2 <= lim));
+        };
+
+        // running-reference path: the first tile's exact row max is the reference
+        auto first_body = [&](auto bufc) __attribute__((always_inline)) {
             constexpr int BUF = decltype(bufc)::value;
-            const bf16_t* Kc = BUF ? Ks1 : Ks0;
-            const bf16_t* Vc = BUF ? Vs1 : Vs0;
-            begin_tile(bufc, t);
-            s_tile<false>(Kc, ro, qf, m, s, hh);
+            s_tile<false>(BUF ? Ks1 : Ks0, ro, qf, m, s, hh);
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) m[qt] = tile_max(s, qt);
             float lt[2];
             exp_pack<false, true>(s, m, 1.f, pb, lt);
             l[0] += lt[0];
             l[1] += lt[1];
-            pv_tile(Vc, ro, pb, o);
+            pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
         };
-        auto sel_step = [&](auto bufc, int t) {
+        auto sel_body = [&](auto bufc) __attribute__((always_inline)) {
             constexpr int BUF = decltype(bufc)::value;
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
-            const bf16_t* Vc = BUF ? Vs1 : Vs0;
-            begin_tile(bufc, t);
             s_tile<false>(Kc, ro, qf, m, s, hh);
             float lt[2];
             exp_pack<false, true>(s, m, 1.f, pb, lt);
@@ -530,23 +621,72 @@ void bsa_attn_kernel(AttnParams p) {
             }
             l[0] += lt[0];
             l[1] += lt[1];
-            pv_tile(Vc, ro, pb, o);
+            pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
         };
+
         int t = tl_count;
-        if (t < total_tiles) {
-            if (t & 1) first_step(Buf1{}, t);
-            else first_step(Buf0{}, t);
+        bool fast = false;
+        if (t < total_tiles) {  // barrier of the first selected tile, then the path choice
+            if (t & 1) begin_tile(Buf1{}, t);
+            else begin_tile(Buf0{}, t);
+            if constexpr (kFastSel) fast = bounded();
+        }
+        if (fast) {
+            const bf16x8 rsel = row_sum_selector(lane);
+            f32x4 lacc[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            auto fast_body = [&](auto bufc) __attribute__((always_inline)) {
+                constexpr int BUF = decltype(bufc)::value;
+                s_tile<false>(BUF ? Ks1 : Ks0, ro, qf, m, s, hh);
+                exp_pack_raw(s, pb);
+                row_sums(rsel, pb, lacc);
+                pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
+            };
+            if (t & 1) fast_body(Buf1{});
+            else fast_body(Buf0{});
             ++t;
-        }
-        if ((t & 1) && t < total_tiles) {
-            sel_step(Buf1{}, t);
+            if ((t & 1) && t < total_tiles) {
+                begin_tile(Buf1{}, t);
+                fast_body(Buf1{});
+                ++t;
+            }
+            for (; t + 1 < total_tiles; t += 2) {
+                begin_tile(Buf0{}, t);
+                fast_body(Buf0{});
+                begin_tile(Buf1{}, t + 1);
+                fast_body(Buf1{});
+            }
+            if (t < total_tiles) {
+                begin_tile(Buf0{}, t);
+                fast_body(Buf0{});
+            }
+            // every lane holds its row's whole sum; the epilogue adds the two key halves
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                l[qt] = hh == 0 ? lacc[qt][0] : 0.f;
+                m[qt] = 0.f;
+            }
+        } else if (t < total_tiles) {
+            if (t & 1) first_body(Buf1{});
+            else first_body(Buf0{});
             ++t;
+            if ((t & 1) && t < total_tiles) {
+                begin_tile(Buf1{}, t);
+                sel_body(Buf1{});
+                ++t;
+            }
+            for (; t + 1 < total_tiles; t += 2) {
+                begin_tile(Buf0{}, t);
+                sel_body(Buf0{});
+                begin_tile(Buf1{}, t + 1);
+                sel_body(Buf1{});
+            }
+            if (t < total_tiles) {
+                begin_tile(Buf0{}, t);
+                sel_body(Buf0{});
+            }
         }
-        for (; t + 1 < total_tiles; t += 2) {
-            sel_step(Buf0{}, t);
-            sel_step(Buf1{}, t + 1);
-        }
-        if (t < total_tiles) sel_step(Buf0{}, t);
     }
 
     // ------------------------------------------------------------------ epilogue

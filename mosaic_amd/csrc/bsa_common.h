@@ -44,6 +44,12 @@ __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x32_bf16: A (16 x 32) lane holds A[l % 16][8*(l/16) + i]; B (32 x 16) lane
+// holds B[8*(l/16) + i][l % 16]; D (16 x 16, 4 fp32) register e holds D[4*(l/16) + e][l % 16].
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
@@ -71,6 +77,8 @@ struct PoolParams {
     int heads[3];
     bf16_t* out_bnhd[3];       // [B, nb, H, 64] outputs (null: not written)
     bf16_t* out_t;             // optional transposed output of tensor 2: [B, H, 64, nb_pad]
+    float* kbnd;               // optional [B, nb, H1, 8]: per 8-dim chunk of tensor 1, the block's
+                               // largest squared chunk norm (their sum bounds |k|^2 in the block)
     int B, nb, nb_pad, bs;
 };
 
@@ -121,6 +129,7 @@ struct AttnParams {
     float* lse;              // [B, N, Hq] (selected-only mode, optional)
     const void* idx;         // [B, nb, Hk, K] int32 or int64
     const bf16_t* ocmp;      // compressed-branch output [B, nb, Hq, 64]
+    const float* kbnd;       // key-norm bounds per selected block [B, nb, Hk, 8] (optional)
     int B, N, Hq, Hk, G;
     int bs_l, bs, K, nb;
     int head_groups;         // G / waves-per-workgroup

@@ -6,6 +6,9 @@
 // (HBM-bound: each thread streams one 16-byte column chunk down the block's tokens).
 // Outputs: [B, nb, H, 64] for the pooled tensors and, for v, the transposed layout
 // [B, Hk, 64, nb_pad] (zero beyond nb) read by the compressed-attention PV product.
+// Optionally, for the keys (tensor 1), the largest squared norm of each 8-dim chunk over the
+// block's tokens: the sum of a head's 8 values bounds |k|^2 for every key of the block, which
+// the attention kernel uses to bound its logits.
 #include "bsa_common.h"
 
 namespace mosaic {
@@ -33,18 +36,26 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
         float acc[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+        float sqmax = 0.f;  // largest squared norm of this 8-dim chunk over the block's tokens
         for (int n = 0; n < p.bs; n += 8) {
             uint4 v[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) v[u] = ld16(src + (int64_t)(n + u) * sn);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                acc[0] += bf_lo(v[u].x); acc[1] += bf_hi(v[u].x);
-                acc[2] += bf_lo(v[u].y); acc[3] += bf_hi(v[u].y);
-                acc[4] += bf_lo(v[u].z); acc[5] += bf_hi(v[u].z);
-                acc[6] += bf_lo(v[u].w); acc[7] += bf_hi(v[u].w);
+                const float x[8] = {bf_lo(v[u].x), bf_hi(v[u].x), bf_lo(v[u].y), bf_hi(v[u].y),
+                                    bf_lo(v[u].z), bf_hi(v[u].z), bf_lo(v[u].w), bf_hi(v[u].w)};
+                float sq = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    acc[e] += x[e];
+                    sq = fmaf(x[e], x[e], sq);
+                }
+                sqmax = fmaxf(sqmax, sq);
             }
         }
+        if (which == 1 && p.kbnd != nullptr)
+            p.kbnd[(((int64_t)b * p.nb + t) * p.heads[1] + hd) * 8 + ch] = sqmax;
         const float denom = (float)p.bs;
         float mean[8];
 #pragma unroll

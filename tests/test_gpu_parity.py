@@ -164,6 +164,33 @@ def test_mosaic_attn_func_variants():
     close(got, ref)
 
 
+@pytest.mark.parametrize("qscale", [30.0, 3.0], ids=["logits_to_200", "logits_to_20"])
+def test_mosaic_attn_func_large_logits_mixed_paths(qscale):
+    """Every other query head scaled: with qscale 30 its selected-branch logits reach ~200 (base 2),
+    beyond what P = exp2(s) without a reference could hold in fp32, so those waves must take the
+    running-reference path (and its recompute of tiles that exceed the reference) while the
+    other waves of the same workgroups take the bounded path; a wrong choice gives inf/NaN."""
+    wl = BOTTLENECK_NSIDE16
+    q, k, v, w = make_inputs(wl, seed=4)
+    sc = torch.ones(wl.q_heads)
+    sc[::2] = qscale
+    q = (q.float() * sc[None, None, :, None]).to(torch.bfloat16)
+    out, idx = _run_full(q, k, v, w, wl.block_attn_size, wl.sparse_block_size, wl.sparse_block_count)
+    ref_out, parts = O.mosaic_attn_func(q, k, v, w, wl.block_attn_size, wl.sparse_block_size,
+                                        wl.sparse_block_count, False, block_indices=idx, return_parts=True)
+    bad, amb, rows = O.selection_band_check(parts["scores"].permute(0, 2, 1, 3), idx, wl.sparse_block_count)
+    assert bad == 0, f"{bad}/{rows} rows violate the band rule"
+    # Such peaked rows return single v entries (|v| up to ~4.5), where the bf16 spacing is
+    # 2^-6 .. 2^-5 and the reference's five bf16-rounded merge steps alone move an element by
+    # up to 2 spacings: the absolute bar is widened by 2^-7 |ref| (two bf16 half-ulps).
+    g, r = out.float(), ref_out.float()
+    assert torch.isfinite(g).all(), "non-finite output"
+    excess = ((g - r).abs() - (MAX_ABS + r.abs() * 2.0 ** -7)).max().item()
+    assert excess <= 0, f"max excess over the bar {excess:.3e}"
+    rel = ((g - r).norm() / r.norm()).item()
+    assert rel <= REL_L2, f"rel_l2 {rel:.3e}"
+
+
 def test_strided_inputs_match_contiguous():
     """q/k/v as the caller produces them: [B, S, H, d] views of a sequence-first [S, B, H*d]."""
     wl = Workload("nside8_b2_h12kv3_bs64_top4", 8, 2, 12, 3, 64, 64, 64, 4, False)
