@@ -149,6 +149,21 @@ __device__ __forceinline__ void s_tile(const bf16_t* Ks, const ReadOffsets& ro, 
     }
 }
 
+// S^T = K Q^T (as s_tile<false>) with the key tiles in sequence: the scores of keys 0..31
+// are complete after half of the MFMAs, so their exponentials can overlap the other half.
+__device__ __forceinline__ void s_tile_seq(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[2][4],
+                                           f32x16 (&s)[2][2]) {
+    zero(s);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds) {
+            const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(Ks + 32 * kt * 64 + ro.k[ds]));
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) s[kt][qt] = mfma32(a, qf[qt][ds], s[kt][qt]);
+        }
+}
+
 // One query tile of s_tile<BIAS> (rare recompute path), as s[key tile].
 template <bool BIAS>
 __device__ __forceinline__ void s_half(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[4], float m,
@@ -246,9 +261,9 @@ __device__ __forceinline__ void exp_pack_half(const f32x16 (&s)[2], float m, bf1
 // (row_sums).
 __device__ __forceinline__ void exp_pack_raw(const f32x16 (&s)[2][2], bf16x8 (&pb)[2][2][2]) {
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
                 uint32_t w[4];
@@ -301,8 +316,6 @@ __device__ __forceinline__ float half_max(const f32x16 (&s)[2]) {
     return fmaxf(mx, __shfl_xor(mx, 32));
 }
 
-__device__ __forceinline__ float load_bf16(const bf16_t* p) { return bf2f(*p); }
-
 using Buf0 = std::integral_constant<int, 0>;
 using Buf1 = std::integral_constant<int, 1>;
 
@@ -327,6 +340,7 @@ void bsa_attn_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) bf16_t Ocmp[kCmp ? NW * 64 : 8];  // compressed-branch rows
     __shared__ int sel_key0[kSel ? kMaxSelected : 1];  // first key of each in-range selected block
     __shared__ int sel_count;
+    __shared__ uint32_t Gw[kWeights ? NW * 3 * 64 : 1];  // gate words [wave][branch][row]
     __shared__ __attribute__((aligned(16))) float sel_kbnd[kFastSel ? kMaxBounded * 8 : 4];  // key-norm bounds
 
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, hh = lane >> 5;
@@ -358,16 +372,23 @@ void bsa_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int ds = 0; ds < 4; ++ds)
             qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
-    // gate weights of rows n0 + 32*qt + r: branch 0 is needed when the local branch ends,
-    // branches 1 and 2 are loaded in the epilogue
-    auto gate = [&](int sidx, int qt) -> float {
-        return load_bf16(p.w + sidx * p.w_ss + b * p.w_sb + (int64_t)(n0 + 32 * qt + r) * p.w_sn + (int64_t)j * p.w_sh);
+    // Gate weights of the 64 rows: the aligned 4-byte word holding each bf16 gate goes straight
+    // to LDS (lane L: row n0 + L), so no register waits on them; gate(s, qt) picks the half.
+    auto gate_ptr = [&](int sidx, int row) -> const bf16_t* {
+        return p.w + sidx * p.w_ss + b * p.w_sb + (int64_t)(n0 + row) * p.w_sn + (int64_t)j * p.w_sh;
     };
-    float w0r[2] = {0.f, 0.f};
     if constexpr (kWeights) {
-        w0r[0] = gate(0, 0);
-        w0r[1] = gate(0, 1);
+#pragma unroll
+        for (int sidx = 0; sidx < 3; ++sidx) {
+            const uintptr_t a = reinterpret_cast<uintptr_t>(gate_ptr(sidx, lane)) & ~uintptr_t(3);
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a), (lds_void*)(Gw + (wave * 3 + sidx) * 64),
+                                             4, 0, 0);
+        }
     }
+    auto gate = [&](int sidx, int qt) -> float {
+        const uint32_t wd = Gw[(wave * 3 + sidx) * 64 + 32 * qt + r];
+        return (reinterpret_cast<uintptr_t>(gate_ptr(sidx, 32 * qt + r)) & 2) ? bf_hi(wd) : bf_lo(wd);
+    };
     if constexpr (kCmp) {  // compressed-branch output row of (block, head j): 128 bytes into LDS
         const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim;
         if (lane < 32) __builtin_amdgcn_global_load_lds(ocp + 2 * lane, (lds_void*)(Ocmp + wave * 64), 4, 0, 0);
@@ -493,7 +514,7 @@ void bsa_attn_kernel(AttnParams p) {
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
                 f[qt] = inv[qt];
-                if constexpr (kWeights) f[qt] *= w0r[qt];
+                if constexpr (kWeights) f[qt] *= gate(0, qt);
             }
             if constexpr (MODE == kModeLocalOnly) {
 #pragma unroll
@@ -638,7 +659,7 @@ void bsa_attn_kernel(AttnParams p) {
             for (int qt = 0; qt < 2; ++qt) lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
             auto fast_body = [&](auto bufc) __attribute__((always_inline)) {
                 constexpr int BUF = decltype(bufc)::value;
-                s_tile<false>(BUF ? Ks1 : Ks0, ro, qf, m, s, hh);
+                s_tile_seq(BUF ? Ks1 : Ks0, ro, qf, s);
                 exp_pack_raw(s, pb);
                 row_sums(rsel, pb, lacc);
                 pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
@@ -719,7 +740,7 @@ void bsa_attn_kernel(AttnParams p) {
         float fs[2], fc[2], nrm[2];
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            const float w0 = w0r[qt], w1 = gate(1, qt), w2 = gate(2, qt);
+            const float w0 = gate(0, qt), w1 = gate(1, qt), w2 = gate(2, qt);
             if constexpr (kSel) fs[qt] = w2 / (l[qt] + __shfl_xor(l[qt], 32));
             fc[qt] = w1;
             nrm[qt] = MODE == kModeNoCompression ? 1.f / (w0 + w2 + 1e-8f)

@@ -52,6 +52,12 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
     const int bh = row / p.nb;
     const int h = bh % p.Hk, b = bh / p.Hk;
 
+    // The row's scores are loaded unconditionally (index clamped into the padded row) and
+    // before the combine's loads, so all of them share one memory round trip.
+    uint32_t raw[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) raw[i] = src[min(lane + 64 * i, p.nb_pad - 1)];
+
     // compressed-branch output of block t for the G query heads g*Hk + h of this row
     if (p.cmb.ocmp != nullptr) {
         int g = 0;
@@ -63,7 +69,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
         const int u = lane + 64 * i;
-        key[i] = (u < p.nb) ? ((order16(src[u]) << 16) | (0xffffu - (uint32_t)u)) : 0u;
+        key[i] = (u < p.nb) ? ((order16(raw[i]) << 16) | (0xffffu - (uint32_t)u)) : 0u;
     }
     // Each lane keeps its four largest remaining keys.  Keys leave the wave in descending
     // order, so a lane's emitted keys are always its largest ones: after emitting key x the
