@@ -30,15 +30,17 @@
 // element b of the 8-byte rows addressed by lanes a, a+4, a+8, a+12.
 //
 // Softmax.  Local tiles: exact row max per tile with a lazy reference (a row's reference
-// only moves when a tile's max exceeds it by more than kTau).  Selected tiles: the first
-// tile's row max, rounded to bf16, is the reference m; later tiles get -m as one extra
-// contraction step of the QK^T MFMA (A = ones, B = -m), so P = exp2(S - m) is taken without
-// a max pass, and a tile whose row sums exceed kSumLimit (or are not finite) is recomputed
-// from LDS with the reference moved up to its row max.  Numerator and denominator share the
-// reference, so the result is the same softmax.  Row sums add the fp32 P before its bf16
-// rounding, as the selected-branch kernel does (ops.py:125), with plain fp32 adds: on gfx950
-// v_dot2c_f32_bf16 shares the matrix pipe and stalls behind the other wave's MFMAs, while
-// fp32 VALU work overlaps them.
+// only moves when a tile's max exceeds it by more than kTau), fp32 row sums.  Selected
+// tiles take one of two paths, chosen per wave at the first selected tile:
+//   bounded     the pooling kernel's per-block key-norm bounds and |q'| bound every logit
+//               of the wave by kLogitBound, so P = exp2(s) needs no reference, no max and
+//               no rescale; row sums of the bf16 P run on the matrix pipe (row_sums).
+//   running     the first tile's exact row max is the reference m; later tiles take
+//               exp2(s - m) without a max pass, and a tile whose row sums exceed kSumLimit
+//               (or are not finite) is recomputed from LDS with the reference moved up to
+//               its row max.  Row sums add the fp32 P, as the selected-branch kernel does
+//               (ops.py:125).
+// Numerator and denominator share the reference, so both give the same softmax.
 //
 // Two workgroups share a CU (2 waves per SIMD): one wave's softmax VALU work overlaps the
 // other's MFMA work.  The local branch's partial merge (w0 * o_ba) waits in LDS as bf16.
@@ -118,26 +120,10 @@ struct ReadOffsets {
     }
 };
 
-// S^T = K Q^T for one 64-key tile: s[key tile][query tile].  With BIAS the per-query
-// reference m (bf16-representable) enters as one extra contraction step (A = ones at
-// contraction element (hh=0, i=0), B = -m at the same element), so s = S^T - m.
-template <bool BIAS>
+// S^T = K Q^T for one 64-key tile: s[key tile][query tile].
 __device__ __forceinline__ void s_tile(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[2][4],
-                                       const float (&m)[2], f32x16 (&s)[2][2], int hh) {
-    if constexpr (BIAS) {
-        f32x16 z;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) z[e] = 0.f;
-        const bf16x8 kbias = as_bf16x8(make_uint4(hh == 0 ? 0x3f80u : 0u, 0u, 0u, 0u));
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            const bf16x8 qbias = as_bf16x8(make_uint4(hh == 0 ? pack_bf16x2(-m[qt], 0.f) : 0u, 0u, 0u, 0u));
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) s[kt][qt] = mfma32(kbias, qbias, z);
-        }
-    } else {
-        zero(s);
-    }
+                                       f32x16 (&s)[2][2]) {
+    zero(s);
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
 #pragma unroll
@@ -149,7 +135,7 @@ __device__ __forceinline__ void s_tile(const bf16_t* Ks, const ReadOffsets& ro, 
     }
 }
 
-// S^T = K Q^T (as s_tile<false>) with the key tiles in sequence: the scores of keys 0..31
+// S^T = K Q^T (as s_tile) with the key tiles in sequence: the scores of keys 0..31
 // are complete after half of the MFMAs, so their exponentials can overlap the other half.
 __device__ __forceinline__ void s_tile_seq(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[2][4],
                                            f32x16 (&s)[2][2]) {
@@ -164,21 +150,12 @@ __device__ __forceinline__ void s_tile_seq(const bf16_t* Ks, const ReadOffsets& 
         }
 }
 
-// One query tile of s_tile<BIAS> (rare recompute path), as s[key tile].
-template <bool BIAS>
-__device__ __forceinline__ void s_half(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[4], float m,
-                                       f32x16 (&s)[2], int hh) {
-    f32x16 z;
+// One query tile of s_tile (rare recompute path), as s[key tile].
+__device__ __forceinline__ void s_half(const bf16_t* Ks, const ReadOffsets& ro, const bf16x8 (&qf)[4], f32x16 (&s)[2]) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) z[e] = 0.f;
-    if constexpr (BIAS) {
-        const bf16x8 kbias = as_bf16x8(make_uint4(hh == 0 ? 0x3f80u : 0u, 0u, 0u, 0u));
-        const bf16x8 qbias = as_bf16x8(make_uint4(hh == 0 ? pack_bf16x2(-m, 0.f) : 0u, 0u, 0u, 0u));
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) s[kt] = mfma32(kbias, qbias, z);
-    } else {
-        s[0] = s[1] = z;
-    }
+        for (int e = 0; e < 16; ++e) s[kt][e] = 0.f;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
 #pragma unroll
@@ -474,7 +451,7 @@ void bsa_attn_kernel(AttnParams p) {
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
             const bf16_t* Vc = BUF ? Vs1 : Vs0;
             begin_tile(bufc, t);
-            s_tile<false>(Kc, ro, qf, m, s, hh);
+            s_tile(Kc, ro, qf, s);
             float mt[2];
             bool need = false;
 #pragma unroll
@@ -608,7 +585,7 @@ void bsa_attn_kernel(AttnParams p) {
         // running-reference path: the first tile's exact row max is the reference
         auto first_body = [&](auto bufc) __attribute__((always_inline)) {
             constexpr int BUF = decltype(bufc)::value;
-            s_tile<false>(BUF ? Ks1 : Ks0, ro, qf, m, s, hh);
+            s_tile(BUF ? Ks1 : Ks0, ro, qf, s);
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) m[qt] = tile_max(s, qt);
             float lt[2];
@@ -620,7 +597,7 @@ void bsa_attn_kernel(AttnParams p) {
         auto sel_body = [&](auto bufc) __attribute__((always_inline)) {
             constexpr int BUF = decltype(bufc)::value;
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
-            s_tile<false>(Kc, ro, qf, m, s, hh);
+            s_tile(Kc, ro, qf, s);
             float lt[2];
             exp_pack<false, true>(s, m, 1.f, pb, lt);
             if (__builtin_amdgcn_ballot_w64(!(lt[0] <= kSumLimit && lt[1] <= kSumLimit))) {
@@ -629,7 +606,7 @@ void bsa_attn_kernel(AttnParams p) {
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) {
                     f32x16 sh[2];
-                    s_half<false>(Kc, ro, qf[qt], m[qt], sh, hh);
+                    s_half(Kc, ro, qf[qt], sh);
                     const float mx = half_max(sh);
                     const float mnew = mx > m[qt] ? mx : m[qt];
                     const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);
