@@ -459,11 +459,14 @@ void bsa_attn_kernel(AttnParams p) {
                 mt[qt] = tile_max(s, qt) * p.scale_log2;
                 need |= mt[qt] > m[qt] + kTau;
             }
-            if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform; rare after a row's first tile
+            if (t == 0) {  // first tile: O and l are still zero, the reference is the tile max
+                m[0] = mt[0];
+                m[1] = mt[1];
+            } else if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform; rare after the first tile
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) {
                     const float mnew = mt[qt] > m[qt] + kTau ? mt[qt] : m[qt];
-                    const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);  // 0 on a row's first tile
+                    const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);
                     l[qt] *= alpha;
 #pragma unroll
                     for (int dt = 0; dt < 2; ++dt) o[dt][qt] *= alpha;
@@ -561,8 +564,8 @@ void bsa_attn_kernel(AttnParams p) {
                     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
                     for (int mm = 0; mm < 4; ++mm) {
-                        qn2[qt] = fmaf(bf_lo(w[mm]), bf_lo(w[mm]), qn2[qt]);
-                        qn2[qt] = fmaf(bf_hi(w[mm]), bf_hi(w[mm]), qn2[qt]);
+                        const bf16x2 h = __builtin_bit_cast(bf16x2, w[mm]);
+                        qn2[qt] = __builtin_amdgcn_fdot2_f32_bf16(h, h, qn2[qt], false);
                     }
                 }
                 qn2[qt] += __shfl_xor(qn2[qt], 32);
