@@ -31,6 +31,14 @@ COMMON_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-source flags.  cmp.hip: keep MFMA accumulators in VGPRs; by default the compiler puts
+# them in AGPRs there and copies the softmax operands back and forth every tile (48
+# v_accvgpr_read per tile).  The attention kernel keeps its default (the flag costs it
+# occupancy in its two-wave instantiations).
+FILE_FLAGS = {
+    "cmp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def hipcc() -> str:
     for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -45,7 +53,7 @@ def sources() -> list[str]:
 
 def _compile(src: str, extra: list[str]) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *extra, "-c", src, "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), *extra, "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

@@ -56,7 +56,7 @@ int choose_splits(int B, int nb, int Hk) {
 
 struct Layout {
     int nb = 0, nb_pad = 0, nsplit = 1;
-    size_t qc = 0, kc = 0, vct = 0, sbar = 0, idx = 0, kbnd = 0, opart = 0, ml = 0, ocmp = 0, total = 0;
+    size_t qc = 0, kfr = 0, vfr = 0, sbar = 0, idx = 0, kbnd = 0, opart = 0, ml = 0, ocmp = 0, total = 0;
 };
 
 bool uses_selection(int mode) { return mode == MOSAIC_BSA_FULL || mode == MOSAIC_BSA_NO_COMPRESSION; }
@@ -100,9 +100,9 @@ Layout layout_of(const mosaic_bsa_args* a) {
     const size_t nb = L.nb, nbp = L.nb_pad, K = a->sparse_block_count, U = L.nsplit;
     size_t off = 0;
     L.qc = off; off = align_up(off + B * nb * Hq * kHeadDim * 2);
-    L.kc = off; off = align_up(off + B * nb * Hk * kHeadDim * 2);
+    L.kfr = off; off = align_up(off + B * Hk * nbp * kHeadDim * 2);
     if (uses_compression(a->mode)) {
-        L.vct = off; off = align_up(off + B * Hk * kHeadDim * nbp * 2);
+        L.vfr = off; off = align_up(off + B * Hk * nbp * kHeadDim * 2);
         L.opart = off; off = align_up(off + B * U * nb * Hq * kHeadDim * 4);
         L.ml = off; off = align_up(off + B * U * nb * Hq * 8);
         L.ocmp = off; off = align_up(off + B * nb * Hq * kHeadDim * 2);
@@ -165,16 +165,15 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
     if (int e = record(events, 0, s)) return e;
     if (a->mode != MOSAIC_BSA_LOCAL_ONLY) {
         const bf16_t* qc = reinterpret_cast<const bf16_t*>(w + L.qc);
-        const bf16_t* kc = reinterpret_cast<const bf16_t*>(w + L.kc);
 
         PoolParams pp{};
         pp.x[0] = ap.q; pp.sb[0] = ap.q_sb; pp.sn[0] = ap.q_sn; pp.sh[0] = ap.q_sh; pp.heads[0] = Hq;
         pp.x[1] = ap.k; pp.sb[1] = ap.k_sb; pp.sn[1] = ap.k_sn; pp.sh[1] = ap.k_sh; pp.heads[1] = Hk;
         pp.out_bnhd[0] = reinterpret_cast<bf16_t*>(w + L.qc);
-        pp.out_bnhd[1] = reinterpret_cast<bf16_t*>(w + L.kc);
+        pp.kfrag = reinterpret_cast<bf16_t*>(w + L.kfr);
         if (cmp) {
             pp.x[2] = ap.v; pp.sb[2] = ap.v_sb; pp.sn[2] = ap.v_sn; pp.sh[2] = ap.v_sh; pp.heads[2] = Hk;
-            pp.out_t = reinterpret_cast<bf16_t*>(w + L.vct);
+            pp.vfrag = reinterpret_cast<bf16_t*>(w + L.vfr);
         }
         pp.B = B; pp.nb = L.nb; pp.nb_pad = L.nb_pad; pp.bs = a->sparse_block_size;
         if (sel) pp.kbnd = reinterpret_cast<float*>(w + L.kbnd);
@@ -183,8 +182,8 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
 
         CmpParams cp{};
         cp.qc = qc; cp.q_sb = (int64_t)L.nb * Hq * kHeadDim; cp.q_sn = (int64_t)Hq * kHeadDim; cp.q_sh = kHeadDim;
-        cp.kc = kc; cp.k_sb = (int64_t)L.nb * Hk * kHeadDim; cp.k_sn = (int64_t)Hk * kHeadDim; cp.k_sh = kHeadDim;
-        cp.vct = cmp ? reinterpret_cast<const bf16_t*>(w + L.vct) : nullptr;
+        cp.kfr = reinterpret_cast<const bf16_t*>(w + L.kfr);
+        cp.vfr = cmp ? reinterpret_cast<const bf16_t*>(w + L.vfr) : nullptr;
         cp.sbar = sel ? reinterpret_cast<bf16_t*>(w + L.sbar) : nullptr;
         cp.opart = cmp ? reinterpret_cast<float*>(w + L.opart) : nullptr;
         cp.ml = cmp ? reinterpret_cast<float2*>(w + L.ml) : nullptr;
@@ -301,10 +300,16 @@ int mosaic_pool_mean_fwd(mosaic_bnhd x, int32_t batch, int32_t seq_len, int32_t 
     return launch_status(launch_pool(pp, static_cast<hipStream_t>(stream)));
 }
 
+// scores [B, Hk, nb, nb_pad] bf16, then k_cmp in operand order [B, Hk, nb_pad, 64] bf16
+size_t topk_scores_bytes(size_t batch, size_t num_blocks, size_t num_kv_heads) {
+    const size_t nbp = (num_blocks + 31) / 32 * 32;
+    return align_up(batch * num_kv_heads * num_blocks * nbp * 2);
+}
+
 size_t mosaic_attn_topk_workspace_size(int32_t batch, int32_t num_blocks, int32_t num_kv_heads) {
     if (batch <= 0 || num_blocks <= 0 || num_kv_heads <= 0) return 0;
     const size_t nbp = (size_t)(num_blocks + 31) / 32 * 32;
-    return align_up((size_t)batch * num_kv_heads * num_blocks * nbp * 2);
+    return topk_scores_bytes(batch, num_blocks, num_kv_heads) + align_up((size_t)batch * num_kv_heads * nbp * kHeadDim * 2);
 }
 
 int mosaic_attn_topk_fwd(mosaic_bnhd q_cmp, mosaic_bnhd k_cmp, int32_t batch, int32_t num_blocks,
@@ -323,9 +328,17 @@ int mosaic_attn_topk_fwd(mosaic_bnhd q_cmp, mosaic_bnhd k_cmp, int32_t batch, in
         return MOSAIC_ERR_WORKSPACE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int nb_pad = (num_blocks + 31) / 32 * 32;
+    // k_cmp into operand order: the pooling kernel with blocks of one token (an exact copy)
+    bf16_t* kfr = reinterpret_cast<bf16_t*>(static_cast<char*>(workspace) + topk_scores_bytes(batch, num_blocks, num_kv_heads));
+    PoolParams pp{};
+    pp.x[1] = static_cast<const bf16_t*>(k_cmp.ptr);
+    pp.sb[1] = k_cmp.stride_b; pp.sn[1] = k_cmp.stride_n; pp.sh[1] = k_cmp.stride_h; pp.heads[1] = num_kv_heads;
+    pp.kfrag = kfr;
+    pp.B = batch; pp.nb = num_blocks; pp.nb_pad = nb_pad; pp.bs = 1;
+    if (int e = launch_status(launch_pool(pp, s))) return e;
     CmpParams cp{};
     cp.qc = static_cast<const bf16_t*>(q_cmp.ptr); cp.q_sb = q_cmp.stride_b; cp.q_sn = q_cmp.stride_n; cp.q_sh = q_cmp.stride_h;
-    cp.kc = static_cast<const bf16_t*>(k_cmp.ptr); cp.k_sb = k_cmp.stride_b; cp.k_sn = k_cmp.stride_n; cp.k_sh = k_cmp.stride_h;
+    cp.kfr = kfr;
     cp.sbar = static_cast<bf16_t*>(workspace);
     cp.B = batch; cp.nb = num_blocks; cp.nb_pad = nb_pad; cp.Hq = num_q_heads; cp.Hk = num_kv_heads;
     cp.G = num_q_heads / num_kv_heads;

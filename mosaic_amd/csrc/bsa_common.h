@@ -50,6 +50,21 @@ __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const 
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Pooled K and V in MFMA-operand order for the compressed-attention kernel: per 32-block
+// tile ut, every operand fragment is a contiguous 1 KB run (lane l's 16 bytes at 16*l), so a
+// wave reads it with one coalesced 16-byte load per lane.  H heads, UT = nb_pad / 32 tiles.
+//   K (A of S^T = K Q^T):  [B][H][UT][ds 4][lane 64][8]; lane 32*hh + r holds
+//                          k[32*ut + r][16*ds + 8*hh .. +7]
+//   V (A of O^T = V^T P^T): [B][H][UT][dt 2][s2 2][lane 64][8]; lane 32*hh + r holds
+//                          v[32*ut + 16*s2 + 4*hh + i][32*dt + r] (i = 0..3), then the same
+//                          for blocks + 8
+__host__ __device__ __forceinline__ int64_t kfrag_index(int b, int h, int H, int UT, int ut, int ds, int lane) {
+    return ((((int64_t)b * H + h) * UT + ut) * 4 + ds) * 512 + lane * 8;
+}
+__host__ __device__ __forceinline__ int64_t vfrag_index(int b, int h, int H, int UT, int ut, int dt, int s2, int lane) {
+    return (((((int64_t)b * H + h) * UT + ut) * 2 + dt) * 2 + s2) * 512 + lane * 8;
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
@@ -76,7 +91,10 @@ struct PoolParams {
     int64_t sb[3], sn[3], sh[3];
     int heads[3];
     bf16_t* out_bnhd[3];       // [B, nb, H, 64] outputs (null: not written)
-    bf16_t* out_t;             // optional transposed output of tensor 2: [B, H, 64, nb_pad]
+    // Optional MFMA-operand-ordered outputs for the compressed-attention kernel, zero past nb
+    // (layouts at kfrag_index / vfrag_index):
+    bf16_t* kfrag;             // tensor 1 as the A operand of S^T = K Q^T
+    bf16_t* vfrag;             // tensor 2 as the A operand of O^T = V^T P^T
     float* kbnd;               // optional [B, nb, H1, 8]: per 8-dim chunk of tensor 1, the block's
                                // largest squared chunk norm (their sum bounds |k|^2 in the block)
     int B, nb, nb_pad, bs;
@@ -84,8 +102,8 @@ struct PoolParams {
 
 struct CmpParams {
     const bf16_t* qc; int64_t q_sb, q_sn, q_sh;   // pooled queries [B, nb, Hq, 64]
-    const bf16_t* kc; int64_t k_sb, k_sn, k_sh;   // pooled keys    [B, nb, Hk, 64]
-    const bf16_t* vct;                             // pooled values, transposed [B, Hk, 64, nb_pad]
+    const bf16_t* kfr;                             // pooled keys, operand order (kfrag_index)
+    const bf16_t* vfr;                             // pooled values, operand order (vfrag_index)
     bf16_t* sbar;                                  // selection scores [B, Hk, nb, nb_pad]
     float* opart;                                  // [B, U, nb, Hq, 64] unnormalised O
     float2* ml;                                    // [B, U, nb, Hq] (running max, sum), log2 units

@@ -18,9 +18,12 @@
 //
 // The loop over key-block tiles is latency-bound (little arithmetic per tile): the K and
 // V^T fragments of the next tile are loaded into registers while the current one is
-// computed (two register sets, unrolled by two).  All loads are unconditional (rows past the last block are clamped and their
-// results masked or never read), so the compiler's wait counts stay exact and a wait for
-// the prefetched fragments never waits for the score stores issued after them.
+// computed (two register sets, unrolled by two).  The pooling kernel writes K and V in MFMA
+// operand order (kfrag_index / vfrag_index), so each fragment is one coalesced 16-byte load
+// per lane; gathering them from row-major K and transposed V (32 rows per instruction) made
+// this kernel memory-pipeline bound (27.5 us against 15.7 us at Nside 64).  All loads are
+// unconditional, so the compiler's wait counts stay exact and a wait for the prefetched
+// fragments never waits for the score stores issued after them.
 #include "bsa_common.h"
 
 namespace mosaic {
@@ -34,20 +37,20 @@ struct CmpFrags {
     uint2 v[2][2][2];  // A operand of O^T += V^T P^T: [dt][s2][lo/hi]
 };
 
+// One 32-block tile's fragments: contiguous 1 KB runs of the operand-ordered pooled K / V
+// (blocks past nb are zero there; their scores are masked or never stored).
 template <bool ATTN>
-__device__ __forceinline__ void load_frags(CmpFrags& f, const CmpParams& p, const bf16_t* kp0, const bf16_t* vtp,
-                                           int u0, int r, int hh) {
-    const int urow = min(u0 + r, p.nb - 1);  // rows past the last block: clamped, masked later
+__device__ __forceinline__ void load_frags(CmpFrags& f, const CmpParams& p, int b, int c, int ut, int lane) {
 #pragma unroll
-    for (int ds = 0; ds < 4; ++ds) f.k[ds] = ld16(kp0 + (int64_t)urow * p.k_sn + 16 * ds);
+    for (int ds = 0; ds < 4; ++ds) f.k[ds] = ld16(p.kfr + kfrag_index(b, c, p.Hk, p.ut_total, ut, ds, lane));
     if constexpr (ATTN) {
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2) {
-                const bf16_t* vp = vtp + (int64_t)(32 * dt + r) * p.nb_pad + u0 + 16 * s2 + 4 * hh;
-                f.v[dt][s2][0] = ld8(vp);
-                f.v[dt][s2][1] = ld8(vp + 8);
+                const uint4 w = ld16(p.vfr + vfrag_index(b, c, p.Hk, p.ut_total, ut, dt, s2, lane));
+                f.v[dt][s2][0] = make_uint2(w.x, w.y);
+                f.v[dt][s2][1] = make_uint2(w.z, w.w);
             }
     }
 }
@@ -128,8 +131,6 @@ void cmp_kernel(CmpParams p) {
 #pragma unroll
         for (int ds = 0; ds < 4; ++ds) qf[ds] = as_bf16x8(ld16(qp + 16 * ds));
     }
-    const bf16_t* kp0 = p.kc + b * p.k_sb + (int64_t)c * p.k_sh + 8 * hh;
-    const bf16_t* vtp = ATTN ? p.vct + ((int64_t)(b * p.Hk + c) * kHeadDim) * p.nb_pad : nullptr;
     bf16_t* srow0 = SCORES ? p.sbar + ((int64_t)(b * p.Hk + h) * p.nb + t0) * p.nb_pad : nullptr;
 
     f32x16 o[2];
@@ -207,12 +208,12 @@ void cmp_kernel(CmpParams p) {
     // the last one again, never used), so every wait targets exactly the set about to be used.
     if (ut0 < ut1) {
         CmpFrags f0, f1;
-        load_frags<ATTN>(f0, p, kp0, vtp, ut0 * 32, r, hh);
+        load_frags<ATTN>(f0, p, b, c, ut0, lane);
         for (int ut = ut0;; ut += 2) {
-            load_frags<ATTN>(f1, p, kp0, vtp, min(ut + 1, ut1 - 1) * 32, r, hh);
+            load_frags<ATTN>(f1, p, b, c, min(ut + 1, ut1 - 1), lane);
             step(f0, ut);
             if (ut + 1 >= ut1) break;
-            load_frags<ATTN>(f0, p, kp0, vtp, min(ut + 2, ut1 - 1) * 32, r, hh);
+            load_frags<ATTN>(f0, p, b, c, min(ut + 2, ut1 - 1), lane);
             step(f1, ut + 1);
             if (ut + 2 >= ut1) break;
         }

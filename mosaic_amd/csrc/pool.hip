@@ -4,8 +4,9 @@
 // sum over the block's tokens in token order, divided by the block size, rounded to bf16.
 // One workgroup per (pooled block t, batch b) reads the block's q, k and v rows once
 // (HBM-bound: each thread streams one 16-byte column chunk down the block's tokens).
-// Outputs: [B, nb, H, 64] for the pooled tensors and, for v, the transposed layout
-// [B, Hk, 64, nb_pad] (zero beyond nb) read by the compressed-attention PV product.
+// Outputs: [B, nb, H, 64] for the pooled tensors and, for k and v, the MFMA-operand-ordered
+// layouts read by the compressed-attention kernel (kfrag_index / vfrag_index; zero for the
+// padding blocks nb .. nb_pad-1).
 // Optionally, for the keys (tensor 1), the largest squared norm of each 8-dim chunk over the
 // block's tokens: the sum of a head's 8 values bounds |k|^2 for every key of the block, which
 // the attention kernel uses to bound its logits.
@@ -22,12 +23,29 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
         const int which = col < c0 ? 0 : (col < c0 + c1 ? 1 : 2);
         const int cc = col - (which == 0 ? 0 : (which == 1 ? c0 : c0 + c1));
         const int hd = cc >> 3, ch = cc & 7;
-        bf16_t* out_t = (which == 2) ? p.out_t : nullptr;
-        if (t >= p.nb) {  // padding columns of the transposed output
-            if (out_t) {
+        bf16_t* frag = which == 1 ? p.kfrag : (which == 2 ? p.vfrag : nullptr);
+        // operand-ordered output of this thread's 8 dims of block t (zero past nb)
+        auto store_frag = [&](const float (&x)[8]) {
+            const int UT = p.nb_pad >> 5, ut = t >> 5, w = t & 31;
+            if (which == 1) {
+                uint4 u;
+                u.x = pack_bf16x2(x[0], x[1]); u.y = pack_bf16x2(x[2], x[3]);
+                u.z = pack_bf16x2(x[4], x[5]); u.w = pack_bf16x2(x[6], x[7]);
+                *reinterpret_cast<uint4*>(frag + kfrag_index(b, hd, p.heads[1], UT, ut, ch >> 1, 32 * (ch & 1) + w)) = u;
+            } else {
+                const int s2 = w >> 4, rem = w & 15, slot = 4 * (rem >> 3) + (rem & 3), hh = (rem & 7) >> 2;
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    out_t[((int64_t)(b * p.heads[2] + hd) * kHeadDim + ch * 8 + e) * p.nb_pad + t] = 0;
+                for (int e = 0; e < 8; ++e) {
+                    const int d = 8 * ch + e;
+                    frag[vfrag_index(b, hd, p.heads[2], UT, ut, d >> 5, s2, 32 * hh + (d & 31)) + slot] =
+                        (bf16_t)(pack_bf16x2(x[e], 0.f) & 0xffffu);
+                }
+            }
+        };
+        if (t >= p.nb) {  // padding blocks of the operand-ordered outputs
+            if (frag) {
+                const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                store_frag(zero);
             }
             continue;
         }
@@ -37,23 +55,26 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
         float sqmax = 0.f;  // largest squared norm of this 8-dim chunk over the block's tokens
-        for (int n = 0; n < p.bs; n += 8) {
+        auto add_token = [&](const uint4& v) __attribute__((always_inline)) {
+            const float x[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y),
+                                bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
+            float sq = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                acc[e] += x[e];
+                sq = fmaf(x[e], x[e], sq);
+            }
+            sqmax = fmaxf(sqmax, sq);
+        };
+        int n = 0;
+        for (; n + 8 <= p.bs; n += 8) {  // eight tokens' loads in flight, summed in token order
             uint4 v[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) v[u] = ld16(src + (int64_t)(n + u) * sn);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float x[8] = {bf_lo(v[u].x), bf_hi(v[u].x), bf_lo(v[u].y), bf_hi(v[u].y),
-                                    bf_lo(v[u].z), bf_hi(v[u].z), bf_lo(v[u].w), bf_hi(v[u].w)};
-                float sq = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    acc[e] += x[e];
-                    sq = fmaf(x[e], x[e], sq);
-                }
-                sqmax = fmaxf(sqmax, sq);
-            }
+            for (int u = 0; u < 8; ++u) add_token(v[u]);
         }
+        for (; n < p.bs; ++n) add_token(ld16(src + (int64_t)n * sn));
         if (which == 1 && p.kbnd != nullptr)
             p.kbnd[(((int64_t)b * p.nb + t) * p.heads[1] + hd) * 8 + ch] = sqmax;
         const float denom = (float)p.bs;
@@ -69,12 +90,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
             w.w = pack_bf16x2(mean[6], mean[7]);
             *reinterpret_cast<uint4*>(out + (((int64_t)b * p.nb + t) * p.heads[which] + hd) * kHeadDim + ch * 8) = w;
         }
-        if (out_t) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                out_t[((int64_t)(b * p.heads[2] + hd) * kHeadDim + ch * 8 + e) * p.nb_pad + t] =
-                    (bf16_t)(pack_bf16x2(mean[e], 0.f) & 0xffffu);
-        }
+        if (frag) store_frag(mean);
     }
 }
 
@@ -82,7 +98,7 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
 
 hipError_t launch_pool(const PoolParams& p, hipStream_t s) {
     void* args[] = {const_cast<PoolParams*>(&p)};
-    const int tgrid = p.out_t ? p.nb_pad : p.nb;
+    const int tgrid = (p.kfrag || p.vfrag) ? p.nb_pad : p.nb;
     return hipLaunchKernel((const void*)pool_kernel, dim3(tgrid, p.B), dim3(256), args, 0, s);
 }
 

@@ -106,4 +106,6 @@ def test_other_entry_points_validate():
     assert L.mosaic_attn_topk_fwd(t, t, 1, 48, 4, 1, 64, 49, FAKE, FAKE, 1 << 20, None) == 5
     assert L.mosaic_attn_topk_fwd(t, t, 1, 48, 4, 1, 64, 4, FAKE, FAKE, 16, None) == 6
     assert L.mosaic_attn_topk_fwd(t, t, 1, 9000, 4, 1, 64, 4, FAKE, FAKE, 1 << 30, None) == 11
-    assert L.mosaic_attn_topk_workspace_size(1, 48, 5) == ((5 * 48 * 64 * 2 + 255) // 256) * 256
+    # scores [1, 5, 48, 64] bf16, then k_cmp in operand order [1, 5, 64 (padded blocks), 64] bf16
+    align = lambda n: (n + 255) // 256 * 256
+    assert L.mosaic_attn_topk_workspace_size(1, 48, 5) == align(5 * 48 * 64 * 2) + align(5 * 64 * 64 * 2)
