@@ -745,7 +745,7 @@ void bsa_attn_kernel(AttnParams p) {
                     oc[dt][4 * g4 + 3] = bf_hi(ocw[dt][g4].y);
                 }
         }
-        const bf16_t* pp = Part + wave * 64 * PS;
+        bf16_t* pp = Part + wave * 64 * PS;
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
@@ -769,8 +769,27 @@ void bsa_attn_kernel(AttnParams p) {
                     uint2 w2;
                     w2.x = pack_bf16x2(v[0], v[1]);
                     w2.y = pack_bf16x2(v[2], v[3]);
-                    *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                    if constexpr (kPartial)  // back into this lane's own Part slot, stored below
+                        *reinterpret_cast<uint2*>(pp + (32 * qt + r) * PS + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                    else
+                        *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
                 }
+        if constexpr (kPartial) {
+            // Row-major read-back: lane l stores 16 bytes at chunk l % 8 of row l / 8 (+ 8 i),
+            // 8 full 128-byte rows per store instead of 16-byte pieces of 32 rows.  Only this
+            // wave's lanes touch its Part rows; LDS operations of a wave complete in order.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int rr = lane >> 3, cc = (lane & 7) * 8;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int row = 8 * i + rr;
+                const uint2 lo = *reinterpret_cast<const uint2*>(pp + row * PS + cc);
+                const uint2 hi = *reinterpret_cast<const uint2*>(pp + row * PS + cc + 4);
+                *reinterpret_cast<uint4*>(outp + (int64_t)row * p.Hq * kHeadDim + cc) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            }
+        }
     }
 }
 
