@@ -344,11 +344,24 @@ void bsa_attn_kernel(AttnParams p) {
     // branch) the first tile do not depend on the top-k indices: their loads are issued
     // first, so they are in flight while wave 0 stages the indices.
     bf16x8 qf[2][4];
+    if constexpr (kPartial) {
+        // The wave's 64 Q rows go to its (still unused) partial buffer in LDS as full 128-byte
+        // rows, chunks swizzled as the K tiles, and are read into registers after the first
+        // barrier: 8 row-contiguous 1 KB requests instead of 16-byte pieces of 32 rows.
+        bf16_t* qs = Part + wave * 64 * PS;
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt)
+        for (int i = 0; i < 8; ++i) {
+            const int row = 8 * i + (lane >> 3), pos = lane & 7;
+            __builtin_amdgcn_global_load_lds(qb + (int64_t)(n0 + row) * p.q_sn + 8 * (pos ^ ((row >> 1) & 7)),
+                                             (lds_void*)(qs + 8 * i * 64), 16, 0, 0);
+        }
+    } else {
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds)
-            qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds)
+                qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)(n0 + 32 * qt + r) * p.q_sn + 16 * ds + 8 * hh));
+    }
     // Gate weights of the 64 rows: the aligned 4-byte word holding each bf16 gate goes straight
     // to LDS (lane L: row n0 + L), so no register waits on them; gate(s, qt) picks the half.
     auto gate_ptr = [&](int sidx, int row) -> const bf16_t* {
@@ -451,6 +464,16 @@ void bsa_attn_kernel(AttnParams p) {
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
             const bf16_t* Vc = BUF ? Vs1 : Vs0;
             begin_tile(bufc, t);
+            if constexpr (kPartial) {
+                if (t == 0) {  // the Q rows staged in the prologue (same layout as a K tile)
+                    const bf16_t* qs = Part + wave * 64 * PS;
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                        for (int ds = 0; ds < 4; ++ds)
+                            qf[qt][ds] = as_bf16x8(*reinterpret_cast<const uint4*>(qs + 32 * qt * 64 + ro.k[ds]));
+                }
+            }
             s_tile(Kc, ro, qf, s);
             float mt[2];
             bool need = false;
