@@ -281,7 +281,7 @@ __device__ __forceinline__ float tile_max(const f32x16 (&s)[2][2], int qt) {
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][qt][e]);
-    return fmaxf(mx, __shfl_xor(mx, 32));
+    return xor32_max(mx);
 }
 
 __device__ __forceinline__ float half_max(const f32x16 (&s)[2]) {
@@ -290,7 +290,7 @@ __device__ __forceinline__ float half_max(const f32x16 (&s)[2]) {
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[kt][e]);
-    return fmaxf(mx, __shfl_xor(mx, 32));
+    return xor32_max(mx);
 }
 
 using Buf0 = std::integral_constant<int, 0>;
@@ -434,7 +434,7 @@ void bsa_attn_kernel(AttnParams p) {
     // makes every wave's loads visible and guarantees the other buffer (tile t-1) is no
     // longer read; the loads of tile t+1 go there.
     auto begin_tile = [&](auto bufc, int t) {
-        constexpr int BUF = decltype(bufc)::value;
+        const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
         wait_vmem();
         __syncthreads();
         if (t + 1 < total_tiles)
@@ -460,7 +460,7 @@ void bsa_attn_kernel(AttnParams p) {
     // ------------------------------------------------------------------ local branch
     if constexpr (kLocal) {
         auto local_step = [&](auto bufc, int t) {
-            constexpr int BUF = decltype(bufc)::value;
+            const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
             const bf16_t* Vc = BUF ? Vs1 : Vs0;
             begin_tile(bufc, t);
@@ -502,15 +502,22 @@ void bsa_attn_kernel(AttnParams p) {
             l[1] += lt[1];
             pv_tile(Vc, ro, pb, o);
         };
-        int t = 0;
-        for (; t + 1 < tl_count; t += 2) {
-            local_step(Buf0{}, t);
-            local_step(Buf1{}, t + 1);
+        if constexpr (MODE == kModeLocalOnly) {  // the local tiles are the hot loop
+            int t = 0;
+            for (; t + 1 < tl_count; t += 2) {
+                local_step(Buf0{}, t);
+                local_step(Buf1{}, t + 1);
+            }
+            if (t < tl_count) local_step(Buf0{}, t);
+        } else {
+            // one copy of the local step (runtime buffer): the selected loop is the hot one,
+            // and the kernel's code stays small in the instruction cache
+#pragma clang loop unroll(disable)
+            for (int t = 0; t < tl_count; ++t) local_step(t & 1, t);
         }
-        if (t < tl_count) local_step(Buf0{}, t);
         float inv[2];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) inv[qt] = 1.f / (l[qt] + __shfl_xor(l[qt], 32));
+        for (int qt = 0; qt < 2; ++qt) inv[qt] = 1.f / xor32_add(l[qt]);
 
         if constexpr (MODE == kModeLocalOnly || MODE == kModeNoSelection || kPartial) {
             float f[2];
@@ -591,7 +598,7 @@ void bsa_attn_kernel(AttnParams p) {
                         qn2[qt] = __builtin_amdgcn_fdot2_f32_bf16(h, h, qn2[qt], false);
                     }
                 }
-                qn2[qt] += __shfl_xor(qn2[qt], 32);
+                qn2[qt] = xor32_add(qn2[qt]);
             }
         }
         // after the barrier of the first selected tile: every row of this wave bounded?
@@ -603,14 +610,14 @@ void bsa_attn_kernel(AttnParams p) {
                 const float4 c4 = *reinterpret_cast<const float4*>(sel_kbnd + 8 * i + 4);
                 kb2 = fmaxf(kb2, ((a.x + a.y) + (a.z + a.w)) + ((c4.x + c4.y) + (c4.z + c4.w)));
             }
-            kb2 = wave_max(kb2);
+            kb2 = wave_max_nonneg(kb2);
             const float lim = kLogitBound * kLogitBound;
             return !__builtin_amdgcn_ballot_w64(!(qn2[0] * kb2 <= lim && qn2[1] * kb2 <= lim));
         };
 
         // running-reference path: the first tile's exact row max is the reference
         auto first_body = [&](auto bufc) __attribute__((always_inline)) {
-            constexpr int BUF = decltype(bufc)::value;
+            const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
             s_tile(BUF ? Ks1 : Ks0, ro, qf, s);
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) m[qt] = tile_max(s, qt);
@@ -621,7 +628,7 @@ void bsa_attn_kernel(AttnParams p) {
             pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
         };
         auto sel_body = [&](auto bufc) __attribute__((always_inline)) {
-            constexpr int BUF = decltype(bufc)::value;
+            const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
             s_tile(Kc, ro, qf, s);
             float lt[2];
@@ -651,8 +658,7 @@ void bsa_attn_kernel(AttnParams p) {
         int t = tl_count;
         bool fast = false;
         if (t < total_tiles) {  // barrier of the first selected tile, then the path choice
-            if (t & 1) begin_tile(Buf1{}, t);
-            else begin_tile(Buf0{}, t);
+            begin_tile(t & 1, t);
             if constexpr (kFastSel) fast = bounded();
         }
         if (fast) {
@@ -661,14 +667,13 @@ void bsa_attn_kernel(AttnParams p) {
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) lacc[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
             auto fast_body = [&](auto bufc) __attribute__((always_inline)) {
-                constexpr int BUF = decltype(bufc)::value;
+                const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
                 s_tile_seq(BUF ? Ks1 : Ks0, ro, qf, s);
                 exp_pack_raw(s, pb);
                 row_sums(rsel, pb, lacc);
                 pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
             };
-            if (t & 1) fast_body(Buf1{});
-            else fast_body(Buf0{});
+            fast_body(t & 1);
             ++t;
             if ((t & 1) && t < total_tiles) {
                 begin_tile(Buf1{}, t);
@@ -692,23 +697,30 @@ void bsa_attn_kernel(AttnParams p) {
                 m[qt] = 0.f;
             }
         } else if (t < total_tiles) {
-            if (t & 1) first_body(Buf1{});
-            else first_body(Buf0{});
+            first_body(t & 1);
             ++t;
-            if ((t & 1) && t < total_tiles) {
-                begin_tile(Buf1{}, t);
-                sel_body(Buf1{});
-                ++t;
-            }
-            for (; t + 1 < total_tiles; t += 2) {
-                begin_tile(Buf0{}, t);
-                sel_body(Buf0{});
-                begin_tile(Buf1{}, t + 1);
-                sel_body(Buf1{});
-            }
-            if (t < total_tiles) {
-                begin_tile(Buf0{}, t);
-                sel_body(Buf0{});
+            if constexpr (MODE == kModeSelectedOnly) {  // the only path of this mode: unrolled
+                if ((t & 1) && t < total_tiles) {
+                    begin_tile(Buf1{}, t);
+                    sel_body(Buf1{});
+                    ++t;
+                }
+                for (; t + 1 < total_tiles; t += 2) {
+                    begin_tile(Buf0{}, t);
+                    sel_body(Buf0{});
+                    begin_tile(Buf1{}, t + 1);
+                    sel_body(Buf1{});
+                }
+                if (t < total_tiles) {
+                    begin_tile(Buf0{}, t);
+                    sel_body(Buf0{});
+                }
+            } else {  // fallback of the bounded path: one copy, runtime buffers
+#pragma clang loop unroll(disable)
+                for (; t < total_tiles; ++t) {
+                    begin_tile(t & 1, t);
+                    sel_body(t & 1);
+                }
             }
         }
     }
@@ -718,7 +730,7 @@ void bsa_attn_kernel(AttnParams p) {
         float ltot[2], inv[2];
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
-            ltot[qt] = l[qt] + __shfl_xor(l[qt], 32);
+            ltot[qt] = xor32_add(l[qt]);
             inv[qt] = 1.f / ltot[qt];
         }
 #pragma unroll
@@ -744,7 +756,7 @@ void bsa_attn_kernel(AttnParams p) {
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
             const float w0 = gate(0, qt), w1 = gate(1, qt), w2 = gate(2, qt);
-            if constexpr (kSel) fs[qt] = w2 / (l[qt] + __shfl_xor(l[qt], 32));
+            if constexpr (kSel) fs[qt] = w2 / xor32_add(l[qt]);
             fc[qt] = w1;
             nrm[qt] = MODE == kModeNoCompression ? 1.f / (w0 + w2 + 1e-8f)
                     : MODE == kModeNoSelection ? 1.f / (w0 + w1 + 1e-8f) : 1.f;

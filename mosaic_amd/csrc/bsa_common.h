@@ -69,9 +69,33 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& u) { return __builtin_b
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ uint2 ld8(const void* p) { return *reinterpret_cast<const uint2*>(p); }
 
-__device__ __forceinline__ float wave_max(float x) {
-    for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-    return x;
+// x[l] + x[l ^ 32] and max(x[l], x[l ^ 32]) in every lane l: one v_permlane32_swap (lanes
+// l < 32 get x[l] and x[l + 32], lanes l >= 32 get x[l - 32] and x[l]) instead of an LDS
+// permute round trip.  The operations are commutative, so both halves get the same value.
+__device__ __forceinline__ float xor32_add(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Wave-uniform maximum of a non-negative float (or NaN, which wins) held per lane: DPP
+// steps within each 16-lane row, then the four row maxima through scalar registers.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t x) {
+    return max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    uint32_t x = __float_as_uint(v);
+    x = dpp_max_u32<0xb1>(x);   // quad_perm [1,0,3,2]
+    x = dpp_max_u32<0x4e>(x);   // quad_perm [2,3,0,1]
+    x = dpp_max_u32<0x141>(x);  // row_half_mirror
+    x = dpp_max_u32<0x140>(x);  // row_mirror
+    const uint32_t a = __builtin_amdgcn_readlane(x, 0), b = __builtin_amdgcn_readlane(x, 16);
+    const uint32_t c = __builtin_amdgcn_readlane(x, 32), d = __builtin_amdgcn_readlane(x, 48);
+    return __uint_as_float(max(max(a, b), max(c, d)));
 }
 
 // Map a linear workgroup id to a logical tile so that each of the 8 XCDs (which receive

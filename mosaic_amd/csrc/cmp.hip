@@ -169,7 +169,7 @@ void cmp_kernel(CmpParams p) {
             float mx = s[0];
 #pragma unroll
             for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32)) * p.scale_log2;
+            mx = xor32_max(mx) * p.scale_log2;
             // lazy reference: moves only when a tile's max exceeds it by more than kTau (the
             // first tile always moves it), so P <= 2^kTau and O is rarely rescaled
             if (__builtin_amdgcn_ballot_w64(mx > m + kTau)) {
@@ -220,7 +220,7 @@ void cmp_kernel(CmpParams p) {
     }
 
     if constexpr (ATTN) {
-        const float ltot = l + __shfl_xor(l, 32);
+        const float ltot = xor32_add(l);
         if (tvalid) {
             const int64_t row = (((int64_t)b * p.nsplit + split) * p.nb + t0 + r) * p.Hq + j;
             if (hh == 0) p.ml[row] = make_float2(m, ltot);
