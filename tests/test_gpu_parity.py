@@ -147,6 +147,35 @@ def test_mosaic_attn_func_full_small(wl):
     close(out, ref_out)
 
 
+@pytest.mark.parametrize("Hq,Hk", [(8, 1), (16, 1), (6, 2), (4, 4), (6, 3), (10, 5)],
+                         ids=lambda x: str(x))
+def test_mosaic_attn_func_head_layouts(Hq, Hk):
+    """Query heads per kv head 8 and 16 (several workgroups per kv head), 3 and 1 (one wave
+    per workgroup), 2 (two waves)."""
+    wl = Workload(f"nside8_h{Hq}kv{Hk}_bs64_top4", 8, 1, Hq, Hk, 64, 64, 64, 4, True)
+    q, k, v, w = make_inputs(wl, seed=5)
+    out, idx = _run_full(q, k, v, w, 64, 64, 4)
+    ref_out, parts = O.mosaic_attn_func(q, k, v, w, 64, 64, 4, False, block_indices=idx, return_parts=True)
+    bad, amb, rows = O.selection_band_check(parts["scores"].permute(0, 2, 1, 3), idx, 4)
+    assert bad == 0, f"{bad}/{rows} rows violate the band rule"
+    close(out, ref_out)
+
+
+def test_mosaic_attn_func_many_selected_blocks():
+    """K = 80 selected blocks: more than the bounded path stages key bounds for, so every wave
+    takes the running-reference path; checked on a sample of query blocks."""
+    wl = Workload("nside32_h4kv1_bs64_top80", 32, 1, 4, 1, 64, 64, 64, 80, True)
+    q, k, v, w = make_inputs(wl, seed=6)
+    out, idx = _run_full(q, k, v, w, 64, 64, 80)
+    assert torch.isfinite(out.float()).all()
+    blocks = torch.tensor([0, 57, 128, 191])
+    ref_rows, parts = O.mosaic_attn_func_blocks(q, k, v, w, 64, 64, 80, blocks, block_indices=idx)
+    bad, amb, rows = O.selection_band_check(parts["scores"].permute(0, 2, 1, 3), idx, 80)
+    assert bad == 0, f"{bad}/{rows} rows violate the band rule"
+    got_rows = torch.cat([out[:, i * 64:(i + 1) * 64] for i in blocks.tolist()], dim=1)
+    close(got_rows, ref_rows)
+
+
 def test_mosaic_attn_func_variants():
     wl = BOTTLENECK_NSIDE16
     q, k, v, w = make_inputs(wl, seed=1)
