@@ -17,7 +17,6 @@ namespace {
 constexpr size_t kAlign = 256;
 constexpr int kMaxBlocksTopk = 8192;  // selection rows live in registers: 128 keys per lane
 constexpr int kMaxGroup = 16;         // query heads per kv head (one wave each in cmp_kernel)
-constexpr int kMaxSplits = 4;  // <= kMaxSplitsCombine
 
 size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
 

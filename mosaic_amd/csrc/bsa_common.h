@@ -191,35 +191,38 @@ hipError_t launch_attn(const AttnParams& p, int mode, bool idx64, int waves, hip
 // Maximum number of selected blocks per query block (block indices are staged in LDS).
 constexpr int kMaxSelected = 1024;
 
+// Most compressed-attention splits (partials per row).
+constexpr int kMaxSplits = 4;
+
 // The compressed-branch output at block t of NH heads j0, j0 + jstep, ..., combined over the
 // splits: lane owns dimension d = lane.  exp2 weights are relative to the largest split max.
-// All loads of all heads and splits are issued before any arithmetic (one memory round trip).
-constexpr int kMaxSplitsCombine = 8;
+// All loads of all heads and splits are issued before any arithmetic (one memory round trip);
+// they are unconditional (past nsplit: the last split again, not used), so no branch sits
+// between them.
 template <int NH>
 __device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int nb, int t, int j0, int jstep, int lane) {
     const int64_t stride = (int64_t)nb * c.Hq;
-    float2 mlv[NH][kMaxSplitsCombine];
-    float ov[NH][kMaxSplitsCombine];
+    float2 mlv[NH][kMaxSplits];
+    float ov[NH][kMaxSplits];
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         const int64_t row0 = ((int64_t)b * c.nsplit * nb + t) * c.Hq + j0 + h * jstep;
 #pragma unroll
-        for (int sp = 0; sp < kMaxSplitsCombine; ++sp) {
-            if (sp < c.nsplit) {
-                mlv[h][sp] = c.ml[row0 + sp * stride];
-                ov[h][sp] = c.opart[(row0 + sp * stride) * kHeadDim + lane];
-            }
+        for (int sp = 0; sp < kMaxSplits; ++sp) {
+            const int64_t row = row0 + min(sp, c.nsplit - 1) * stride;
+            mlv[h][sp] = c.ml[row];
+            ov[h][sp] = c.opart[row * kHeadDim + lane];
         }
     }
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         float M = -INFINITY;
 #pragma unroll
-        for (int sp = 0; sp < kMaxSplitsCombine; ++sp)
+        for (int sp = 0; sp < kMaxSplits; ++sp)
             if (sp < c.nsplit) M = fmaxf(M, mlv[h][sp].x);
         float L = 0.f, acc = 0.f;
 #pragma unroll
-        for (int sp = 0; sp < kMaxSplitsCombine; ++sp) {
+        for (int sp = 0; sp < kMaxSplits; ++sp) {
             if (sp < c.nsplit) {
                 const float a = __builtin_amdgcn_exp2f(mlv[h][sp].x - M);
                 L += a * mlv[h][sp].y;
