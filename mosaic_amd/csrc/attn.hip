@@ -44,6 +44,9 @@
 //
 // Two workgroups share a CU (2 waves per SIMD): one wave's softmax VALU work overlaps the
 // other's MFMA work.  The local branch's partial merge (w0 * o_ba) waits in LDS as bf16.
+// In the modes with that partial buffer, the same per-wave region first receives the wave's
+// Q rows (row-contiguous DMA) and finally stages the merged output, so Q loads and O stores
+// move whole 128-byte rows instead of 16-byte pieces of 32 rows.
 //
 // S^T = K Q^T and O^T = V^T P^T are computed so a lane owns one query column (see
 // bsa_common.h).
