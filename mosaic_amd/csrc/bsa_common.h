@@ -192,7 +192,7 @@ hipError_t launch_attn(const AttnParams& p, int mode, bool idx64, int waves, hip
 constexpr int kMaxSelected = 1024;
 
 // Most compressed-attention splits (partials per row).
-constexpr int kMaxSplits = 4;
+constexpr int kMaxSplits = 2;
 
 // The compressed-branch output at block t of NH heads j0, j0 + jstep, ..., combined over the
 // splits: lane owns dimension d = lane.  exp2 weights are relative to the largest split max.
