@@ -74,23 +74,24 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Direct-to-LDS loads of one 64-key tile (K and V rows key0 .. key0+63): NW waves, 8/NW
-// 1 KB runs per wave and tensor.  The per-lane element offsets (key row * stride + swizzled
-// chunk) do not change between tiles and are computed once; a tile only adds key0 * stride.
+// 1 KB runs per wave and tensor.  The per-lane byte offsets (key row * stride + swizzled
+// chunk) do not change between tiles and are computed once as unsigned 32-bit values, so
+// each load is a wave-uniform base (key0 * stride, scalar) plus a lane offset.
 template <int NW>
-__device__ __forceinline__ void dma_init(int* dk, int* dv, int wave_u, int lane, int64_t ksn, int64_t vsn) {
+__device__ __forceinline__ void dma_init(uint32_t* dk, uint32_t* dv, int wave_u, int lane, int64_t ksn, int64_t vsn) {
 #pragma unroll
     for (int i = 0; i < 8 / NW; ++i) {
         const int row = 8 * (wave_u * (8 / NW) + i) + (lane >> 3), pos = lane & 7;
-        dk[i] = (int)(row * ksn) + 8 * (pos ^ ((row >> 1) & 7));  // global chunk stored at position pos
-        dv[i] = (int)(row * vsn) + 8 * (pos ^ ((row & 3) << 1));
+        dk[i] = 2u * (uint32_t)(row * ksn + 8 * (pos ^ ((row >> 1) & 7)));  // global chunk at position pos
+        dv[i] = 2u * (uint32_t)(row * vsn + 8 * (pos ^ ((row & 3) << 1)));
     }
 }
 template <int NW>
-__device__ __forceinline__ void dma_issue(const int* dk, const int* dv, const bf16_t* kb, const bf16_t* vb,
+__device__ __forceinline__ void dma_issue(const uint32_t* dk, const uint32_t* dv, const bf16_t* kb, const bf16_t* vb,
                                           int64_t ksn, int64_t vsn, int key0, bf16_t* Kd, bf16_t* Vd, int wave_u) {
     const int k0 = __builtin_amdgcn_readfirstlane(key0);
-    const bf16_t* kt = kb + (int64_t)k0 * ksn;
-    const bf16_t* vt = vb + (int64_t)k0 * vsn;
+    const char* kt = reinterpret_cast<const char*>(kb + (int64_t)k0 * ksn);
+    const char* vt = reinterpret_cast<const char*>(vb + (int64_t)k0 * vsn);
 #pragma unroll
     for (int i = 0; i < 8 / NW; ++i) {
         const int row0 = 8 * (wave_u * (8 / NW) + i);
@@ -386,7 +387,7 @@ void bsa_attn_kernel(AttnParams p) {
         const bf16_t* ocp = p.ocmp + (((int64_t)b * p.nb + n0 / p.bs) * p.Hq + j) * kHeadDim;
         if (lane < 32) __builtin_amdgcn_global_load_lds(ocp + 2 * lane, (lds_void*)(Ocmp + wave * 64), 4, 0, 0);
     }
-    int dk[8 / NW], dv[8 / NW];
+    uint32_t dk[8 / NW], dv[8 / NW];
     dma_init<NW>(dk, dv, wave, lane, p.k_sn, p.v_sn);
     if constexpr (kLocal) dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, lstart, Ks0, Vs0, wave);
 
@@ -414,9 +415,13 @@ void bsa_attn_kernel(AttnParams p) {
     // first key of tile t >= 1 (tile 0 of a local branch is issued above); tiles are
     // requested in order
     int cur_k = 0, cur_s = 0;
+    // up to 64 selected blocks: every wave keeps their first keys in a register (lane i,
+    // block i), so a tile address is a readlane instead of an LDS round trip
+    const int selv = (kSel && lane < nvalid) ? sel_key0[lane] : 0;
     auto next_key0 = [&](int t) -> int {
         if (kLocal && t < tl_count) return lstart + kTile * t;
-        const int key0 = sel_key0[cur_k] + cur_s * kTile;
+        const int base = nvalid <= 64 ? __builtin_amdgcn_readlane(selv, cur_k) : sel_key0[cur_k];
+        const int key0 = base + cur_s * kTile;
         if (++cur_s == sub) {
             cur_s = 0;
             ++cur_k;
