@@ -11,8 +11,9 @@ W warm-up steps, then K timed steps bracketed by device synchronisation; per-ker
 come from HIP events recorded between the kernels of every timed step, on the launch stream.
 
 Prints one JSON line.  Options: --gpus (only 1 is supported: the op runs on one GPU),
---steps, --warmup, --workload {nside64, nside32_b24, nside16, nside128}, --no-cpu-baseline,
---calibration-copy-mb.
+--steps, --warmup, --workload {nside64, nside32_b24, nside16, nside32_sweep, nside64_sweep,
+nside128}, --no-cpu-baseline, --calibration-copy-mb, --dense-baseline (also times full
+attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v).
 """
 
 from __future__ import annotations
@@ -42,6 +43,8 @@ WORKLOADS = {
     "nside64": STAGE1_NSIDE64,
     "nside32_b24": STAGE2_NSIDE32_B24,
     "nside16": BOTTLENECK_NSIDE16,
+    "nside32_sweep": scaling_workload(32),
+    "nside64_sweep": scaling_workload(64),
     "nside128": scaling_workload(128),
 }
 KERNELS = ("pool", "cmp_scores", "topk", "attn")
@@ -83,6 +86,33 @@ def profiled_traffic(workload_name):
     return None
 
 
+def dense_baseline(L, q, k, v, out, wl, args, stream):
+    """Full attention over the whole sequence (flash_attn_func defaults) on the same q/k/v,
+    through mosaic_dense_attn_fwd: the dense baseline the sparse op replaces."""
+    B, N, Hq, d = q.shape
+    sp = stream.cuda_stream
+
+    def run():
+        st = L.mosaic_dense_attn_fwd(bnhd(q), bnhd(k), bnhd(v), B, N, Hq, k.shape[2], d, 0.0, out.data_ptr(), sp)
+        if st:
+            raise RuntimeError(_lib.strerror(st))
+
+    steps = max(3, min(args.steps, 20))
+    for _ in range(2):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 4 * B * Hq * d * N * N
+    return {"kernel": "dense_attn (mosaic_dense_attn_fwd)", "ms": round(ms, 4), "steps": steps,
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "flops": flops}
+
+
 def cpu_baseline(wl, q, k, v, w):
     """The CPU oracle (torch restatement of the reference path) on the full workload."""
     from oracle import bsa_oracle as O
@@ -122,6 +152,7 @@ def main():
     ap.add_argument("--workload", default="nside64", choices=sorted(WORKLOADS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--dense-baseline", action="store_true")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -249,6 +280,8 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = n
+    if args.dense_baseline:
+        result["dense_baseline"] = dense_baseline(L, q, k, v, out, wl, args, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, q_c, k_c, v_c, w_c)
     print(json.dumps(result))
