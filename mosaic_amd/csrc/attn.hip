@@ -681,22 +681,18 @@ void bsa_attn_kernel(AttnParams p) {
                 row_sums(rsel, pb, lacc);
                 pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
             };
-            fast_body(t & 1);
-            ++t;
-            if ((t & 1) && t < total_tiles) {
+            // the first selected tile has begun; enter the two-buffer loop at its parity
+            if (t & 1) {
+                fast_body(Buf1{});
+                if (++t < total_tiles) begin_tile(Buf0{}, t);
+            }
+            while (t < total_tiles) {
+                fast_body(Buf0{});
+                if (++t >= total_tiles) break;
                 begin_tile(Buf1{}, t);
                 fast_body(Buf1{});
-                ++t;
-            }
-            for (; t + 1 < total_tiles; t += 2) {
+                if (++t >= total_tiles) break;
                 begin_tile(Buf0{}, t);
-                fast_body(Buf0{});
-                begin_tile(Buf1{}, t + 1);
-                fast_body(Buf1{});
-            }
-            if (t < total_tiles) {
-                begin_tile(Buf0{}, t);
-                fast_body(Buf0{});
             }
             // every lane holds its row's whole sum; the epilogue adds the two key halves
 #pragma unroll
