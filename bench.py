@@ -11,8 +11,8 @@ W warm-up steps, then K timed steps bracketed by device synchronisation; per-ker
 come from HIP events recorded between the kernels of every timed step, on the launch stream.
 
 Prints one JSON line.  Options: --gpus (only 1 is supported: the op runs on one GPU),
---steps, --warmup, --workload {nside64, nside32_b24, nside16, nside32_sweep, nside64_sweep,
-nside128}, --no-cpu-baseline, --calibration-copy-mb, --dense-baseline (also times full
+--steps, --warmup, --workload {nside64, nside64_model, nside32_b24, nside16, nside32_sweep,
+nside64_sweep, nside128}, --no-cpu-baseline, --calibration-copy-mb, --dense-baseline (also times full
 attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v).
 """
 
@@ -32,8 +32,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from mosaic_amd import _lib  # noqa: E402
-from mosaic_amd.inputs import (BOTTLENECK_NSIDE16, STAGE1_NSIDE64, STAGE2_NSIDE32_B24,  # noqa: E402
-                               make_inputs, scaling_workload)
+from mosaic_amd.inputs import (BOTTLENECK_NSIDE16, STAGE1_NSIDE64, STAGE1_NSIDE64_MODEL,  # noqa: E402
+                               STAGE2_NSIDE32_B24, make_inputs, scaling_workload)
 from mosaic_amd.ops import bnhd  # noqa: E402
 
 METRIC = "BSA fwd ms/call & MFMA util at Nside=64 (N=49152); 24-member step ms"
@@ -41,6 +41,7 @@ PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 WORKLOADS = {
     "nside64": STAGE1_NSIDE64,
+    "nside64_model": STAGE1_NSIDE64_MODEL,
     "nside32_b24": STAGE2_NSIDE32_B24,
     "nside16": BOTTLENECK_NSIDE16,
     "nside32_sweep": scaling_workload(32),

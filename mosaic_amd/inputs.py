@@ -47,6 +47,9 @@ class Workload:
 BOTTLENECK_NSIDE16 = Workload("bsa_nside16_b1_h20kv5_bs64_top4", 16, 1, 20, 5, 64, 64, 64, 4, False)
 # Stage-1 attention forward: Nside 64 (N = 49152), 12/3 heads, top-16, RoPE.
 STAGE1_NSIDE64 = Workload("bsa_nside64_b1_h12kv3_bs64_top16", 64, 1, 12, 3, 64, 64, 64, 16, True)
+# Stage-1 attention forward with the shipped model's block settings (inference.py:71-88):
+# local blocks of 1024 tokens, selection blocks of 128, top-24.
+STAGE1_NSIDE64_MODEL = Workload("bsa_nside64_b1_h12kv3_bl1024_bs128_top24", 64, 1, 12, 3, 64, 1024, 128, 24, True)
 # Stage-2 attention forward, ensemble-batched: Nside 32, 24 members, 16/4 heads, top-16, RoPE.
 STAGE2_NSIDE32_B24 = Workload("bsa_nside32_b24_h16kv4_bs64_top16", 32, 24, 16, 4, 64, 64, 64, 16, True)
 
