@@ -98,6 +98,20 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return __uint_as_float(max(max(a, b), max(c, d)));
 }
 
+// Unsigned maximum over the wave, in every lane and without scalar round trips: DPP steps
+// within each 16-lane row, then v_permlane16_swap (rows 0 <-> 1 and 2 <-> 3) and
+// v_permlane32_swap (halves), each followed by a max of the two swapped copies.
+__device__ __forceinline__ uint32_t wave_max_all_u32(uint32_t x) {
+    x = dpp_max_u32<0xb1>(x);   // quad_perm [1,0,3,2]
+    x = dpp_max_u32<0x4e>(x);   // quad_perm [2,3,0,1]
+    x = dpp_max_u32<0x141>(x);  // row_half_mirror
+    x = dpp_max_u32<0x140>(x);  // row_mirror: every lane of a row holds the row max
+    const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = max((uint32_t)a[0], (uint32_t)a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return max((uint32_t)b[0], (uint32_t)b[1]);
+}
+
 // Map a linear workgroup id to a logical tile so that each of the 8 XCDs (which receive
 // workgroups round-robin) works on one contiguous range of logical tiles and keeps that
 // range's K/V blocks in its own L2.

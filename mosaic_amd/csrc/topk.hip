@@ -8,7 +8,8 @@
 // order of exactly tied scores is unspecified there).
 //
 // The wave max runs on DPP within each 16-lane row (quad swaps, half-row and row mirrors),
-// then reads the four row maxima into scalar registers; no LDS round trips.
+// then across rows with the two lane-swap permutes, leaving the maximum in every lane: no
+// LDS or scalar round trips inside a selection round.
 #include "bsa_common.h"
 
 namespace mosaic {
@@ -16,22 +17,6 @@ namespace {
 
 __device__ __forceinline__ uint32_t order16(uint32_t bits) {
     return (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u);
-}
-
-template <int CTRL>
-__device__ __forceinline__ uint32_t dpp_max(uint32_t x) {
-    return max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false));
-}
-
-// Maximum over the wave, returned as a wave-uniform value.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-    x = dpp_max<0xb1>(x);   // quad_perm [1,0,3,2]
-    x = dpp_max<0x4e>(x);   // quad_perm [2,3,0,1]
-    x = dpp_max<0x141>(x);  // row_half_mirror
-    x = dpp_max<0x140>(x);  // row_mirror: every lane of a 16-lane row holds the row max
-    const uint32_t a = __builtin_amdgcn_readlane(x, 0), b = __builtin_amdgcn_readlane(x, 16);
-    const uint32_t c = __builtin_amdgcn_readlane(x, 32), d = __builtin_amdgcn_readlane(x, 48);
-    return max(max(a, b), max(c, d));
 }
 
 // Insert x into the descending list (b0 >= b1 >= b2 >= b3); the smallest falls off.
@@ -83,7 +68,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
 
     int mine = 0;  // lane (kk mod 64) keeps the kk-th index for one coalesced store
     for (int kk = 0; kk < p.K; ++kk) {
-        const uint32_t mx = wave_max_u32(b0);
+        const uint32_t mx = wave_max_all_u32(b0);
         const int u = (int)(0xffffu - (mx & 0xffffu));
         const bool win = b0 == mx;
         if (win) {
