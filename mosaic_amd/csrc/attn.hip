@@ -300,8 +300,18 @@ __device__ __forceinline__ float half_max(const f32x16 (&s)[2]) {
 using Buf0 = std::integral_constant<int, 0>;
 using Buf1 = std::integral_constant<int, 1>;
 
+// Waves per SIMD the kernel is compiled for: 2 where the registers allow it.  The one- and
+// two-wave workgroups of the modes with a selected branch (GQA groups of 1, 2 or an odd
+// size) need more than 256 registers per lane and run one wave per SIMD.
+template <int NW, int MODE>
+constexpr int kWavesPerSimd = (NW == 1 && MODE != kModeLocalOnly) ||
+                                      (NW == 2 && (MODE == kModeFull || MODE == kModeNoCompression))
+                                  ? 1
+                                  : 2;
+
 template <int NW, int MODE, typename IdxT>
-__global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64),
+                          amdgpu_waves_per_eu(kWavesPerSimd<NW, MODE>, kWavesPerSimd<NW, MODE>)))
 void bsa_attn_kernel(AttnParams p) {
     constexpr bool kLocal = MODE != kModeSelectedOnly;
     constexpr bool kSel = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeSelectedOnly;
