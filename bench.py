@@ -13,7 +13,9 @@ come from HIP events recorded between the kernels of every timed step, on the la
 Prints one JSON line.  Options: --gpus (only 1 is supported: the op runs on one GPU),
 --steps, --warmup, --workload {nside64, nside64_model, nside32_b24, nside16, nside32_sweep,
 nside64_sweep, nside128}, --no-cpu-baseline, --calibration-copy-mb, --dense-baseline (also times full
-attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v).
+attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v), --rope-fused (also
+times the op with the input side's RoPE fused into its pooling pass, mosaic_bsa_fwd_rope,
+against eager torch RoPE followed by the op, both on unrotated q/k).
 """
 
 from __future__ import annotations
@@ -114,6 +116,53 @@ def dense_baseline(L, q, k, v, out, wl, args, stream):
             "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "flops": flops}
 
 
+def rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream):
+    """The op with the RoPE of q and k fused into its pooling pass (mosaic_bsa_fwd_rope)
+    against eager torch RoPE (the RoPE module's elementwise ops) followed by the op, on the
+    workload's shapes with unrotated q and k."""
+    from dataclasses import replace
+    from mosaic_amd.healpix import apply_rope, get_healpix_grid, rope_tables
+    dev = v.device
+    q0, k0, _, _ = make_inputs(replace(wl, rope=False), seed=args.seed)
+    q0, k0 = q0.to(dev), k0.to(dev)
+    cos, sin = (t.to(dev) for t in rope_tables(get_healpix_grid(wl.nside), wl.head_dim))
+    q_rot, k_rot = torch.empty_like(q0), torch.empty_like(k0)
+    sp = stream.cuda_stream
+    fa = _lib.BsaArgs.from_buffer_copy(a)
+    fa.q, fa.k = bnhd(q0), bnhd(k0)
+
+    def fused():
+        st = L.mosaic_bsa_fwd_rope(ctypes.byref(fa), cos.data_ptr(), sin.data_ptr(), q_rot.data_ptr(),
+                                   k_rot.data_ptr(), ws_ptr, nbytes, sp)
+        if st:
+            raise RuntimeError(_lib.strerror(st))
+
+    def unfused():
+        qr, kr = apply_rope(q0, cos, sin), apply_rope(k0, cos, sin)
+        ua = _lib.BsaArgs.from_buffer_copy(a)
+        ua.q, ua.k = bnhd(qr), bnhd(kr)
+        st = L.mosaic_bsa_fwd(ctypes.byref(ua), ws_ptr, nbytes, sp)
+        if st:
+            raise RuntimeError(_lib.strerror(st))
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    fused_ms, unfused_ms = timed(fused), timed(unfused)
+    return {"fused_ms": round(fused_ms, 4), "rope_then_op_ms": round(unfused_ms, 4),
+            "saved_ms": round(unfused_ms - fused_ms, 4),
+            "rope": "torch eager on the GPU (fp32 math, bf16 out), then mosaic_bsa_fwd"}
+
+
 def cpu_baseline(wl, q, k, v, w):
     """The CPU oracle (torch restatement of the reference path) on the full workload."""
     from oracle import bsa_oracle as O
@@ -154,6 +203,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dense-baseline", action="store_true")
+    ap.add_argument("--rope-fused", action="store_true")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -283,6 +333,8 @@ def main():
         result["calibration_copy_bytes"] = n
     if args.dense_baseline:
         result["dense_baseline"] = dense_baseline(L, q, k, v, out, wl, args, stream)
+    if args.rope_fused:
+        result["rope_fused"] = rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, q_c, k_c, v_c, w_c)
     print(json.dumps(result))

@@ -99,6 +99,18 @@ MOSAIC_API int mosaic_bsa_fwd(const mosaic_bsa_args* args, void* workspace, size
 MOSAIC_API int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* workspace,
                             size_t workspace_bytes, void* stream, void* const* events);
 
+/* Full forward with the input side's 2-D RoPE fused into the pooling pass: q and k are
+   rotated as the caller's RoPE modules rotate them (primitives.py:125-135, applied at
+   :193-195) and the op (primitives.py:54-89) runs on the rotated tensors.
+   rope_cos, rope_sin: fp32 [seq_len, 32], the reference's cos_freqs / sin_freqs buffers
+   (primitives.py:115-123: 16 longitude then 16 latitude frequencies per position); pair
+   (2m, 2m+1) of every head is rotated by angle m.  q_rot, k_rot: caller-allocated bf16
+   [batch, seq_len, H, 64] contiguous outputs holding the rotated q and k.  Same workspace
+   as mosaic_bsa_fwd. */
+MOSAIC_API int mosaic_bsa_fwd_rope(const mosaic_bsa_args* args, const float* rope_cos, const float* rope_sin,
+                                   void* q_rot, void* k_rot, void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
 /*
  * Selected-branch attention given block indices.  Replaces mosaic_sparse_attn /
  * MosaicAttnFunction.forward / mosaic_attn_fwd (ops.py:557-566, 510-538, 137-176):

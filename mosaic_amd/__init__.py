@@ -2,7 +2,8 @@
 
 Drop-in Python surface of the reference op (primitives.py / ops.py):
 ``mosaic_attn_func``, ``block_attention``, ``attn_topk``, ``mosaic_sparse_attn``,
-``MosaicAttnFunction``, ``RoPE``, ``MosaicAttention``.  All compute runs in libmosaic_bsa.so
+``MosaicAttnFunction``, ``RoPE``, ``MosaicAttention``; ``mosaic_attn_func_rope`` runs the op
+with the input side's RoPE fused into its pooling pass.  All compute runs in libmosaic_bsa.so
 (built with ``python -m mosaic_amd.build``) through its C ABI (include/mosaic_bsa.h).
 """
 
@@ -14,12 +15,13 @@ from .primitives import (
     block_attention,
     dense_attention,
     mosaic_attn_func,
+    mosaic_attn_func_rope,
     pool_mean,
 )
 from .healpix import get_healpix_grid, pix2ang_nest
 
 __all__ = [
     "MosaicAttnFunction", "mosaic_attn_fwd", "mosaic_sparse_attn", "MosaicAttention", "RoPE",
-    "attn_topk", "block_attention", "dense_attention", "mosaic_attn_func", "pool_mean",
+    "attn_topk", "block_attention", "dense_attention", "mosaic_attn_func", "mosaic_attn_func_rope", "pool_mean",
     "get_healpix_grid", "pix2ang_nest",
 ]

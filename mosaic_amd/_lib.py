@@ -24,6 +24,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_bsa_workspace_size",
     "mosaic_bsa_fwd",
     "mosaic_bsa_fwd_profiled",
+    "mosaic_bsa_fwd_rope",
     "mosaic_sparse_attn_fwd",
     "mosaic_block_attn_fwd",
     "mosaic_dense_attn_fwd",
@@ -73,6 +74,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_bsa_fwd.restype = c_int
     lib.mosaic_bsa_fwd_profiled.argtypes = [P(BsaArgs), c_vp, c_size, c_vp, P(c_vp)]
     lib.mosaic_bsa_fwd_profiled.restype = c_int
+    lib.mosaic_bsa_fwd_rope.argtypes = [P(BsaArgs), c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]
+    lib.mosaic_bsa_fwd_rope.restype = c_int
     lib.mosaic_sparse_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
                                            c_i32, c_i32, c_f, c_vp, c_vp, c_vp]
     lib.mosaic_sparse_attn_fwd.restype = c_int

@@ -138,8 +138,23 @@ int record(void* const* events, int i, hipStream_t s) {
     return launch_status(hipEventRecord(static_cast<hipEvent_t>(events[i]), s));
 }
 
-int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* stream, void* const* events) {
+// Inputs of the fused RoPE path: fp32 cos / sin tables [N, 32] and the rotated q, k outputs
+// (bf16 [B, N, H, 64] contiguous).
+struct RopeIO {
+    const float* cos;
+    const float* sin;
+    void* q_rot;
+    void* k_rot;
+};
+
+int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* stream, void* const* events,
+                const RopeIO* rope = nullptr) {
     if (int e = validate(a)) return e;
+    if (rope != nullptr) {
+        if (!rope->cos || !rope->sin || !rope->q_rot || !rope->k_rot) return MOSAIC_ERR_NULL_POINTER;
+        if (!aligned16(rope->cos) || !aligned16(rope->sin) || !aligned16(rope->q_rot) || !aligned16(rope->k_rot))
+            return MOSAIC_ERR_ALIGNMENT;
+    }
     const Layout L = layout_of(a);
     if (L.total > 0) {
         if (ws == nullptr || ws_bytes < L.total) return MOSAIC_ERR_WORKSPACE;
@@ -160,6 +175,20 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
     ap.w = static_cast<const bf16_t*>(a->weights);
     ap.w_ss = a->w_stride_s; ap.w_sb = a->w_stride_b; ap.w_sn = a->w_stride_n; ap.w_sh = a->w_stride_h;
     const int waves = attn_waves(ap.G);
+    // With RoPE, the pooling pass rotates q and k (reading them once) and the later kernels
+    // read the rotated copies.
+    auto set_rope = [&](PoolParams& pp) {
+        pp.rope_cos = rope->cos;
+        pp.rope_sin = rope->sin;
+        pp.rot[0] = static_cast<bf16_t*>(rope->q_rot);
+        pp.rot[1] = static_cast<bf16_t*>(rope->k_rot);
+    };
+    auto use_rotated = [&]() {
+        ap.q = static_cast<const bf16_t*>(rope->q_rot);
+        ap.q_sb = (int64_t)N * Hq * kHeadDim; ap.q_sn = (int64_t)Hq * kHeadDim; ap.q_sh = kHeadDim;
+        ap.k = static_cast<const bf16_t*>(rope->k_rot);
+        ap.k_sb = (int64_t)N * Hk * kHeadDim; ap.k_sn = (int64_t)Hk * kHeadDim; ap.k_sh = kHeadDim;
+    };
 
     if (int e = record(events, 0, s)) return e;
     if (a->mode != MOSAIC_BSA_LOCAL_ONLY) {
@@ -176,7 +205,9 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         }
         pp.B = B; pp.nb = L.nb; pp.nb_pad = L.nb_pad; pp.bs = a->sparse_block_size;
         if (sel) pp.kbnd = reinterpret_cast<float*>(w + L.kbnd);
+        if (rope) set_rope(pp);
         if (int e = launch_status(launch_pool(pp, s))) return e;
+        if (rope) use_rotated();
         if (int e = record(events, 1, s)) return e;
 
         CmpParams cp{};
@@ -213,6 +244,15 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         if (int e = record(events, 3, s)) return e;
         ap.ocmp = cb.ocmp;
     } else {
+        if (rope) {  // local attention only: the pooling pass just rotates q and k
+            PoolParams pp{};
+            pp.x[0] = ap.q; pp.sb[0] = ap.q_sb; pp.sn[0] = ap.q_sn; pp.sh[0] = ap.q_sh; pp.heads[0] = Hq;
+            pp.x[1] = ap.k; pp.sb[1] = ap.k_sb; pp.sn[1] = ap.k_sn; pp.sh[1] = ap.k_sh; pp.heads[1] = Hk;
+            pp.B = B; pp.nb = N / kTile; pp.nb_pad = pp.nb; pp.bs = kTile;
+            set_rope(pp);
+            if (int e = launch_status(launch_pool(pp, s))) return e;
+            use_rotated();
+        }
         if (int e = record(events, 1, s)) return e;
         if (int e = record(events, 2, s)) return e;
         if (int e = record(events, 3, s)) return e;
@@ -238,6 +278,12 @@ int mosaic_bsa_fwd(const mosaic_bsa_args* args, void* workspace, size_t workspac
 int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes, void* stream,
                             void* const* events) {
     return bsa_forward(args, workspace, workspace_bytes, stream, events);
+}
+
+int mosaic_bsa_fwd_rope(const mosaic_bsa_args* args, const float* rope_cos, const float* rope_sin, void* q_rot,
+                        void* k_rot, void* workspace, size_t workspace_bytes, void* stream) {
+    const RopeIO rope{rope_cos, rope_sin, q_rot, k_rot};
+    return bsa_forward(args, workspace, workspace_bytes, stream, nullptr, &rope);
 }
 
 int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const int64_t* block_indices,

@@ -135,6 +135,14 @@ struct PoolParams {
     bf16_t* vfrag;             // tensor 2 as the A operand of O^T = V^T P^T
     float* kbnd;               // optional [B, nb, H1, 8]: per 8-dim chunk of tensor 1, the block's
                                // largest squared chunk norm (their sum bounds |k|^2 in the block)
+    // Optional 2-D RoPE of tensors 0 and 1 before pooling: fp32 cos / sin tables [N, 32]
+    // (one per token and rotated pair), rotated bf16 copies written to rot[0..1]
+    // ([B, N, H, 64] contiguous); the pooled outputs and bounds are then those of the
+    // rotated tensors.
+    const float* rope_cos;
+    const float* rope_sin;
+    bf16_t* rot[2];
+    int rope_lds;              // the block's table rows are staged in dynamic LDS (bs * 256 bytes)
     int B, nb, nb_pad, bs;
 };
 

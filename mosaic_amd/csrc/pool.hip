@@ -10,13 +10,39 @@
 // Optionally, for the keys (tensor 1), the largest squared norm of each 8-dim chunk over the
 // block's tokens: the sum of a head's 8 values bounds |k|^2 for every key of the block, which
 // the attention kernel uses to bound its logits.
+// Optionally, q and k (tensors 0 and 1) are first rotated by the 2-D RoPE of the tokens'
+// positions (primitives.py:125-135: x * cos + rotate_half(x) * sin in fp32, back to bf16):
+// pair m = (2m, 2m+1) of a head becomes (x0 c_m - x1 s_m, x1 c_m + x0 s_m), each product and
+// the sum rounded as the reference rounds them.  The rotated rows are written out (the
+// attention reads them) and pooled, so the rotation costs no extra read of q and k.
 #include "bsa_common.h"
 
 namespace mosaic {
 namespace {
 
+// a*b - c*d and a*b + c*d with both products and the sum rounded separately (no fused
+// multiply-add), as the reference's elementwise tensor ops round them
+__device__ __forceinline__ float mul_sub(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+    return a * b - c * d;
+}
+__device__ __forceinline__ float mul_add(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+    return a * b + c * d;
+}
+
 __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
     const int t = blockIdx.x, b = blockIdx.y;
+    // RoPE tables of the block's tokens, read once per workgroup: [token][8 float4] of cos,
+    // then of sin (every head of a token uses the same row)
+    extern __shared__ float4 rope_rows[];
+    if (p.rope_cos != nullptr && p.rope_lds && t < p.nb) {
+        const float4* c4 = reinterpret_cast<const float4*>(p.rope_cos) + (int64_t)t * p.bs * 8;
+        const float4* s4 = reinterpret_cast<const float4*>(p.rope_sin) + (int64_t)t * p.bs * 8;
+        for (int i = threadIdx.x; i < 16 * p.bs; i += blockDim.x)
+            rope_rows[i] = i < 8 * p.bs ? c4[i] : s4[i - 8 * p.bs];
+        __syncthreads();
+    }
     const int c0 = p.heads[0] * 8, c1 = p.heads[1] * 8, c2 = p.heads[2] * 8;
     const int ctot = c0 + c1 + c2;
     for (int col = threadIdx.x; col < ctot; col += blockDim.x) {
@@ -51,11 +77,34 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
         }
         const int64_t sn = p.sn[which];
         const bf16_t* src = p.x[which] + b * p.sb[which] + (int64_t)t * p.bs * sn + (int64_t)hd * p.sh[which] + ch * 8;
+        // RoPE of this thread's 4 pairs (frequencies 4 ch .. 4 ch + 3) of token n of the block
+        const bool rope = p.rope_cos != nullptr && which < 2;
+        const int64_t tok0 = (int64_t)t * p.bs;
+        bf16_t* rdst = rope ? p.rot[which] + (((int64_t)b * p.nb * p.bs + tok0) * p.heads[which] + hd) * kHeadDim + ch * 8
+                            : nullptr;
+        auto rotate = [&](uint4 v, int n) __attribute__((always_inline)) -> uint4 {
+            const float4 c = p.rope_lds ? rope_rows[n * 8 + ch]
+                                        : *reinterpret_cast<const float4*>(p.rope_cos + (tok0 + n) * 32 + 4 * ch);
+            const float4 s = p.rope_lds ? rope_rows[8 * p.bs + n * 8 + ch]
+                                        : *reinterpret_cast<const float4*>(p.rope_sin + (tok0 + n) * 32 + 4 * ch);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            const float cf[4] = {c.x, c.y, c.z, c.w}, sf[4] = {s.x, s.y, s.z, s.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float x0 = bf_lo(w[i]), x1 = bf_hi(w[i]);
+                o[i] = pack_bf16x2(mul_sub(x0, cf[i], x1, sf[i]), mul_add(x1, cf[i], x0, sf[i]));
+            }
+            const uint4 r = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4*>(rdst + (int64_t)n * p.heads[which] * kHeadDim) = r;
+            return r;
+        };
         float acc[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
         float sqmax = 0.f;  // largest squared norm of this 8-dim chunk over the block's tokens
-        auto add_token = [&](const uint4& v) __attribute__((always_inline)) {
+        auto add_token = [&](uint4 v, int n) __attribute__((always_inline)) {
+            if (rope) v = rotate(v, n);
             const float x[8] = {bf_lo(v.x), bf_hi(v.x), bf_lo(v.y), bf_hi(v.y),
                                 bf_lo(v.z), bf_hi(v.z), bf_lo(v.w), bf_hi(v.w)};
             float sq = 0.f;
@@ -72,9 +121,9 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) v[u] = ld16(src + (int64_t)(n + u) * sn);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) add_token(v[u]);
+            for (int u = 0; u < 8; ++u) add_token(v[u], n + u);
         }
-        for (; n < p.bs; ++n) add_token(ld16(src + (int64_t)n * sn));
+        for (; n < p.bs; ++n) add_token(ld16(src + (int64_t)n * sn), n);
         if (which == 1 && p.kbnd != nullptr)
             p.kbnd[(((int64_t)b * p.nb + t) * p.heads[1] + hd) * 8 + ch] = sqmax;
         const float denom = (float)p.bs;
@@ -97,9 +146,13 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
 }  // namespace
 
 hipError_t launch_pool(const PoolParams& p, hipStream_t s) {
-    void* args[] = {const_cast<PoolParams*>(&p)};
+    PoolParams q = p;
+    // stage the RoPE rows in LDS when the block's rows fit the default dynamic limit (256 tokens, 64 KB)
+    q.rope_lds = p.rope_cos != nullptr && p.bs <= 256;
+    void* args[] = {&q};
     const int tgrid = (p.kfrag || p.vfrag) ? p.nb_pad : p.nb;
-    return hipLaunchKernel((const void*)pool_kernel, dim3(tgrid, p.B), dim3(256), args, 0, s);
+    const size_t lds = q.rope_lds ? (size_t)p.bs * 256 : 0;
+    return hipLaunchKernel((const void*)pool_kernel, dim3(tgrid, p.B), dim3(256), args, lds, s);
 }
 
 }  // namespace mosaic

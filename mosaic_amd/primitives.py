@@ -147,6 +147,32 @@ def mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_s
     otherwise ``o_ba*w0 + o_cmp*w1 + o_slc*w2``.  With ``return_block_indices`` the selected
     block indices (int64 [B, N/sparse_block_size, Hk, K]) are returned as well.
     """
+    out, idx, _ = _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
+                               block_attn_only, no_compression, return_block_indices, None)
+    return (out, idx) if return_block_indices else out
+
+
+def mosaic_attn_func_rope(q, k, v, weight_ba_cmp_slc, rope_cos, rope_sin, block_attn_size, sparse_block_size,
+                          sparse_block_count, block_attn_only, no_compression=False, *, return_rotated=False,
+                          return_block_indices=False):
+    """mosaic_attn_func on q and k rotated by the 2-D RoPE, with the rotation fused into the
+    op's pooling pass (primitives.py:193-195 followed by :54-89): q and k are read once,
+    rotated, pooled and written rotated for the attention kernel.
+
+    ``rope_cos`` / ``rope_sin`` are the RoPE module's ``cos_freqs`` / ``sin_freqs`` ([N, 32]
+    fp32, primitives.py:115-123).  The result equals ``mosaic_attn_func(RoPE(q), RoPE(k), v,
+    ...)``.  With ``return_rotated`` the rotated q and k ([B, N, H, 64] bf16) are returned
+    after the output (and before the indices, when those are asked for too).
+    """
+    out, idx, rot = _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
+                                 sparse_block_count, block_attn_only, no_compression, return_block_indices,
+                                 (rope_cos, rope_sin))
+    res = (out,) + (rot if return_rotated else ()) + ((idx,) if return_block_indices else ())
+    return res[0] if len(res) == 1 else res
+
+
+def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
+                 block_attn_only, no_compression, return_block_indices, rope):
     dtype = q.dtype
     q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     _check_gqa(q, k, v)
@@ -170,18 +196,29 @@ def mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_s
     out = _out_like(q)
     a = _bsa_args(q, k, v, w, out, block_attn_size, sparse_block_size, sparse_block_count, mode, idx)
     L = _lib.lib()
+    rot = ()
+    if rope is not None:
+        cos, sin = (t.to(device=q.device, dtype=torch.float32).contiguous() for t in rope)
+        if tuple(cos.shape) != (N, d // 2) or tuple(sin.shape) != (N, d // 2):
+            raise ValueError(f"RoPE tables must be [seq_len, head_dim/2] = [{N}, {d // 2}]")
+        rot = (torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=q.device),
+               torch.empty(B, N, Hk, d, dtype=torch.bfloat16, device=q.device))
+
+        def run(ws_ptr, nbytes):
+            return L.mosaic_bsa_fwd_rope(ctypes.byref(a), cos.data_ptr(), sin.data_ptr(), rot[0].data_ptr(),
+                                         rot[1].data_ptr(), ws_ptr, nbytes, stream_of(q))
+        name = "mosaic_bsa_fwd_rope"
+    else:
+        def run(ws_ptr, nbytes):
+            return L.mosaic_bsa_fwd(ctypes.byref(a), ws_ptr, nbytes, stream_of(q))
+        name = "mosaic_bsa_fwd"
     nbytes = L.mosaic_bsa_workspace_size(ctypes.byref(a))
     if nbytes == 0 and mode != _lib.MODE_LOCAL_ONLY:
         # invalid arguments: let the entry point report which
-        _lib.check(L.mosaic_bsa_fwd(ctypes.byref(a), None, 0, stream_of(q)), "mosaic_bsa_fwd")
+        _lib.check(run(None, 0), name)
     ws = _workspace(nbytes, q.device) if nbytes else None
-    st = L.mosaic_bsa_fwd(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
-                          ws.numel() if ws is not None else 0, stream_of(q))
-    _lib.check(st, "mosaic_bsa_fwd")
-    out = out.to(dtype)
-    if return_block_indices:
-        return out, idx
-    return out
+    _lib.check(run(ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0), name)
+    return out.to(dtype), idx, tuple(t.to(dtype) for t in rot)
 
 
 class RoPE(nn.Module):
@@ -244,18 +281,32 @@ class MosaicAttention(nn.Module):
         logits = logits.view(S_, B_, self.q_heads, 3).permute(3, 1, 0, 2)   # [3, B, S, Hq]
         return torch.softmax(logits.float(), dim=0).type_as(x).unsqueeze(-1)
 
+    def _shared_rope_tables(self):
+        """True when the q and k RoPE modules hold equal tables (the model initialises both
+        from the same grid, mosaic.py:268-270); the comparison is cached per table version."""
+        tabs = (self.q_rope.cos_freqs, self.q_rope.sin_freqs, self.k_rope.cos_freqs, self.k_rope.sin_freqs)
+        key = tuple((t.data_ptr(), t._version) for t in tabs)
+        if getattr(self, "_rope_key", None) != key:
+            self._rope_key = key
+            self._rope_shared = bool(torch.equal(tabs[0], tabs[2]) and torch.equal(tabs[1], tabs[3]))
+        return self._rope_shared
+
     def forward(self, x):
         S_, B_ = x.shape[:2]
         q = self.to_q(x).view(S_, B_, self.q_heads, -1).transpose(0, 1)
         k = self.to_k(x).view(S_, B_, self.kv_heads, -1).transpose(0, 1)
         v = self.to_v(x).view(S_, B_, self.kv_heads, -1).transpose(0, 1)
         w = self.generate_strategy_weights(x)
-        if self.q_rope is not None:
-            q = self.q_rope(q)
-            k = self.k_rope(k)
-        out = mosaic_attn_func(q=q, k=k, v=v, weight_ba_cmp_slc=w, block_attn_size=self.block_attn_size,
-                               sparse_block_size=self.sparse_block_size,
-                               sparse_block_count=self.sparse_block_count,
-                               block_attn_only=self.block_attn_only, no_compression=self.no_compression)
+        args = dict(block_attn_size=self.block_attn_size, sparse_block_size=self.sparse_block_size,
+                    sparse_block_count=self.sparse_block_count, block_attn_only=self.block_attn_only,
+                    no_compression=self.no_compression)
+        if self.q_rope is not None and self._shared_rope_tables():
+            # the rotation runs inside the op's pooling pass (one read of q and k)
+            out = mosaic_attn_func_rope(q, k, v, w, self.q_rope.cos_freqs, self.q_rope.sin_freqs, **args)
+        else:
+            if self.q_rope is not None:
+                q = self.q_rope(q)
+                k = self.k_rope(k)
+            out = mosaic_attn_func(q=q, k=k, v=v, weight_ba_cmp_slc=w, **args)
         out = out.transpose(0, 1).reshape(S_, B_, -1)
         return self.to_o(out)

@@ -94,6 +94,18 @@ def test_workspace_size_and_missing_workspace():
     assert L.mosaic_bsa_workspace_size(ctypes.byref(local)) == 0
 
 
+def test_fused_rope_entry_validates():
+    L = _lib.lib()
+    a = _args()
+    n = L.mosaic_bsa_workspace_size(ctypes.byref(a))
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), None, FAKE, FAKE, FAKE, FAKE, n, None) == 1
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE, FAKE, None, FAKE, FAKE, n, None) == 1
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE + 4, FAKE, FAKE, FAKE, FAKE, n, None) == 7
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE, FAKE, FAKE, FAKE + 2, FAKE, n, None) == 7
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(_args(head_dim=32)), FAKE, FAKE, FAKE, FAKE, FAKE, n, None) == 2
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE, FAKE, FAKE, FAKE, None, 0, None) == 6
+
+
 def test_other_entry_points_validate():
     L = _lib.lib()
     t = _lib.Bnhd(FAKE, 0, 64 * 4, 64)

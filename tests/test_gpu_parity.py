@@ -11,6 +11,7 @@ import torch
 
 import mosaic_amd as M
 from mosaic_amd.inputs import BOTTLENECK_NSIDE16, STAGE1_NSIDE64, STAGE2_NSIDE32_B24, Workload, make_inputs
+from mosaic_amd.healpix import apply_rope, get_healpix_grid, rope_tables
 from oracle import bsa_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -220,6 +221,35 @@ def test_mosaic_attn_func_large_logits_mixed_paths(qscale):
     assert rel <= REL_L2, f"rel_l2 {rel:.3e}"
 
 
+@pytest.mark.parametrize("mode", ["full", "no_compression", "no_selection", "local_only"])
+@pytest.mark.parametrize("wl", [Workload("nside16_h20kv5_bs64_top4", 16, 1, 20, 5, 64, 64, 64, 4, False),
+                                Workload("nside8_b3_h8kv2_bl256_bs128_top3", 8, 3, 8, 2, 64, 256, 128, 3, False)],
+                         ids=lambda w: w.name)
+def test_fused_rope_equals_rotated_inputs(wl, mode):
+    """RoPE inside the pooling pass: the rotated q and k equal the CPU rotation bit for bit
+    (products and sum rounded as the reference rounds them), and the op's output and indices
+    equal those of the op run on the rotated inputs -- which the oracle checks as well."""
+    q, k, v, w = make_inputs(wl, seed=9)
+    cos, sin = rope_tables(get_healpix_grid(wl.nside), 64)
+    qr, kr = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+    K = 0 if mode == "no_selection" else wl.sparse_block_count
+    args = (wl.block_attn_size, wl.sparse_block_size, K, mode == "local_only", mode == "no_compression")
+    wd = None if mode == "local_only" else w
+    res = M.mosaic_attn_func_rope(*dev(q, k, v), wd if wd is None else wd.to(DEV), cos, sin, *args,
+                                  return_rotated=True, return_block_indices=True)
+    out, q_rot, k_rot, idx = res
+    assert torch.equal(q_rot.cpu(), qr) and torch.equal(k_rot.cpu(), kr)
+    ref_out, ref_idx = M.mosaic_attn_func(*dev(qr, kr, v), wd if wd is None else wd.to(DEV), *args,
+                                          return_block_indices=True)
+    assert (idx is None) == (ref_idx is None)
+    if idx is not None:
+        assert torch.equal(idx, ref_idx)
+    assert torch.equal(out, ref_out)
+    oracle = O.mosaic_attn_func(qr, kr, v, wd, *args[:4], no_compression=args[4],
+                                block_indices=None if idx is None else idx.cpu())
+    close(out.cpu(), oracle)
+
+
 def test_strided_inputs_match_contiguous():
     """q/k/v as the caller produces them: [B, S, H, d] views of a sequence-first [S, B, H*d]."""
     wl = Workload("nside8_b2_h12kv3_bs64_top4", 8, 2, 12, 3, 64, 64, 64, 4, False)
@@ -274,5 +304,8 @@ def test_mosaic_attention_module_runs():
     m.k_rope.initialize_rope(pos)
     m = m.to(DEV).to(torch.bfloat16)
     x = torch.randn(768, 2, 768, device=DEV, dtype=torch.bfloat16)
-    y = m(x)
+    assert m._shared_rope_tables()
+    y = m(x)   # RoPE fused into the op's pooling pass
     assert y.shape == x.shape and torch.isfinite(y.float()).all()
+    m._shared_rope_tables = lambda: False
+    assert torch.equal(m(x), y)   # RoPE modules, then the op
