@@ -126,14 +126,14 @@ def rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream):
     q0, k0, _, _ = make_inputs(replace(wl, rope=False), seed=args.seed)
     q0, k0 = q0.to(dev), k0.to(dev)
     cos, sin = (t.to(dev) for t in rope_tables(get_healpix_grid(wl.nside), wl.head_dim))
-    q_rot, k_rot = torch.empty_like(q0), torch.empty_like(k0)
+    k_rot = torch.empty_like(k0)   # the full mode rotates q in the attention kernel: no q_rot
     sp = stream.cuda_stream
     fa = _lib.BsaArgs.from_buffer_copy(a)
     fa.q, fa.k = bnhd(q0), bnhd(k0)
 
     def fused():
-        st = L.mosaic_bsa_fwd_rope(ctypes.byref(fa), cos.data_ptr(), sin.data_ptr(), q_rot.data_ptr(),
-                                   k_rot.data_ptr(), ws_ptr, nbytes, sp)
+        st = L.mosaic_bsa_fwd_rope(ctypes.byref(fa), cos.data_ptr(), sin.data_ptr(), None, k_rot.data_ptr(),
+                                   ws_ptr, nbytes, sp)
         if st:
             raise RuntimeError(_lib.strerror(st))
 

@@ -105,8 +105,9 @@ MOSAIC_API int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* worksp
    rope_cos, rope_sin: fp32 [seq_len, 32], the reference's cos_freqs / sin_freqs buffers
    (primitives.py:115-123: 16 longitude then 16 latitude frequencies per position); pair
    (2m, 2m+1) of every head is rotated by angle m.  q_rot, k_rot: caller-allocated bf16
-   [batch, seq_len, H, 64] contiguous outputs holding the rotated q and k.  Same workspace
-   as mosaic_bsa_fwd. */
+   [batch, seq_len, H, 64] contiguous outputs holding the rotated q and k.  In the FULL and
+   NO_COMPRESSION modes the attention kernel rotates q itself and q_rot may be null (then
+   the rotated q is not written).  Same workspace as mosaic_bsa_fwd. */
 MOSAIC_API int mosaic_bsa_fwd_rope(const mosaic_bsa_args* args, const float* rope_cos, const float* rope_sin,
                                    void* q_rot, void* k_rot, void* workspace, size_t workspace_bytes,
                                    void* stream);

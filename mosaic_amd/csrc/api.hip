@@ -150,9 +150,13 @@ struct RopeIO {
 int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* stream, void* const* events,
                 const RopeIO* rope = nullptr) {
     if (int e = validate(a)) return e;
+    // With RoPE, the modes with both local and selected branches rotate q inside the attention
+    // kernel, so the rotated q is an optional output there; the other modes read it back.
+    const bool q_in_kernel = a->mode == MOSAIC_BSA_FULL || a->mode == MOSAIC_BSA_NO_COMPRESSION;
     if (rope != nullptr) {
-        if (!rope->cos || !rope->sin || !rope->q_rot || !rope->k_rot) return MOSAIC_ERR_NULL_POINTER;
-        if (!aligned16(rope->cos) || !aligned16(rope->sin) || !aligned16(rope->q_rot) || !aligned16(rope->k_rot))
+        if (!rope->cos || !rope->sin || !rope->k_rot || (!rope->q_rot && !q_in_kernel)) return MOSAIC_ERR_NULL_POINTER;
+        if (!aligned16(rope->cos) || !aligned16(rope->sin) || !aligned16(rope->k_rot) ||
+            (rope->q_rot && !aligned16(rope->q_rot)))
             return MOSAIC_ERR_ALIGNMENT;
     }
     const Layout L = layout_of(a);
@@ -184,8 +188,13 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         pp.rot[1] = static_cast<bf16_t*>(rope->k_rot);
     };
     auto use_rotated = [&]() {
-        ap.q = static_cast<const bf16_t*>(rope->q_rot);
-        ap.q_sb = (int64_t)N * Hq * kHeadDim; ap.q_sn = (int64_t)Hq * kHeadDim; ap.q_sh = kHeadDim;
+        if (q_in_kernel) {
+            ap.rope_cos = rope->cos;
+            ap.rope_sin = rope->sin;
+        } else {
+            ap.q = static_cast<const bf16_t*>(rope->q_rot);
+            ap.q_sb = (int64_t)N * Hq * kHeadDim; ap.q_sn = (int64_t)Hq * kHeadDim; ap.q_sh = kHeadDim;
+        }
         ap.k = static_cast<const bf16_t*>(rope->k_rot);
         ap.k_sb = (int64_t)N * Hk * kHeadDim; ap.k_sn = (int64_t)Hk * kHeadDim; ap.k_sh = kHeadDim;
     };

@@ -369,6 +369,18 @@ void bsa_attn_kernel(AttnParams p) {
             __builtin_amdgcn_global_load_lds(qb + (int64_t)(n0 + row) * p.q_sn + 8 * (pos ^ ((row >> 1) & 7)),
                                              (lds_void*)(qs + 8 * i * 64), 16, 0, 0);
         }
+        // With RoPE, the 64 query rows' cos / sin table rows (128 bytes each) go to the K and V
+        // buffers of tile 1, unused until the first barrier; q is rotated from them there.
+        if (p.rope_cos != nullptr) {
+#pragma unroll
+            for (int i = 0; i < 8 / NW; ++i) {
+                const int row0 = 8 * ((8 / NW) * wave + i);
+                __builtin_amdgcn_global_load_lds(p.rope_cos + (int64_t)(n0 + row0) * 32 + 4 * lane,
+                                                 (lds_void*)(Ks1 + row0 * 64), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(p.rope_sin + (int64_t)(n0 + row0) * 32 + 4 * lane,
+                                                 (lds_void*)(Vs1 + row0 * 64), 16, 0, 0);
+            }
+        }
     } else {
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt)
@@ -451,10 +463,8 @@ void bsa_attn_kernel(AttnParams p) {
     // Start of tile t in buffer BUF: wait for this wave's loads of tile t, then the barrier
     // makes every wave's loads visible and guarantees the other buffer (tile t-1) is no
     // longer read; the loads of tile t+1 go there.
-    auto begin_tile = [&](auto bufc, int t) {
+    auto issue_next = [&](auto bufc, int t) {
         const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
-        wait_vmem();
-        __syncthreads();
         if (t + 1 < total_tiles)
             dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(t + 1), BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, wave);
         if constexpr (kFastSel) {
@@ -472,6 +482,11 @@ void bsa_attn_kernel(AttnParams p) {
             }
         }
     };
+    auto begin_tile = [&](auto bufc, int t) {
+        wait_vmem();
+        __syncthreads();
+        issue_next(bufc, t);
+    };
 
     bf16_t* outp = p.out + ((int64_t)b * p.N + n0) * p.Hq * kHeadDim + (int64_t)j * kHeadDim;
 
@@ -481,16 +496,37 @@ void bsa_attn_kernel(AttnParams p) {
             const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
             const bf16_t* Kc = BUF ? Ks1 : Ks0;
             const bf16_t* Vc = BUF ? Vs1 : Vs0;
-            begin_tile(bufc, t);
-            if constexpr (kPartial) {
-                if (t == 0) {  // the Q rows staged in the prologue (same layout as a K tile)
-                    const bf16_t* qs = Part + wave * 64 * PS;
+            if (kPartial && t == 0) {
+                wait_vmem();
+                __syncthreads();
+                // the Q rows staged in the prologue (same layout as a K tile)
+                const bf16_t* qs = Part + wave * 64 * PS;
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                    for (int ds = 0; ds < 4; ++ds)
+                        qf[qt][ds] = as_bf16x8(*reinterpret_cast<const uint4*>(qs + 32 * qt * 64 + ro.k[ds]));
+                if (p.rope_cos != nullptr) {
+                    // RoPE of q: this lane's dims 16 ds + 8 hh .. + 7 of query row 32 qt + r are
+                    // the pairs 8 ds + 4 hh .. + 3 of that row's table entries
+                    const float* cs = reinterpret_cast<const float*>(Ks1);
+                    const float* sn = reinterpret_cast<const float*>(Vs1);
 #pragma unroll
                     for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-                        for (int ds = 0; ds < 4; ++ds)
-                            qf[qt][ds] = as_bf16x8(*reinterpret_cast<const uint4*>(qs + 32 * qt * 64 + ro.k[ds]));
+                        for (int ds = 0; ds < 4; ++ds) {
+                            const int e = (32 * qt + r) * 32 + 8 * ds + 4 * hh;
+                            const float4 c4 = *reinterpret_cast<const float4*>(cs + e);
+                            const float4 s4 = *reinterpret_cast<const float4*>(sn + e);
+                            const uint4 u = __builtin_bit_cast(uint4, qf[qt][ds]);
+                            qf[qt][ds] = as_bf16x8(make_uint4(rope_pair(u.x, c4.x, s4.x), rope_pair(u.y, c4.y, s4.y),
+                                                              rope_pair(u.z, c4.z, s4.z), rope_pair(u.w, c4.w, s4.w)));
+                        }
+                    __syncthreads();  // every wave is done with the tables before tile 1 lands there
                 }
+                issue_next(bufc, t);
+            } else {
+                begin_tile(bufc, t);
             }
             s_tile(Kc, ro, qf, s);
             float mt[2];

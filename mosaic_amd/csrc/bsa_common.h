@@ -112,6 +112,23 @@ __device__ __forceinline__ uint32_t wave_max_all_u32(uint32_t x) {
     return max((uint32_t)b[0], (uint32_t)b[1]);
 }
 
+// 2-D RoPE of one bf16 pair (x0, x1) packed in a word, by angle (c = cos, s = sin):
+// (x0 c - x1 s, x1 c + x0 s) in fp32 with both products and the sum rounded separately (no
+// fused multiply-add), as the reference's elementwise tensor ops round them
+// (primitives.py:125-135), then rounded to bf16.
+__device__ __forceinline__ float rope_mul_sub(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+    return a * b - c * d;
+}
+__device__ __forceinline__ float rope_mul_add(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+    return a * b + c * d;
+}
+__device__ __forceinline__ uint32_t rope_pair(uint32_t w, float c, float s) {
+    const float x0 = bf_lo(w), x1 = bf_hi(w);
+    return pack_bf16x2(rope_mul_sub(x0, c, x1, s), rope_mul_add(x1, c, x0, s));
+}
+
 // Map a linear workgroup id to a logical tile so that each of the 8 XCDs (which receive
 // workgroups round-robin) works on one contiguous range of logical tiles and keeps that
 // range's K/V blocks in its own L2.
@@ -194,6 +211,10 @@ struct AttnParams {
     const void* idx;         // [B, nb, Hk, K] int32 or int64
     const bf16_t* ocmp;      // compressed-branch output [B, nb, Hq, 64]
     const float* kbnd;       // key-norm bounds per selected block [B, nb, Hk, 8] (optional)
+    // Optional 2-D RoPE of q inside the kernel (modes with a partial buffer): fp32 cos / sin
+    // tables [N, 32]; q is read unrotated and rotated in registers.
+    const float* rope_cos;
+    const float* rope_sin;
     int B, N, Hq, Hk, G;
     int bs_l, bs, K, nb;
     int head_groups;         // G / waves-per-workgroup

@@ -20,17 +20,6 @@
 namespace mosaic {
 namespace {
 
-// a*b - c*d and a*b + c*d with both products and the sum rounded separately (no fused
-// multiply-add), as the reference's elementwise tensor ops round them
-__device__ __forceinline__ float mul_sub(float a, float b, float c, float d) {
-#pragma clang fp contract(off)
-    return a * b - c * d;
-}
-__device__ __forceinline__ float mul_add(float a, float b, float c, float d) {
-#pragma clang fp contract(off)
-    return a * b + c * d;
-}
-
 __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
     const int t = blockIdx.x, b = blockIdx.y;
     // RoPE tables of the block's tokens, read once per workgroup: [token][8 float4] of cos,
@@ -80,8 +69,9 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
         // RoPE of this thread's 4 pairs (frequencies 4 ch .. 4 ch + 3) of token n of the block
         const bool rope = p.rope_cos != nullptr && which < 2;
         const int64_t tok0 = (int64_t)t * p.bs;
-        bf16_t* rdst = rope ? p.rot[which] + (((int64_t)b * p.nb * p.bs + tok0) * p.heads[which] + hd) * kHeadDim + ch * 8
-                            : nullptr;
+        bf16_t* rdst = rope && p.rot[which] != nullptr
+                           ? p.rot[which] + (((int64_t)b * p.nb * p.bs + tok0) * p.heads[which] + hd) * kHeadDim + ch * 8
+                           : nullptr;
         auto rotate = [&](uint4 v, int n) __attribute__((always_inline)) -> uint4 {
             const float4 c = p.rope_lds ? rope_rows[n * 8 + ch]
                                         : *reinterpret_cast<const float4*>(p.rope_cos + (tok0 + n) * 32 + 4 * ch);
@@ -91,12 +81,9 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
             const float cf[4] = {c.x, c.y, c.z, c.w}, sf[4] = {s.x, s.y, s.z, s.w};
             uint32_t o[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x0 = bf_lo(w[i]), x1 = bf_hi(w[i]);
-                o[i] = pack_bf16x2(mul_sub(x0, cf[i], x1, sf[i]), mul_add(x1, cf[i], x0, sf[i]));
-            }
+            for (int i = 0; i < 4; ++i) o[i] = rope_pair(w[i], cf[i], sf[i]);
             const uint4 r = make_uint4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<uint4*>(rdst + (int64_t)n * p.heads[which] * kHeadDim) = r;
+            if (rdst) *reinterpret_cast<uint4*>(rdst + (int64_t)n * p.heads[which] * kHeadDim) = r;
             return r;
         };
         float acc[8];

@@ -166,13 +166,13 @@ def mosaic_attn_func_rope(q, k, v, weight_ba_cmp_slc, rope_cos, rope_sin, block_
     """
     out, idx, rot = _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
                                  sparse_block_count, block_attn_only, no_compression, return_block_indices,
-                                 (rope_cos, rope_sin))
+                                 (rope_cos, rope_sin), return_rotated)
     res = (out,) + (rot if return_rotated else ()) + ((idx,) if return_block_indices else ())
     return res[0] if len(res) == 1 else res
 
 
 def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
-                 block_attn_only, no_compression, return_block_indices, rope):
+                 block_attn_only, no_compression, return_block_indices, rope, return_rotated=False):
     dtype = q.dtype
     q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     _check_gqa(q, k, v)
@@ -201,12 +201,17 @@ def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
         cos, sin = (t.to(device=q.device, dtype=torch.float32).contiguous() for t in rope)
         if tuple(cos.shape) != (N, d // 2) or tuple(sin.shape) != (N, d // 2):
             raise ValueError(f"RoPE tables must be [seq_len, head_dim/2] = [{N}, {d // 2}]")
-        rot = (torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=q.device),
-               torch.empty(B, N, Hk, d, dtype=torch.bfloat16, device=q.device))
+        # the full and no-compression modes rotate q inside the attention kernel: the rotated q
+        # is only written when asked for
+        want_q = return_rotated or mode not in (_lib.MODE_FULL, _lib.MODE_NO_COMPRESSION)
+        q_rot = torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=q.device) if want_q else None
+        k_rot = torch.empty(B, N, Hk, d, dtype=torch.bfloat16, device=q.device)
+        rot = (q_rot, k_rot)
 
         def run(ws_ptr, nbytes):
-            return L.mosaic_bsa_fwd_rope(ctypes.byref(a), cos.data_ptr(), sin.data_ptr(), rot[0].data_ptr(),
-                                         rot[1].data_ptr(), ws_ptr, nbytes, stream_of(q))
+            return L.mosaic_bsa_fwd_rope(ctypes.byref(a), cos.data_ptr(), sin.data_ptr(),
+                                         q_rot.data_ptr() if q_rot is not None else None, k_rot.data_ptr(),
+                                         ws_ptr, nbytes, stream_of(q))
         name = "mosaic_bsa_fwd_rope"
     else:
         def run(ws_ptr, nbytes):
@@ -218,7 +223,7 @@ def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
         _lib.check(run(None, 0), name)
     ws = _workspace(nbytes, q.device) if nbytes else None
     _lib.check(run(ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0), name)
-    return out.to(dtype), idx, tuple(t.to(dtype) for t in rot)
+    return out.to(dtype), idx, tuple(t.to(dtype) if t is not None else None for t in rot)
 
 
 class RoPE(nn.Module):

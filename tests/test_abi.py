@@ -99,7 +99,10 @@ def test_fused_rope_entry_validates():
     a = _args()
     n = L.mosaic_bsa_workspace_size(ctypes.byref(a))
     assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), None, FAKE, FAKE, FAKE, FAKE, n, None) == 1
-    assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE, FAKE, None, FAKE, FAKE, n, None) == 1
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE, FAKE, FAKE, None, FAKE, n, None) == 1   # k_rot
+    # the rotated q is optional only where the attention kernel rotates q itself
+    local = _args(mode=_lib.MODE_LOCAL_ONLY, weights=None)
+    assert L.mosaic_bsa_fwd_rope(ctypes.byref(local), FAKE, FAKE, None, FAKE, None, 0, None) == 1
     assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE + 4, FAKE, FAKE, FAKE, FAKE, n, None) == 7
     assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE, FAKE, FAKE, FAKE + 2, FAKE, n, None) == 7
     assert L.mosaic_bsa_fwd_rope(ctypes.byref(_args(head_dim=32)), FAKE, FAKE, FAKE, FAKE, FAKE, n, None) == 2

@@ -226,9 +226,10 @@ def test_mosaic_attn_func_large_logits_mixed_paths(qscale):
                                 Workload("nside8_b3_h8kv2_bl256_bs128_top3", 8, 3, 8, 2, 64, 256, 128, 3, False)],
                          ids=lambda w: w.name)
 def test_fused_rope_equals_rotated_inputs(wl, mode):
-    """RoPE inside the pooling pass: the rotated q and k equal the CPU rotation bit for bit
-    (products and sum rounded as the reference rounds them), and the op's output and indices
-    equal those of the op run on the rotated inputs -- which the oracle checks as well."""
+    """RoPE inside the op: the rotated q and k written by the pooling pass equal the CPU
+    rotation bit for bit (products and sum rounded as the reference rounds them), and the
+    op's output and indices -- with q rotated again in the attention kernel's registers in the
+    full modes -- equal those of the op run on the rotated inputs; the oracle checks them too."""
     q, k, v, w = make_inputs(wl, seed=9)
     cos, sin = rope_tables(get_healpix_grid(wl.nside), 64)
     qr, kr = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
@@ -245,6 +246,9 @@ def test_fused_rope_equals_rotated_inputs(wl, mode):
     if idx is not None:
         assert torch.equal(idx, ref_idx)
     assert torch.equal(out, ref_out)
+    # without the rotated q as an output (the full modes then rotate q only in registers)
+    out2 = M.mosaic_attn_func_rope(*dev(q, k, v), wd if wd is None else wd.to(DEV), cos, sin, *args)
+    assert torch.equal(out2, out)
     oracle = O.mosaic_attn_func(qr, kr, v, wd, *args[:4], no_compression=args[4],
                                 block_indices=None if idx is None else idx.cpu())
     close(out.cpu(), oracle)
