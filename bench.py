@@ -15,7 +15,9 @@ Prints one JSON line.  Options: --gpus (only 1 is supported: the op runs on one 
 nside64_sweep, nside128}, --no-cpu-baseline, --calibration-copy-mb, --dense-baseline (also times full
 attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v), --rope-fused (also
 times the op with the input side's RoPE fused into its pooling pass, mosaic_bsa_fwd_rope,
-against eager torch RoPE followed by the op, both on unrotated q/k).
+against eager torch RoPE followed by the op, both on unrotated q/k), --interp (also times the
+k-nearest-neighbour cross-attention between the model's lat-lon and HEALPix grids,
+mosaic_knn_interp_fwd, at --interp-batch members).
 """
 
 from __future__ import annotations
@@ -163,6 +165,73 @@ def rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream):
             "rope": "torch eager on the GPU (fp32 math, bf16 out), then mosaic_bsa_fwd"}
 
 
+def interp_leg(L, args, dev, stream):
+    """k-nearest-neighbour cross-attention between the model's grids (mosaic_knn_interp_fwd):
+    121 x 240 lat-lon (29040 points) <-> HEALPix nside 64 (49152), 24 neighbours, 12 heads of
+    64, ``--interp-batch`` members, both directions.  Algorithmic bytes per launch: every k / v
+    row read once, the output written once, the neighbour lists and relative positions read."""
+    import numpy as np
+    from mosaic_amd.healpix import get_healpix_grid
+    from mosaic_amd.interp import get_neighbors, rad_to_xyz
+    lon = torch.linspace(0, 358.5, 240)
+    lat = torch.linspace(-90, 90, 121)
+    ll = torch.deg2rad(torch.stack(torch.meshgrid(lon, lat, indexing="ij"), -1).reshape(-1, 2))
+    hp = torch.deg2rad(get_healpix_grid(64))
+    K, H, B = 24, 12, args.interp_batch
+    g = torch.Generator().manual_seed(args.seed)
+    gd = torch.Generator(device=dev).manual_seed(args.seed)
+    res = {"neighbours": K, "heads": H, "batch": B}
+    for name, src, dst in (("ll_to_hp", ll, hp), ("hp_to_ll", hp, ll)):
+        nb = torch.from_numpy(np.ascontiguousarray(get_neighbors(src.numpy(), dst.numpy(), k=K)))
+        rel = torch.nn.functional.normalize(rad_to_xyz(dst).unsqueeze(1) - rad_to_xyz(src)[nb], dim=-1)
+        nb_d, rel_d = nb.to(dev, torch.int32), rel.to(dev)
+        kv = torch.randn(len(src), B, 2 * H * 64, generator=gd, device=dev, dtype=torch.bfloat16)
+        k = kv[..., :H * 64].unflatten(-1, (H, 64))
+        v = kv[..., H * 64:].unflatten(-1, (H, 64))
+        w_q = torch.randn(H * 64, 3, generator=g).to(torch.bfloat16).to(dev)
+        out = torch.empty(len(dst), B, H, 64, dtype=torch.bfloat16, device=dev)
+        sp = stream.cuda_stream
+        kb, vb = _lib.Bnhd(k.data_ptr(), k.stride(1), k.stride(0), k.stride(2)), \
+            _lib.Bnhd(v.data_ptr(), v.stride(1), v.stride(0), v.stride(2))
+
+        def call():
+            st = L.mosaic_knn_interp_fwd(kb, vb, nb_d.data_ptr(), rel_d.data_ptr(), w_q.data_ptr(), len(src),
+                                         len(dst), B, H, 64, K, 0.125, out.data_ptr(), sp)
+            if st:
+                raise RuntimeError(_lib.strerror(st))
+        for _ in range(3):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        nbytes = len(src) * B * H * 64 * 2 * 2 + len(dst) * B * H * 64 * 2 + len(dst) * K * (4 + 12)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        leg = {"num_from": len(src), "num_to": len(dst), "ms": round(ms, 4), "bytes": nbytes,
+               "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+        if B <= 4:   # the reference's formulation in eager torch (materialised q and gathers)
+            def eager():
+                q = (rel_d.to(torch.bfloat16) @ w_q.t()).view(len(dst), K, 1, H, 64)
+                kg, vg = k[nb_d.long()], v[nb_d.long()]
+                sc = (q * kg).sum(dim=-1, keepdim=True) * 0.125
+                wt = torch.softmax(sc, dim=1, dtype=torch.float32).type_as(kg)
+                return (wt * vg).sum(dim=1)
+            ref = eager()
+            leg["max_abs_vs_eager"] = round((ref.float() - out.float()).abs().max().item(), 5)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(5):
+                eager()
+            torch.cuda.synchronize()
+            leg["torch_eager_ms"] = round((time.perf_counter() - t0) * 1e3 / 5, 4)
+        res[name] = leg
+    return res
+
+
 def cpu_baseline(wl, q, k, v, w):
     """The CPU oracle (torch restatement of the reference path) on the full workload."""
     from oracle import bsa_oracle as O
@@ -204,6 +273,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--dense-baseline", action="store_true")
     ap.add_argument("--rope-fused", action="store_true")
+    ap.add_argument("--interp", action="store_true")
+    ap.add_argument("--interp-batch", type=int, default=24)
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -335,6 +406,8 @@ def main():
         result["dense_baseline"] = dense_baseline(L, q, k, v, out, wl, args, stream)
     if args.rope_fused:
         result["rope_fused"] = rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream)
+    if args.interp:
+        result["knn_interp"] = interp_leg(L, args, dev, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, q_c, k_c, v_c, w_c)
     print(json.dumps(result))

@@ -112,6 +112,22 @@ MOSAIC_API int mosaic_bsa_fwd_rope(const mosaic_bsa_args* args, const float* rop
                                    void* q_rot, void* k_rot, void* workspace, size_t workspace_bytes,
                                    void* stream);
 
+/* k-nearest-neighbour cross-attention between two grids: the gather-attention of
+   CrossAttentionInterpolate.forward (primitives.py:265-283), from the kv projection to the
+   input of to_o.  Target s attends to the num_neighbors source points neighbors[s, :]
+   (int32 [num_to, num_neighbors]) of k and v, with queries to_q(rel_pos[s, j]) formed
+   inside the kernel from rel_pos (fp32 [num_to, num_neighbors, 3]) and w_q (bf16
+   [num_heads * 64, 3], the to_q weight); softmax over the neighbours in fp32.
+   k, v: bf16 [num_from, batch, num_heads, 64] given by strides (stride_n: source point,
+   stride_b: batch member, stride_h: head).  out: bf16 [num_to, batch, num_heads, 64]
+   contiguous.  num_neighbors <= 32; scale <= 0 selects head_dim^-0.5.  Neighbour indices
+   outside [0, num_from) are clamped.  w_q and out 16-byte aligned. */
+MOSAIC_API int mosaic_knn_interp_fwd(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors,
+                                     const float* rel_pos, const void* w_q, int32_t num_from,
+                                     int32_t num_to, int32_t batch, int32_t num_heads,
+                                     int32_t head_dim, int32_t num_neighbors, float scale,
+                                     void* out, void* stream);
+
 /*
  * Selected-branch attention given block indices.  Replaces mosaic_sparse_attn /
  * MosaicAttnFunction.forward / mosaic_attn_fwd (ops.py:557-566, 510-538, 137-176):

@@ -25,6 +25,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_bsa_fwd",
     "mosaic_bsa_fwd_profiled",
     "mosaic_bsa_fwd_rope",
+    "mosaic_knn_interp_fwd",
     "mosaic_sparse_attn_fwd",
     "mosaic_block_attn_fwd",
     "mosaic_dense_attn_fwd",
@@ -76,6 +77,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_bsa_fwd_profiled.restype = c_int
     lib.mosaic_bsa_fwd_rope.argtypes = [P(BsaArgs), c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]
     lib.mosaic_bsa_fwd_rope.restype = c_int
+    lib.mosaic_knn_interp_fwd.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                          c_f, c_vp, c_vp]
+    lib.mosaic_knn_interp_fwd.restype = c_int
     lib.mosaic_sparse_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
                                            c_i32, c_i32, c_f, c_vp, c_vp, c_vp]
     lib.mosaic_sparse_attn_fwd.restype = c_int

@@ -354,6 +354,30 @@ int mosaic_pool_mean_fwd(mosaic_bnhd x, int32_t batch, int32_t seq_len, int32_t 
     return launch_status(launch_pool(pp, static_cast<hipStream_t>(stream)));
 }
 
+int mosaic_knn_interp_fwd(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors, const float* rel_pos,
+                          const void* w_q, int32_t num_from, int32_t num_to, int32_t batch, int32_t num_heads,
+                          int32_t head_dim, int32_t num_neighbors, float scale, void* out, void* stream) {
+    if (num_from <= 0 || num_to <= 0 || batch <= 0 || num_heads <= 0) return MOSAIC_ERR_SHAPE;
+    if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
+    if (num_neighbors <= 0 || num_neighbors > 32) return MOSAIC_ERR_BLOCK_COUNT;
+    if (int e = check_bnhd(k)) return e;
+    if (int e = check_bnhd(v)) return e;
+    if (neighbors == nullptr || rel_pos == nullptr || w_q == nullptr || out == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(out) || !aligned16(w_q) || reinterpret_cast<uintptr_t>(rel_pos) % 4 ||
+        reinterpret_cast<uintptr_t>(neighbors) % 4)
+        return MOSAIC_ERR_ALIGNMENT;
+    InterpParams p{};
+    p.k = static_cast<const bf16_t*>(k.ptr); p.k_sn = k.stride_n; p.k_sb = k.stride_b; p.k_sh = k.stride_h;
+    p.v = static_cast<const bf16_t*>(v.ptr); p.v_sn = v.stride_n; p.v_sb = v.stride_b; p.v_sh = v.stride_h;
+    p.neighbors = neighbors;
+    p.rel_pos = rel_pos;
+    p.w_q = static_cast<const bf16_t*>(w_q);
+    p.out = static_cast<bf16_t*>(out);
+    p.S_from = num_from; p.S_to = num_to; p.B = batch; p.H = num_heads; p.K = num_neighbors;
+    p.scale = resolve_scale(scale, head_dim);
+    return launch_status(launch_knn_attn(p, static_cast<hipStream_t>(stream)));
+}
+
 // scores [B, Hk, nb, nb_pad] bf16, then k_cmp in operand order [B, Hk, nb_pad, 64] bf16
 size_t topk_scores_bytes(size_t batch, size_t num_blocks, size_t num_kv_heads) {
     const size_t nbp = (num_blocks + 31) / 32 * 32;

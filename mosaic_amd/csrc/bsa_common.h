@@ -231,6 +231,19 @@ hipError_t launch_topk(const TopkParams& p, hipStream_t s);
 hipError_t launch_combine(const CombineParams& c, int B, int nb, hipStream_t s);
 hipError_t launch_attn(const AttnParams& p, int mode, bool idx64, int waves, hipStream_t s);
 
+// k-nearest-neighbour cross-attention between grids (interp.hip).
+struct InterpParams {
+    const bf16_t* k; int64_t k_sn, k_sb, k_sh;   // [S_from, B, H, 64]: point, member, head strides
+    const bf16_t* v; int64_t v_sn, v_sb, v_sh;
+    const int32_t* neighbors;                    // [S_to, K] source points of each target
+    const float* rel_pos;                        // [S_to, K, 3] normalised relative positions
+    const bf16_t* w_q;                           // [H * 64, 3] query projection (to_q.weight)
+    bf16_t* out;                                 // [S_to, B, H, 64] contiguous
+    int S_from, S_to, B, H, K;
+    float scale;
+};
+hipError_t launch_knn_attn(const InterpParams& p, hipStream_t s);
+
 // Maximum number of selected blocks per query block (block indices are staged in LDS).
 constexpr int kMaxSelected = 1024;
 

@@ -1,0 +1,237 @@
+// interp.hip -- k-nearest-neighbour cross-attention between two grids (gfx950).
+//
+// Replaces the gather-attention of CrossAttentionInterpolate.forward (primitives.py:265-283):
+//   q[s, j]    = to_q(rel_pos[s, j])            (Linear 3 -> H*64, bf16 out)
+//   score      = sum_d bf16(q[s, j, h, d] * k[n(s, j), b, h, d])  -> bf16, * scale -> bf16
+//   w          = softmax_j(score) in fp32, then bf16        (softmax over the K neighbours)
+//   out[s,b,h] = sum_j bf16(w[j] * v[n(s, j), b, h, :])      -> bf16
+// with the reference's rounding points (bf16 elementwise products, fp32 sums rounded once).
+// The reference materialises q [S_to, K, H*64] and the gathered k, v [S_to, K, B, H*64];
+// here q is formed in registers from the three rel_pos numbers and the head's 64x3 slice of
+// to_q, and the k / v rows are read straight from [S_from, B, H, 64] (neighbouring targets
+// share most of their neighbours, so rows are reused from L2).
+//
+// The work is VALU-bound: every (target, member, head) takes 2 K 64 bf16-rounded products
+// (a multiply, half a v_cvt_pk_bf16_f32 and half a v_dot2_f32_bf16 each, plus the bf16 ->
+// fp32 unpack of the k / v element).  Staging each tile of targets' neighbour union in LDS
+// (cutting the L2 requests 4-7x) measured slower than this direct form: it halves the
+// occupancy, and occupancy is what hides the latency of the reduction chains.
+//
+// One wave per (target s, head h) pair, looping over the batch members b with the next
+// member's rows in flight.  Lane l = 8 jg + dc holds the 8-dim chunk dc of neighbours
+// jg + 8 i (its "slots"): every k / v read is a 16-byte load and each 128-byte row is read
+// by 8 adjacent lanes.  Scores are summed over the 8 chunk lanes with DPP (lanes l ^ 1,
+// l ^ 2, l ^ 4), the softmax max / sum over the 8 neighbour groups with DPP row_ror:8,
+// v_permlane16_swap and v_permlane32_swap; the output's 8 partial sums per lane are
+// reduce-scattered over the groups by the same three exchanges, leaving one dimension per
+// lane.  Workgroups are remapped so that each XCD takes one contiguous range of targets.
+#include "bsa_common.h"
+
+namespace mosaic {
+namespace {
+
+constexpr int kInterpWaves = 4;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float x) {
+    return fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false)));
+}
+
+// x summed over the 8 chunk lanes of its neighbour group (lanes l ^ 1, l ^ 2, l ^ 4)
+__device__ __forceinline__ float chunk_sum(float x) {
+    x = dpp_add<0xb1>(x);      // quad_perm [1,0,3,2]
+    x = dpp_add<0x4e>(x);      // quad_perm [2,3,0,1]
+    return dpp_add<0x141>(x);  // row_half_mirror
+}
+
+// v_permlane16_swap(a, b): rows 1 and 3 of a trade places with rows 0 and 2 of b.  The
+// returned pair, summed, is a[l] + a[l ^ 16] in even rows and b[l] + b[l ^ 16] in odd rows.
+__device__ __forceinline__ float swap16_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// v_permlane32_swap(a, b): lanes 32-63 of a trade places with lanes 0-31 of b.  The pair,
+// summed, is a[l] + a[l ^ 32] in lanes 0-31 and b[l] + b[l ^ 32] in lanes 32-63.
+__device__ __forceinline__ float swap32_add(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// x summed / maximised over the 8 neighbour groups (lanes l ^ 8, l ^ 16, l ^ 32)
+__device__ __forceinline__ float group_sum(float x) {
+    x = dpp_add<0x128>(x);  // row_ror:8 within a 16-lane row: lane l ^ 8
+    return xor32_add(swap16_add(x, x));
+}
+__device__ __forceinline__ float group_max(float x) {
+    x = dpp_max<0x128>(x);
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return xor32_max(fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1])));
+}
+
+// c + bf16(a0 * b0) + bf16(a1 * b1): both products rounded to bf16 (one v_cvt_pk_bf16_f32),
+// then added in fp32 by a dot product with (1, 1)
+__device__ __forceinline__ float add_rounded_pair(float a0, float b0, float a1, float b1, float c) {
+    const uint32_t pr = pack_bf16x2(a0 * b0, a1 * b1);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr),
+                                           __builtin_bit_cast(bf16x2_t, 0x3f803f80u), c, false);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
+    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { f[2 * e] = bf_lo(a[e]); f[2 * e + 1] = bf_hi(a[e]); }
+}
+
+template <int NSLOT>
+__global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t pair = (int64_t)xcd_remap(blockIdx.x, gridDim.x) * kInterpWaves + wave;
+    if (pair >= (int64_t)p.S_to * p.H) return;  // wave-uniform; the kernel has no barrier
+    const int s = (int)(pair / p.H), h = (int)(pair - (int64_t)s * p.H);
+    const int K = p.K, dc = lane & 7, jg = lane >> 3;
+
+    // to_q rows h*64 + 8 dc .. + 7 (three bf16 weights each: 48 bytes, 16-byte aligned)
+    float wq[24];
+    {
+        const bf16_t* wr = p.w_q + ((int64_t)h * 64 + 8 * dc) * 3;
+        float t[8];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            unpack8(ld16(wr + 8 * c), t);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wq[8 * c + e] = t[e];
+        }
+    }
+    // per slot: the neighbour's row offsets and this lane's 8 query values,
+    // q[j][d] = bf16(rel[j] . W[h*64 + d]) (fp32 sum of the three bf16 products: the
+    // Linear's bf16 inputs)
+    int64_t koff[NSLOT], voff[NSLOT];
+    float q[NSLOT][8];
+#pragma unroll
+    for (int i = 0; i < NSLOT; ++i) {
+        const int64_t sj = (int64_t)s * K + min(jg + 8 * i, K - 1);
+        // indices outside [0, S_from) are clamped (memory safety; the reference would raise)
+        const int64_t n = min(max(p.neighbors[sj], 0), p.S_from - 1);
+        koff[i] = n * p.k_sn + (int64_t)h * p.k_sh + 8 * dc;
+        voff[i] = n * p.v_sn + (int64_t)h * p.v_sh + 8 * dc;
+        const float r0 = round_bf16(p.rel_pos[3 * sj]), r1 = round_bf16(p.rel_pos[3 * sj + 1]),
+                    r2 = round_bf16(p.rel_pos[3 * sj + 2]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            q[i][e] = round_bf16(fmaf(r2, wq[3 * e + 2], fmaf(r1, wq[3 * e + 1], r0 * wq[3 * e])));
+    }
+    // the output dimension this lane ends up holding after the reduce-scatter
+    const int dout = 8 * dc + 4 * (lane >> 5) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
+    bf16_t* out = p.out + ((int64_t)s * p.B * p.H + h) * 64 + dout;
+
+    uint4 kw[NSLOT], vw[NSLOT], kn[NSLOT], vn[NSLOT];
+#pragma unroll
+    for (int i = 0; i < NSLOT; ++i) { kw[i] = ld16(p.k + koff[i]); vw[i] = ld16(p.v + voff[i]); }
+    for (int b = 0; b < p.B; ++b) {
+        if (b + 1 < p.B) {
+#pragma unroll
+            for (int i = 0; i < NSLOT; ++i) {
+                kn[i] = ld16(p.k + koff[i] + (int64_t)(b + 1) * p.k_sb);
+                vn[i] = ld16(p.v + voff[i] + (int64_t)(b + 1) * p.v_sb);
+            }
+        }
+        // scores of this lane's slots (every lane of a neighbour group holds its score)
+        float sc[NSLOT], m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) {
+            float kf[8];
+            unpack8(kw[i], kf);
+            float part = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part = add_rounded_pair(q[i][2 * e], kf[2 * e], q[i][2 * e + 1], kf[2 * e + 1], part);
+            part = chunk_sum(part);
+            sc[i] = jg + 8 * i < K ? round_bf16(round_bf16(part) * p.scale) : -INFINITY;
+            m = fmaxf(m, sc[i]);
+        }
+        m = group_max(m);
+        float ex[NSLOT], l = 0.f;
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) {
+            ex[i] = jg + 8 * i < K ? __expf(sc[i] - m) : 0.f;
+            l += ex[i];
+        }
+        const float inv = __builtin_amdgcn_rcpf(group_sum(l));
+        // out[d] = sum over slots of bf16(w * v[d]); two slots at a time share one rounding
+        // instruction and one dot-product add.  An absent neighbour (j >= K) has weight 0 and
+        // its row (a duplicate of a present one) is replaced by zeros.
+        float acc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int i = 0; i < NSLOT; i += 2) {
+            float va[8], vb[8];
+            unpack8(vw[i], va);
+            if (jg + 8 * i >= K) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) va[e] = 0.f;
+            }
+            const float wa = round_bf16(ex[i] * inv);
+            if (i + 1 < NSLOT) {
+                unpack8(vw[i + 1], vb);
+                if (jg + 8 * (i + 1) >= K) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) vb[e] = 0.f;
+                }
+                const float wb = round_bf16(ex[i + 1] * inv);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[e] = add_rounded_pair(wa, va[e], wb, vb[e], acc[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const uint32_t pr = pack_bf16x2(wa * va[e], wa * va[e + 1]);
+                    acc[e] += bf_lo(pr);
+                    acc[e + 1] += bf_hi(pr);
+                }
+            }
+        }
+        // reduce-scatter over the 8 neighbour groups: halves (dims e / e + 4), row pairs
+        // (e / e + 2), then lanes l ^ 8 (e / e + 1)
+        float r4[4], r2[2];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r4[e] = swap32_add(acc[e], acc[e + 4]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) r2[e] = swap16_add(r4[e], r4[e + 2]);
+        const bool odd8 = lane & 8;
+        const float keep = odd8 ? r2[1] : r2[0], give = odd8 ? r2[0] : r2[1];
+        const float o = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(give), 0x128, 0xf, 0xf, false));
+        out[(int64_t)b * p.H * 64] = (bf16_t)(pack_bf16x2(o, 0.f) & 0xffffu);
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) { kw[i] = kn[i]; vw[i] = vn[i]; }
+    }
+}
+
+template <int NSLOT>
+hipError_t launch_slots(const InterpParams& p, unsigned wgs, hipStream_t s) {
+    void* args[] = {const_cast<InterpParams*>(&p)};
+    return hipLaunchKernel((const void*)&knn_attn_kernel<NSLOT>, dim3(wgs), dim3(kInterpWaves * 64), args, 0, s);
+}
+
+}  // namespace
+
+hipError_t launch_knn_attn(const InterpParams& p, hipStream_t s) {
+    const int64_t pairs = (int64_t)p.S_to * p.H;
+    const int64_t wgs = (pairs + kInterpWaves - 1) / kInterpWaves;
+    if (wgs <= 0) return hipSuccess;
+    if (wgs > 0x7fffffff) return hipErrorInvalidValue;
+    switch ((p.K + 7) / 8) {
+        case 1: return launch_slots<1>(p, (unsigned)wgs, s);
+        case 2: return launch_slots<2>(p, (unsigned)wgs, s);
+        case 3: return launch_slots<3>(p, (unsigned)wgs, s);
+        case 4: return launch_slots<4>(p, (unsigned)wgs, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mosaic

@@ -1,0 +1,120 @@
+"""k-nearest-neighbour cross-attention interpolation between grids.
+
+Mirrors ``CrossAttentionInterpolate`` (primitives.py:230-283) and its helpers
+``rad_to_xyz`` / ``get_neighbors`` (utils.py:7-17, 33-41).  The gather-attention in the
+middle of the forward runs in libmosaic_bsa.so (``mosaic_knn_interp_fwd``): the queries
+``to_q(rel_pos)`` and the gathered keys / values are never materialised.  The RMSNorm and the
+``to_kv`` / ``to_o`` projections stay torch modules (library GEMMs).  Precision is that of the
+model under bf16 autocast: bf16 projections, fp32 softmax, bf16 output.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .ops import stream_of
+
+
+def rad_to_xyz(lonlat: torch.Tensor) -> torch.Tensor:
+    """(lon, lat) in radians -> unit vectors (utils.py:7-17)."""
+    lon, lat = lonlat[..., 0], lonlat[..., 1]
+    return torch.stack([torch.cos(lat) * torch.cos(lon), torch.cos(lat) * torch.sin(lon), torch.sin(lat)], dim=-1)
+
+
+def get_neighbors(pos_from: np.ndarray, pos_to: np.ndarray, k: int = 8) -> np.ndarray:
+    """Indices [len(pos_to), k] of the k nearest points of ``pos_from`` (both (lon, lat) in
+    radians) by great-circle distance, nearest first: scikit-learn's BallTree with the
+    haversine metric on (lat, lon), as utils.py:33-41 builds it."""
+    from sklearn.neighbors import BallTree
+    tree = BallTree(np.ascontiguousarray(pos_from[:, ::-1]), metric="haversine")
+    _, idx = tree.query(np.ascontiguousarray(pos_to[:, ::-1]), k=k)
+    return idx
+
+
+def _snhd(t: torch.Tensor) -> _lib.Bnhd:
+    # [S, B, H, 64] -> the ABI's (stride_b = member, stride_n = point, stride_h = head)
+    return _lib.Bnhd(t.data_ptr(), t.stride(1), t.stride(0), t.stride(2))
+
+
+def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel_pos: torch.Tensor,
+                  w_q: torch.Tensor, scale: float | None = None) -> torch.Tensor:
+    """The gather-attention of CrossAttentionInterpolate.forward (primitives.py:265-283).
+
+    k, v: [S_from, B, H, 64] (views of the kv projection are fine); neighbors: [S_to, K]
+    source indices; rel_pos: [S_to, K, 3]; w_q: [H*64, 3] (``to_q.weight``).  Returns
+    [S_to, B, H, 64] bf16: for each target, softmax over its K neighbours of
+    ``to_q(rel_pos) . k * scale``, applied to v.
+    """
+    if k.dim() != 4 or k.shape != v.shape or k.shape[-1] != 64:
+        raise ValueError(f"k and v must both be [S_from, B, H, 64], got {tuple(k.shape)} and {tuple(v.shape)}")
+    if k.device.type != "cuda":
+        raise ValueError("k and v must be on a ROCm device")
+    S_from, B, H, d = k.shape
+    S_to, K = neighbors.shape
+    if tuple(rel_pos.shape) != (S_to, K, 3) or tuple(w_q.shape) != (H * d, 3):
+        raise ValueError("rel_pos must be [S_to, K, 3] and w_q [H*64, 3]")
+
+    def prep(t):
+        t = t.to(torch.bfloat16)
+        if t.stride(-1) != 1 or t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:3]):
+            t = t.contiguous()
+        return t
+    k, v = prep(k), prep(v)
+    nb = neighbors.to(device=k.device, dtype=torch.int32).contiguous()
+    rp = rel_pos.to(device=k.device, dtype=torch.float32).contiguous()
+    wq = w_q.to(device=k.device, dtype=torch.bfloat16).contiguous()
+    out = torch.empty(S_to, B, H, d, dtype=torch.bfloat16, device=k.device)
+    st = _lib.lib().mosaic_knn_interp_fwd(_snhd(k), _snhd(v), nb.data_ptr(), rp.data_ptr(), wq.data_ptr(),
+                                          S_from, S_to, B, H, d, K, 0.0 if scale is None else float(scale),
+                                          out.data_ptr(), stream_of(k))
+    _lib.check(st, "mosaic_knn_interp_fwd")
+    return out
+
+
+class CrossAttentionInterpolate(nn.Module):
+    """Cross-attention from one grid to another over k nearest neighbours (primitives.py:230-283).
+
+    ``config`` needs: k_neighbors, dim, num_heads, rmsnorm_elementwise_affine.  x_from is
+    sequence-first [S_from, B, dim]; the output is [S_to, B, dim].
+    """
+
+    space_dim = 3
+
+    def __init__(self, config):
+        super().__init__()
+        self.k_neighbors = config.k_neighbors
+        dim, num_heads = config.dim, config.num_heads
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.kv_norm = nn.RMSNorm(dim, elementwise_affine=config.rmsnorm_elementwise_affine)
+        self.to_q = nn.Linear(self.space_dim, dim, bias=False)
+        self.to_kv = nn.Linear(dim, 2 * dim, bias=False)
+        self.to_o = nn.Linear(dim, dim, bias=False)
+        self.register_buffer("neighbors", None, persistent=True)
+        self.register_buffer("rel_pos", None, persistent=True)
+
+    @torch.no_grad()
+    def initialize_interpolation_scheme(self, pos_from_rad: torch.Tensor, pos_to_rad: torch.Tensor):
+        """Neighbours and normalised relative positions of every target (primitives.py:250-263)."""
+        nbrs = get_neighbors(pos_from_rad.cpu().numpy(), pos_to_rad.cpu().numpy(), k=self.k_neighbors)
+        neighbors = torch.from_numpy(nbrs).long().to(pos_from_rad.device).contiguous()
+        to_xyz, from_xyz = rad_to_xyz(pos_to_rad), rad_to_xyz(pos_from_rad)
+        rel = (to_xyz.unsqueeze(1) - from_xyz[neighbors]).contiguous()
+        self.neighbors = neighbors
+        self.rel_pos = torch.nn.functional.normalize(rel, dim=-1).contiguous()
+
+    def forward(self, x_from: torch.Tensor) -> torch.Tensor:
+        if self.neighbors is None or self.rel_pos is None:
+            raise ValueError("Interpolation scheme not initialized.")
+        S_from, B, dim = x_from.shape
+        kv = self.to_kv(self.kv_norm(x_from))
+        k = kv[..., :dim].unflatten(-1, (self.num_heads, self.head_dim))
+        v = kv[..., dim:].unflatten(-1, (self.num_heads, self.head_dim))
+        out = knn_attention(k, v, self.neighbors, self.rel_pos, self.to_q.weight, self.scale)
+        return self.to_o(out.to(x_from.dtype).flatten(-2))

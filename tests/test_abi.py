@@ -124,3 +124,20 @@ def test_other_entry_points_validate():
     # scores [1, 5, 48, 64] bf16, then k_cmp in operand order [1, 5, 64 (padded blocks), 64] bf16
     align = lambda n: (n + 255) // 256 * 256
     assert L.mosaic_attn_topk_workspace_size(1, 48, 5) == align(5 * 48 * 64 * 2) + align(5 * 64 * 64 * 2)
+
+
+def test_knn_interp_entry_validates():
+    L = _lib.lib()
+    t = _lib.Bnhd(FAKE, 3 * 64, 2 * 3 * 64, 64)   # [S_from, B=2, H=3, 64]
+    ok = dict(num_from=84, num_to=48, batch=2, heads=3, d=64, K=24)
+
+    def call(kk=t, nb=FAKE, rel=FAKE, wq=FAKE, out=FAKE, **kw):
+        a = {**ok, **kw}
+        return L.mosaic_knn_interp_fwd(kk, t, nb, rel, wq, a["num_from"], a["num_to"], a["batch"], a["heads"],
+                                       a["d"], a["K"], 0.0, out, None)
+    assert call(nb=None) == 1 and call(rel=None) == 1 and call(wq=None) == 1 and call(out=None) == 1
+    assert call(d=32) == 2
+    assert call(K=0) == 5 and call(K=33) == 5
+    assert call(num_to=0) == 8 and call(batch=-1) == 8
+    assert call(wq=FAKE + 8) == 7 and call(out=FAKE + 2) == 7 and call(rel=FAKE + 2) == 7
+    assert call(kk=_lib.Bnhd(FAKE + 2, 3 * 64, 2 * 3 * 64, 64)) == 7

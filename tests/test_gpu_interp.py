@@ -1,0 +1,149 @@
+"""GPU parity of the k-nearest-neighbour cross-attention (CrossAttentionInterpolate's
+gather-attention, primitives.py:265-283) against the CPU oracle (marked ``gpu``).
+
+Bars: max-abs 2e-2 and relative L2 1e-2 (bf16 in, fp32 accumulate); the kernel rounds where
+the reference's elementwise bf16 tensor ops round, so nearly every output is bit-equal to the
+oracle's (sums in another order and the exponential's last fp32 bits aside): at least 97% of
+the elements must be.
+"""
+
+import pytest
+import torch
+
+from mosaic_amd.healpix import get_healpix_grid
+from mosaic_amd.interp import CrossAttentionInterpolate, get_neighbors, knn_attention, rad_to_xyz
+from oracle import interp_oracle as IO
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+MAX_ABS = 2e-2
+REL_L2 = 1e-2
+
+
+def close(got, ref, min_equal=0.97):
+    g, r = got.float().cpu(), ref.float().cpu()
+    assert g.shape == r.shape, (g.shape, r.shape)
+    assert torch.isfinite(g).all(), "non-finite output"
+    err = (g - r).abs().max().item()
+    rel = ((g - r).norm() / r.norm().clamp_min(1e-30)).item()
+    eq = (got.cpu() == ref.cpu()).float().mean().item()
+    assert err <= MAX_ABS and rel <= REL_L2 and eq >= min_equal, f"max_abs {err:.3e} rel_l2 {rel:.3e} equal {eq:.4f}"
+
+
+def lonlat_grid(n_lon, n_lat):
+    lon = torch.linspace(0, 360 - 360 / n_lon, n_lon)
+    lat = torch.linspace(-90, 90, n_lat)
+    return torch.deg2rad(torch.stack(torch.meshgrid(lon, lat, indexing="ij"), -1).reshape(-1, 2))
+
+
+def scheme(pos_from, pos_to, K):
+    nb = torch.from_numpy(get_neighbors(pos_from.numpy(), pos_to.numpy(), k=K)).long()
+    rel = rad_to_xyz(pos_to).unsqueeze(1) - rad_to_xyz(pos_from)[nb]
+    return nb, torch.nn.functional.normalize(rel, dim=-1)
+
+
+def rand(*shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
+@pytest.mark.parametrize("K", [24, 20, 7, 1])
+def test_knn_attention_matches_oracle(direction, K):
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))    # 312 and 192 points
+    src, dst = (ll, hp) if direction == "ll_to_hp" else (hp, ll)
+    nb, rel = scheme(src, dst, K)
+    B, H = 2, 3
+    k, v = rand(len(src), B, H, 64, seed=K), rand(len(src), B, H, 64, seed=K + 100)
+    w_q = rand(H * 64, 3, seed=K + 200, scale=2.0)
+    ref = IO.knn_attention(k, v, nb, rel, w_q, 0.125)
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
+    torch.cuda.synchronize()
+    if K == 1:
+        assert torch.equal(got.cpu(), v[nb[:, 0]])
+    close(got, ref)
+
+
+def test_knn_attention_zero_queries_and_large_scores():
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(ll, hp, 24)
+    k, v = rand(len(ll), 1, 4, 64, seed=1, scale=3.0), rand(len(ll), 1, 4, 64, seed=2)
+    for w_q, scale in ((torch.zeros(4 * 64, 3, dtype=torch.bfloat16), 0.125), (rand(4 * 64, 3, seed=3, scale=4.0), 1.0)):
+        ref = IO.knn_attention(k, v, nb, rel, w_q, scale)
+        got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), scale)
+        close(got, ref)
+
+
+def test_knn_attention_strided_views_equal_contiguous():
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(hp, ll, 20)
+    S, B, H = len(hp), 3, 2
+    kv = rand(S, B, 2 * H * 64, seed=4).to(DEV)              # the to_kv output layout
+    k = kv[..., :H * 64].unflatten(-1, (H, 64))
+    v = kv[..., H * 64:].unflatten(-1, (H, 64))
+    w_q = rand(H * 64, 3, seed=5).to(DEV)
+    a = knn_attention(k, v, nb.to(DEV), rel.to(DEV), w_q, 0.125)
+    b = knn_attention(k.contiguous(), v.contiguous(), nb.to(DEV), rel.to(DEV), w_q, 0.125)
+    assert torch.equal(a, b)
+    close(a, IO.knn_attention(k.cpu(), v.cpu(), nb, rel, w_q.cpu(), 0.125))
+
+
+@pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
+def test_knn_attention_full_size_sampled(direction):
+    """Model grids: 121 x 240 lat-lon (29040 points) and HEALPix nside 64 (49152), K 24,
+    12 heads; every target computed on the device, a sample of targets against the oracle."""
+    ll, hp = lonlat_grid(240, 121), torch.deg2rad(get_healpix_grid(64))
+    src, dst = (ll, hp) if direction == "ll_to_hp" else (hp, ll)
+    K, B, H = 24, 2, 12
+    nb, rel = scheme(src, dst, K)
+    k, v = rand(len(src), B, H, 64, seed=7), rand(len(src), B, H, 64, seed=8)
+    w_q = rand(H * 64, 3, seed=9)
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125).cpu()
+    g = torch.Generator().manual_seed(10)
+    sample = torch.cat([torch.arange(64), len(dst) - 64 + torch.arange(64),
+                        torch.randint(0, len(dst), (1024,), generator=g)])
+    ref = IO.knn_attention(k, v, nb[sample], rel[sample], w_q, 0.125)
+    close(got[sample], ref)
+
+
+def test_knn_attention_deterministic():
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = [t.to(DEV) for t in scheme(ll, hp, 24)]
+    k, v = rand(len(ll), 2, 3, 64, seed=11).to(DEV), rand(len(ll), 2, 3, 64, seed=12).to(DEV)
+    w_q = rand(3 * 64, 3, seed=13).to(DEV)
+    a = knn_attention(k, v, nb, rel, w_q, 0.125)
+    assert all(torch.equal(a, knn_attention(k, v, nb, rel, w_q, 0.125)) for _ in range(3))
+
+
+def test_cross_attention_interpolate_module():
+    from types import SimpleNamespace
+    cfg = SimpleNamespace(k_neighbors=20, dim=192, num_heads=3, rmsnorm_elementwise_affine=True)
+    torch.manual_seed(0)
+    m = CrossAttentionInterpolate(cfg)
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    m.initialize_interpolation_scheme(ll, hp)
+    m = m.to(DEV).to(torch.bfloat16)
+    x = torch.randn(len(ll), 2, 192, device=DEV).to(torch.bfloat16)
+    y = m(x)
+    # the same torch projections around the oracle's gather-attention
+    with torch.no_grad():
+        kv = m.to_kv(m.kv_norm(x))
+        k = kv[..., :192].unflatten(-1, (3, 64)).cpu()
+        v = kv[..., 192:].unflatten(-1, (3, 64)).cpu()
+        att = IO.knn_attention(k, v, m.neighbors.cpu(), m.rel_pos.float().cpu(), m.to_q.weight.cpu(), m.scale)
+        ref = m.to_o(att.to(DEV).flatten(-2))
+    assert y.shape == (len(hp), 2, 192)
+    close(y, ref, min_equal=0.9)
+
+
+def test_knn_attention_random_neighbour_lists():
+    """Neighbour lists with no spatial structure (repeats allowed), K = 13 (a partial slot)."""
+    S_from, S_to, K = 2000, 160, 13
+    g = torch.Generator().manual_seed(30)
+    nb = torch.randint(0, S_from, (S_to, K), generator=g)
+    rel = torch.nn.functional.normalize(torch.randn(S_to, K, 3, generator=g), dim=-1)
+    k, v = rand(S_from, 2, 2, 64, seed=31), rand(S_from, 2, 2, 64, seed=32)
+    w_q = rand(2 * 64, 3, seed=33)
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
+    close(got, IO.knn_attention(k, v, nb, rel, w_q, 0.125))

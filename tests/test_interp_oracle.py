@@ -1,0 +1,133 @@
+"""Pinning of the k-NN cross-attention oracle (CPU): closed forms, a float64 brute force, an
+invariance, and the neighbour search against a brute-force great-circle search."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from mosaic_amd.healpix import get_healpix_grid
+from mosaic_amd.interp import get_neighbors, rad_to_xyz
+from oracle import interp_oracle as IO
+
+
+def _grids():
+    hp = torch.deg2rad(get_healpix_grid(2))                               # 48 points
+    lon = torch.linspace(0, 330, 12)
+    lat = torch.linspace(-90, 90, 7)
+    ll = torch.deg2rad(torch.stack(torch.meshgrid(lon, lat, indexing="ij"), -1).reshape(-1, 2))   # 84 points
+    return ll, hp
+
+
+def _scheme(pos_from, pos_to, K):
+    nb = torch.from_numpy(get_neighbors(pos_from.numpy(), pos_to.numpy(), k=K)).long()
+    rel = rad_to_xyz(pos_to).unsqueeze(1) - rad_to_xyz(pos_from)[nb]
+    return nb, torch.nn.functional.normalize(rel, dim=-1)
+
+
+def _kv(S, B, H, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(S, B, H, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(S, B, H, 64, generator=g).to(torch.bfloat16)
+    return k, v
+
+
+def test_rad_to_xyz_known_points():
+    pts = torch.tensor([[0.0, 0.0], [math.pi / 2, 0.0], [0.3, math.pi / 2], [math.pi, -math.pi / 2]])
+    xyz = rad_to_xyz(pts)
+    ref = torch.tensor([[1.0, 0.0, 0.0], [0.0, 1.0, 0.0], [0.0, 0.0, 1.0], [0.0, 0.0, -1.0]])
+    torch.testing.assert_close(xyz, ref, atol=1e-6, rtol=0)
+    ll, _ = _grids()
+    torch.testing.assert_close(rad_to_xyz(ll).norm(dim=-1), torch.ones(len(ll)), atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
+def test_neighbours_match_brute_force(direction):
+    ll, hp = _grids()
+    src, dst = (ll, hp) if direction == "ll_to_hp" else (hp, ll)
+    K = 8
+    got = torch.from_numpy(get_neighbors(src.numpy(), dst.numpy(), k=K)).long()
+    ref = IO.great_circle_knn(src, dst, K + 1)
+
+    def ang(idx):
+        a = rad_to_xyz(dst.double()).unsqueeze(1)
+        b = rad_to_xyz(src.double())[idx]
+        return torch.acos((a * b).sum(-1).clamp(-1, 1))
+    # the same distances (equidistant points may be listed in another order), nearest first
+    torch.testing.assert_close(ang(got), ang(ref[:, :K]), atol=1e-9, rtol=0)
+    assert (ang(got).diff(dim=1) >= -1e-12).all()
+    # where the k-th and (k+1)-th distances differ, the neighbour sets are equal
+    clear = (ang(ref)[:, K] - ang(ref)[:, K - 1]) > 1e-9
+    for r in torch.nonzero(clear).flatten().tolist():
+        assert set(got[r].tolist()) == set(ref[r, :K].tolist())
+
+
+def test_single_neighbour_returns_its_value():
+    ll, hp = _grids()
+    nb, rel = _scheme(ll, hp, 1)
+    k, v = _kv(len(ll), 2, 3, seed=1)
+    w_q = torch.randn(3 * 64, 3).to(torch.bfloat16)
+    out = IO.knn_attention(k, v, nb, rel, w_q, 0.125)
+    assert torch.equal(out, v[nb[:, 0]])
+
+
+def test_zero_queries_give_the_mean():
+    ll, hp = _grids()
+    K = 20
+    nb, rel = _scheme(ll, hp, K)
+    k, v = _kv(len(ll), 2, 2, seed=2)
+    out = IO.knn_attention(k, v, nb, rel, torch.zeros(2 * 64, 3), 0.125).double()
+    mean = v.double()[nb].mean(dim=1)
+    assert (out - mean).abs().max().item() <= 2 ** -7 * v.double().abs().max().item()
+
+
+@pytest.mark.parametrize("K", [7, 24])
+def test_matches_float64_brute_force(K):
+    ll, hp = _grids()
+    nb, rel = _scheme(ll, hp, K)
+    H = 2
+    k, v = _kv(len(ll), 2, H, seed=3)
+    w_q = (torch.randn(H * 64, 3, generator=torch.Generator().manual_seed(4)) * 0.6).to(torch.bfloat16)
+    scale = 64 ** -0.5
+    out = IO.knn_attention(k, v, nb, rel, w_q, scale).double()
+    ref = torch.zeros_like(out)
+    W = w_q.double()
+    for t in range(len(hp)):
+        for h in range(H):
+            q = rel[t].double() @ W[h * 64:(h + 1) * 64].t()                 # [K, 64]
+            for b in range(2):
+                s = (q * k.double()[nb[t], b, h]).sum(-1) * scale            # [K]
+                p = torch.softmax(s, dim=0)
+                ref[t, b, h] = (p[:, None] * v.double()[nb[t], b, h]).sum(0)
+    err = (out - ref).abs().max().item()
+    assert err <= 2e-2, err
+    assert ((out - ref).norm() / ref.norm()).item() <= 1e-2
+
+
+def test_neighbour_order_does_not_matter():
+    ll, hp = _grids()
+    K = 12
+    nb, rel = _scheme(ll, hp, K)
+    k, v = _kv(len(ll), 1, 2, seed=5)
+    w_q = torch.randn(2 * 64, 3, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(7))
+    a = IO.knn_attention(k, v, nb, rel, w_q, 0.125).float()
+    b = IO.knn_attention(k, v, nb[:, perm], rel[:, perm], w_q, 0.125).float()
+    # the fp32 sums add in another order: at most one bf16 spacing apart
+    assert ((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2 ** -7 + 1e-6).all()
+
+
+def test_module_scheme_on_cpu():
+    from types import SimpleNamespace
+    from mosaic_amd.interp import CrossAttentionInterpolate
+    m = CrossAttentionInterpolate(SimpleNamespace(k_neighbors=8, dim=128, num_heads=2, rmsnorm_elementwise_affine=True))
+    with pytest.raises(ValueError):
+        m(torch.zeros(84, 1, 128))
+    ll, hp = _grids()
+    m.initialize_interpolation_scheme(ll, hp)
+    nb, rel = _scheme(ll, hp, 8)
+    assert torch.equal(m.neighbors, nb) and torch.equal(m.rel_pos, rel)
+    assert set(m.state_dict()) >= {"neighbors", "rel_pos"}
+    with pytest.raises(ValueError):   # the gather-attention runs on the device only
+        m(torch.zeros(84, 1, 128))
