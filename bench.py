@@ -17,7 +17,9 @@ attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v), --
 times the op with the input side's RoPE fused into its pooling pass, mosaic_bsa_fwd_rope,
 against eager torch RoPE followed by the op, both on unrotated q/k), --interp (also times the
 k-nearest-neighbour cross-attention between the model's lat-lon and HEALPix grids,
-mosaic_knn_interp_fwd, at --interp-batch members).
+mosaic_knn_interp_fwd, at --interp-batch members).  Unless --no-unet, the line also carries
+one forecast step of the full U-Net at --unet-members ensemble members (default 24:
+``unet_24_member_step_ms``, the metric's second half); --unet-only times only that step.
 """
 
 from __future__ import annotations
@@ -232,6 +234,55 @@ def interp_leg(L, args, dev, stream):
     return res
 
 
+def unet_leg(args, dev):
+    """One forecast step of the full U-Net (mosaic.py:304-337) with the shipped era5 preset
+    (inference.py:71-103, 286-302; 214,184,448 parameters, random init as the model initialises
+    itself): input [1, 1, 2, 240, 121, 82] fp32 N(0,1) on the 1.5-degree lat-lon grid, 3 static
+    fields, ``--unet-members`` noise samples (ensemble members), bf16 autocast, no grad.  Every
+    attention layer runs the block-sparse op (local 1024, sparse blocks 128, top-24/12/4), both
+    grid interpolations the k-NN kernel; the projections are library GEMMs."""
+    from mosaic_amd.model import Transformer, era5_config, model_flops
+    cfg = era5_config()
+    torch.manual_seed(args.seed)
+    t0 = time.perf_counter()
+    model = Transformer(cfg)
+    lon = torch.linspace(0, 358.5, 240)
+    lat = torch.linspace(-90, 90, 121)
+    model.initialize_interpolation(lon, lat)
+    g = torch.Generator().manual_seed(args.seed)
+    model.initialize_static_vars(torch.randn(240, 121, 3, generator=g), lon, lat)
+    model = model.to(dev).eval()
+    setup_s = time.perf_counter() - t0
+    x = torch.randn(1, 1, 2, 240, 121, 82, generator=g).to(dev)
+    dyt = torch.rand(1, 1, 2, generator=g).to(dev)
+    S = args.unet_members
+    stream = torch.cuda.current_stream(dev)
+
+    def step():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(x, dyt, S)
+
+    for _ in range(args.unet_warmup):
+        out = step()
+    torch.cuda.synchronize()
+    print(f"unet: warm-up done ({args.unet_warmup} steps)", file=sys.stderr, flush=True)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.unet_steps):
+        out = step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.unet_steps
+    fl = model_flops(cfg, S, 240 * 121)
+    return {"ms_per_step": round(ms, 2), "members": S, "steps": args.unet_steps, "warmup": args.unet_warmup,
+            "tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(fl["total"] / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "flops": fl, "params": sum(p.numel() for p in model.parameters()),
+            "output_shape": list(out.shape), "output_finite": bool(torch.isfinite(out).all().item()),
+            "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 1e9, 1), "setup_s": round(setup_s, 1),
+            "data": "synthetic N(0,1) input and static fields, random-init weights (no checkpoint offline)"}
+
+
 def cpu_baseline(wl, q, k, v, w):
     """The CPU oracle (torch restatement of the reference path) on the full workload."""
     from oracle import bsa_oracle as O
@@ -275,6 +326,11 @@ def main():
     ap.add_argument("--rope-fused", action="store_true")
     ap.add_argument("--interp", action="store_true")
     ap.add_argument("--interp-batch", type=int, default=24)
+    ap.add_argument("--no-unet", action="store_true", help="skip the 24-member U-Net step")
+    ap.add_argument("--unet-only", action="store_true", help="time only the U-Net step (prints its JSON)")
+    ap.add_argument("--unet-members", type=int, default=24)
+    ap.add_argument("--unet-steps", type=int, default=3)
+    ap.add_argument("--unet-warmup", type=int, default=1)
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")
@@ -292,6 +348,9 @@ def main():
 
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
+    if args.unet_only:
+        print(json.dumps({"unet": unet_leg(args, dev)}))
+        return
     q_c, k_c, v_c, w_c = make_inputs(wl, seed=args.seed)
     q, k, v, w = (t.to(dev) for t in (q_c, k_c, v_c, w_c))
     w4 = w[..., 0]
@@ -408,6 +467,10 @@ def main():
         result["rope_fused"] = rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream)
     if args.interp:
         result["knn_interp"] = interp_leg(L, args, dev, stream)
+    if not args.no_unet:
+        leg = unet_leg(args, dev)
+        result["unet_24_member_step_ms"] = leg["ms_per_step"] if leg["members"] == 24 else None
+        result["unet"] = leg
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, q_c, k_c, v_c, w_c)
     print(json.dumps(result))

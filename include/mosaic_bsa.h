@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 1
+#define MOSAIC_BSA_ABI_VERSION 2
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -54,6 +54,12 @@ typedef enum {
                                       (o_ba*w0 + o_cmp*w1) / (w0+w1+1e-8)    (:80-84) */
 } mosaic_bsa_mode;
 
+/* Element types of the model-level elementwise entry points. */
+typedef enum {
+    MOSAIC_DTYPE_F32 = 0,
+    MOSAIC_DTYPE_BF16 = 1
+} mosaic_dtype;
+
 /* A bf16 [B, N, H, 64] tensor: element strides of b, n and h; head_dim stride is 1. */
 typedef struct {
     const void* ptr;
@@ -80,8 +86,13 @@ typedef struct {
        (may be NULL) in MOSAIC_BSA_LOCAL_ONLY mode. */
     const void* weights;
     int64_t w_stride_s, w_stride_b, w_stride_n, w_stride_h;
-    void* out;                     /* bf16 [B, N, Hq, 64], contiguous                        */
+    void* out;                     /* bf16 [B, N, Hq, 64]; heads and head_dim contiguous     */
     int64_t* block_indices_out;    /* optional: int64 [B, N/bs, Hk, K] selected blocks       */
+    /* Element strides of out's batch and token dimensions; 0 selects the contiguous
+       N*Hq*64 / Hq*64.  A caller whose next step wants sequence-first rows ([N, B, Hq*64],
+       the reference's 'b s h d -> s b (h d)' before to_o, primitives.py:207) passes
+       out_stride_b = Hq*64 and out_stride_n = B*Hq*64.  Multiples of 8, 16-byte rows. */
+    int64_t out_stride_b, out_stride_n;
 } mosaic_bsa_args;
 
 /* Bytes of device workspace mosaic_bsa_fwd needs for these arguments (256-byte aligned). */
@@ -173,6 +184,31 @@ MOSAIC_API int mosaic_attn_topk_fwd(mosaic_bnhd q_cmp, mosaic_bnhd k_cmp, int32_
                          int32_t num_blocks, int32_t num_q_heads, int32_t num_kv_heads,
                          int32_t head_dim, int32_t block_count, int64_t* indices_out,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Row-wise RMSNorm, optionally after a residual add.  Replaces torch.nn.RMSNorm as the model
+   calls it (MosaicBlock.norm1 / norm2, primitives.py:220-226; the U-Net's pre/post-processing
+   and resampling norms, mosaic.py:163-217, primitives.py:313-359) and, with residual != NULL,
+   the add in front of it (x + attention(...), primitives.py:225):
+     y = x + residual      rounded to dtype (written to sum_out, contiguous [rows, cols])
+     out = y * rsqrt(mean(y^2) + eps) * weight      fp32 statistics, rounded once to out_dtype
+   x, residual: dtype rows of cols contiguous elements, rows x_row_stride / residual_row_stride
+   elements apart; out: out_dtype [rows, cols] contiguous; weight: optional fp32 [cols].
+   cols a multiple of 8, at most 4096; pointers 16-byte aligned. */
+MOSAIC_API int mosaic_rms_norm_fwd(const void* x, const void* residual, int32_t dtype, int64_t rows,
+                                   int32_t cols, int64_t x_row_stride, int64_t residual_row_stride,
+                                   const float* weight, float eps, void* sum_out, void* out,
+                                   int32_t out_dtype, void* stream);
+
+/* The SwiGLU gate of cSwiGLU.forward (primitives.py:102-105): with x1 = h[:, :hidden] and
+   x3 = h[:, hidden:2*hidden], out = silu(x1 + noise[row % noise_rows]) * x3, each of the
+   add, the silu and the product rounded to dtype as the reference's eager ops round.
+   h: dtype [rows, >= 2*hidden] with row stride h_row_stride; noise: optional dtype
+   [noise_rows, hidden] contiguous (the noise_bias(z) rows, one per batch member of a
+   sequence-first [S, B, .] activation); out: dtype [rows, hidden] contiguous.  hidden a
+   multiple of 8; pointers 16-byte aligned. */
+MOSAIC_API int mosaic_swiglu_fwd(const void* h, int32_t dtype, int64_t rows, int32_t hidden,
+                                 int64_t h_row_stride, const void* noise, int32_t noise_rows, void* out,
+                                 void* stream);
 
 /* Name of a status code (static storage). */
 MOSAIC_API const char* mosaic_bsa_strerror(int status);

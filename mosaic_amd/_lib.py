@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # mosaic_bsa_mode
 MODE_FULL = 0
@@ -20,12 +20,18 @@ MODE_LOCAL_ONLY = 1
 MODE_NO_COMPRESSION = 2
 MODE_NO_SELECTION = 3
 
+# mosaic_dtype
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+
 EXPORTED_SYMBOLS = (
     "mosaic_bsa_workspace_size",
     "mosaic_bsa_fwd",
     "mosaic_bsa_fwd_profiled",
     "mosaic_bsa_fwd_rope",
     "mosaic_knn_interp_fwd",
+    "mosaic_rms_norm_fwd",
+    "mosaic_swiglu_fwd",
     "mosaic_sparse_attn_fwd",
     "mosaic_block_attn_fwd",
     "mosaic_dense_attn_fwd",
@@ -59,6 +65,7 @@ class BsaArgs(ctypes.Structure):
         ("w_stride_n", ctypes.c_int64), ("w_stride_h", ctypes.c_int64),
         ("out", ctypes.c_void_p),
         ("block_indices_out", ctypes.c_void_p),
+        ("out_stride_b", ctypes.c_int64), ("out_stride_n", ctypes.c_int64),
     ]
 
 
@@ -80,6 +87,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_knn_interp_fwd.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                           c_f, c_vp, c_vp]
     lib.mosaic_knn_interp_fwd.restype = c_int
+    c_i64 = ctypes.c_int64
+    lib.mosaic_rms_norm_fwd.argtypes = [c_vp, c_vp, c_i32, c_i64, c_i32, c_i64, c_i64, c_vp, c_f, c_vp, c_vp,
+                                        c_i32, c_vp]
+    lib.mosaic_rms_norm_fwd.restype = c_int
+    lib.mosaic_swiglu_fwd.argtypes = [c_vp, c_i32, c_i64, c_i32, c_i64, c_vp, c_i32, c_vp, c_vp]
+    lib.mosaic_swiglu_fwd.restype = c_int
     lib.mosaic_sparse_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
                                            c_i32, c_i32, c_f, c_vp, c_vp, c_vp]
     lib.mosaic_sparse_attn_fwd.restype = c_int

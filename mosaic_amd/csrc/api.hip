@@ -72,6 +72,8 @@ int validate(const mosaic_bsa_args* a) {
     if (int e = check_bnhd(a->v)) return e;
     if (a->out == nullptr) return MOSAIC_ERR_NULL_POINTER;
     if (!aligned16(a->out)) return MOSAIC_ERR_ALIGNMENT;
+    if (a->out_stride_b < 0 || a->out_stride_n < 0 || a->out_stride_b % 8 || a->out_stride_n % 8)
+        return MOSAIC_ERR_ALIGNMENT;
     if ((int64_t)a->batch * a->seq_len * a->num_q_heads * kHeadDim >= ((int64_t)1 << 40)) return MOSAIC_ERR_SHAPE;
     if (a->block_attn_size <= 0 || a->block_attn_size % kTile || a->seq_len % a->block_attn_size)
         return MOSAIC_ERR_BLOCK_SIZE;
@@ -172,6 +174,8 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
 
     AttnParams ap = attn_params(a->q, a->k, a->v, B, N, Hq, Hk, scale);
     ap.out = static_cast<bf16_t*>(a->out);
+    ap.out_sb = a->out_stride_b ? a->out_stride_b : (int64_t)N * Hq * kHeadDim;
+    ap.out_sn = a->out_stride_n ? a->out_stride_n : (int64_t)Hq * kHeadDim;
     ap.bs_l = a->block_attn_size;
     ap.bs = a->mode == MOSAIC_BSA_LOCAL_ONLY ? kTile : a->sparse_block_size;
     ap.K = a->sparse_block_count;
@@ -312,6 +316,8 @@ int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const in
     AttnParams ap = attn_params(q, k, v, batch, seq_len, num_q_heads, num_kv_heads,
                                 resolve_scale(softmax_scale, head_dim));
     ap.out = static_cast<bf16_t*>(out);
+    ap.out_sb = (int64_t)seq_len * num_q_heads * kHeadDim;
+    ap.out_sn = (int64_t)num_q_heads * kHeadDim;
     ap.lse = lse;
     ap.idx = block_indices;
     ap.bs = block_size;

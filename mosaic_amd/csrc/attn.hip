@@ -488,7 +488,7 @@ void bsa_attn_kernel(AttnParams p) {
         issue_next(bufc, t);
     };
 
-    bf16_t* outp = p.out + ((int64_t)b * p.N + n0) * p.Hq * kHeadDim + (int64_t)j * kHeadDim;
+    bf16_t* outp = p.out + (int64_t)b * p.out_sb + (int64_t)n0 * p.out_sn + (int64_t)j * kHeadDim;
 
     // ------------------------------------------------------------------ local branch
     if constexpr (kLocal) {
@@ -590,7 +590,7 @@ void bsa_attn_kernel(AttnParams p) {
                             uint2 w2;
                             w2.x = pack_bf16x2(o[dt][qt][4 * g4 + 0] * f[qt], o[dt][qt][4 * g4 + 1] * f[qt]);
                             w2.y = pack_bf16x2(o[dt][qt][4 * g4 + 2] * f[qt], o[dt][qt][4 * g4 + 3] * f[qt]);
-                            *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                            *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.out_sn + 32 * dt + 8 * g4 + 4 * hh) = w2;
                         }
                 return;
             } else if constexpr (kPartial) {
@@ -792,7 +792,7 @@ void bsa_attn_kernel(AttnParams p) {
                     uint2 w2;
                     w2.x = pack_bf16x2(o[dt][qt][4 * g4 + 0] * inv[qt], o[dt][qt][4 * g4 + 1] * inv[qt]);
                     w2.y = pack_bf16x2(o[dt][qt][4 * g4 + 2] * inv[qt], o[dt][qt][4 * g4 + 3] * inv[qt]);
-                    *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                    *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.out_sn + 32 * dt + 8 * g4 + 4 * hh) = w2;
                 }
         if (p.lse != nullptr && hh == 0) {
 #pragma unroll
@@ -857,7 +857,7 @@ void bsa_attn_kernel(AttnParams p) {
                     if constexpr (kPartial)  // back into this lane's own Part slot, stored below
                         *reinterpret_cast<uint2*>(pp + (32 * qt + r) * PS + 32 * dt + 8 * g4 + 4 * hh) = w2;
                     else
-                        *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.Hq * kHeadDim + 32 * dt + 8 * g4 + 4 * hh) = w2;
+                        *reinterpret_cast<uint2*>(outp + (int64_t)(32 * qt + r) * p.out_sn + 32 * dt + 8 * g4 + 4 * hh) = w2;
                 }
         if constexpr (kPartial) {
             // Row-major read-back: lane l stores 16 bytes at chunk l % 8 of row l / 8 (+ 8 i),
@@ -872,7 +872,7 @@ void bsa_attn_kernel(AttnParams p) {
                 const int row = 8 * i + rr;
                 const uint2 lo = *reinterpret_cast<const uint2*>(pp + row * PS + cc);
                 const uint2 hi = *reinterpret_cast<const uint2*>(pp + row * PS + cc + 4);
-                *reinterpret_cast<uint4*>(outp + (int64_t)row * p.Hq * kHeadDim + cc) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                *reinterpret_cast<uint4*>(outp + (int64_t)row * p.out_sn + cc) = make_uint4(lo.x, lo.y, hi.x, hi.y);
             }
         }
     }

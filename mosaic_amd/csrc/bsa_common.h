@@ -206,7 +206,8 @@ struct AttnParams {
     const bf16_t* k; int64_t k_sb, k_sn, k_sh;
     const bf16_t* v; int64_t v_sb, v_sn, v_sh;
     const bf16_t* w; int64_t w_ss, w_sb, w_sn, w_sh;
-    bf16_t* out;             // [B, N, Hq, 64]
+    bf16_t* out;             // [B, N, Hq, 64], heads contiguous
+    int64_t out_sb, out_sn;  // element strides of out's batch and token dimensions
     float* lse;              // [B, N, Hq] (selected-only mode, optional)
     const void* idx;         // [B, nb, Hk, K] int32 or int64
     const bf16_t* ocmp;      // compressed-branch output [B, nb, Hq, 64]

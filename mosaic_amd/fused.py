@@ -1,0 +1,130 @@
+"""The model's row-wise elementwise work as single HIP passes (libmosaic_bsa.so).
+
+* ``rms_norm(x, weight, eps, out_dtype, residual=None)``: torch.nn.RMSNorm over the last
+  dimension, optionally after ``x + residual`` (returned too), as MosaicBlock applies them
+  (primitives.py:220-226).
+* ``RMSNorm``: ``torch.nn.RMSNorm`` (same parameters) running ``rms_norm`` on a ROCm device,
+  with ``add_forward`` for the residual-add variant.
+* ``swiglu(h, noise)``: the gate ``silu(x1 + noise) * x3`` of cSwiGLU (primitives.py:102-105).
+
+Inputs must be on a ROCm device; there is no CPU path.  ``autocast_dtype`` reports the dtype
+torch's own RMSNorm returns under the current autocast state, so the fused norm's output has
+the dtype the reference's module would have.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .ops import stream_of
+
+__all__ = ["RMSNorm", "rms_norm", "swiglu", "autocast_dtype"]
+
+_DT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+_autocast_out: dict = {}
+
+# torch's rms_norm with eps=None adds the epsilon of its fp32 accumulation type for fp32 and
+# bf16 inputs alike (the statistics are always computed in fp32)
+DEFAULT_EPS = torch.finfo(torch.float32).eps
+
+
+def autocast_dtype(x: torch.Tensor) -> torch.dtype:
+    """The dtype ``torch.nn.functional.rms_norm`` returns for an input like ``x`` under the
+    current autocast state (probed once per state on a 1x8 tensor, then cached)."""
+    on = torch.is_autocast_enabled(x.device.type)
+    key = (x.dtype, x.device.type, on, torch.get_autocast_dtype(x.device.type) if on else None)
+    dt = _autocast_out.get(key)
+    if dt is None:
+        probe = torch.zeros(1, 8, dtype=x.dtype, device=x.device)
+        dt = torch.nn.functional.rms_norm(probe, (8,)).dtype
+        _autocast_out[key] = dt
+    return dt
+
+
+def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """t as [rows, cols] with a unit last stride and one row stride (copying if needed)."""
+    t2 = t.reshape(-1, t.shape[-1])
+    align = 4 if t.dtype == torch.float32 else 8
+    if t2.stride(-1) != 1 or t2.stride(0) % align or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2, t2.stride(0)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
+             out_dtype: torch.dtype | None = None, residual: torch.Tensor | None = None):
+    """RMSNorm of ``x`` (or of ``x + residual``) over its last dimension.
+
+    Returns ``out`` (dtype ``out_dtype``, default x's), or ``(x + residual, out)`` when a
+    residual is given; the sum has x's dtype, rounded as torch's add rounds.
+    """
+    if not x.is_cuda:
+        raise ValueError("fused.rms_norm needs a ROCm device tensor")
+    if residual is not None and residual.dtype != x.dtype:
+        x = x + residual                      # mixed dtypes: torch's promotion, then the plain norm
+        return x, rms_norm(x, weight, eps, out_dtype)
+    if x.dtype not in _DT:
+        x = x.float()
+    out_dtype = out_dtype or x.dtype
+    shape = x.shape
+    C = shape[-1]
+    x2, xs = _rows(x)
+    rows = x2.shape[0]
+    out = torch.empty(shape, dtype=out_dtype, device=x.device)
+    w = None
+    if weight is not None:
+        w = weight.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    r2, rs, s_out = None, 0, None
+    if residual is not None:
+        r2, rs = _rows(residual.expand(shape))
+        s_out = torch.empty(shape, dtype=x.dtype, device=x.device)
+    st = _lib.lib().mosaic_rms_norm_fwd(
+        x2.data_ptr(), r2.data_ptr() if r2 is not None else None, _DT[x.dtype], rows, C, xs, rs,
+        w.data_ptr() if w is not None else None, float(DEFAULT_EPS if eps is None else eps),
+        s_out.data_ptr() if s_out is not None else None, out.data_ptr(), _DT[out_dtype], stream_of(x))
+    _lib.check(st, "mosaic_rms_norm_fwd")
+    return out if residual is None else (s_out, out)
+
+
+def swiglu(h: torch.Tensor, noise: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(x1 + noise) * x3`` for ``x1, x3 = h.chunk(2, -1)``; h is ``[S, B, 2*hidden]``
+    (sequence-first) and noise, if given, ``[B, hidden]`` (one row per batch member)."""
+    if not h.is_cuda:
+        raise ValueError("fused.swiglu needs a ROCm device tensor")
+    if h.dtype not in _DT:
+        raise ValueError(f"unsupported dtype {h.dtype}")
+    hidden = h.shape[-1] // 2
+    h2, hs = _rows(h)
+    rows = h2.shape[0]
+    n = None
+    if noise is not None:
+        n = noise.to(h.dtype).reshape(-1, hidden).contiguous()
+        if h.dim() < 2 or h.shape[-2] != n.shape[0]:
+            raise ValueError("noise must hold one row per batch member (h.shape[-2])")
+    out = torch.empty(*h.shape[:-1], hidden, dtype=h.dtype, device=h.device)
+    st = _lib.lib().mosaic_swiglu_fwd(h2.data_ptr(), _DT[h.dtype], rows, hidden, hs,
+                                      n.data_ptr() if n is not None else None,
+                                      n.shape[0] if n is not None else 0, out.data_ptr(), stream_of(h))
+    _lib.check(st, "mosaic_swiglu_fwd")
+    return out
+
+
+class RMSNorm(nn.RMSNorm):
+    """``torch.nn.RMSNorm`` (same parameters and eps rule) whose forward on a ROCm device is
+    one fused kernel: fp32 statistics, output in the autocast dtype when autocast is on (the
+    module's output dtype under the reference's bf16 autocast), else in the input's dtype."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda:
+            return rms_norm(x, self.weight, self.eps, out_dtype=autocast_dtype(x))
+        return super().forward(x)
+
+    def add_forward(self, x: torch.Tensor, residual: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(x + residual, self(x + residual))``; on a ROCm device one kernel reads x and the
+        residual once and writes both results."""
+        if x.is_cuda and x.dtype == residual.dtype:
+            y, out = rms_norm(x, self.weight, self.eps, out_dtype=autocast_dtype(x), residual=residual)
+            return y, out
+        y = x + residual
+        return y, self(y)

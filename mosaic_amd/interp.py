@@ -17,6 +17,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
+from .fused import RMSNorm
 from .ops import stream_of
 
 
@@ -92,7 +93,7 @@ class CrossAttentionInterpolate(nn.Module):
         self.num_heads = num_heads
         self.head_dim = dim // num_heads
         self.scale = self.head_dim ** -0.5
-        self.kv_norm = nn.RMSNorm(dim, elementwise_affine=config.rmsnorm_elementwise_affine)
+        self.kv_norm = RMSNorm(dim, elementwise_affine=config.rmsnorm_elementwise_affine)
         self.to_q = nn.Linear(self.space_dim, dim, bias=False)
         self.to_kv = nn.Linear(dim, 2 * dim, bias=False)
         self.to_o = nn.Linear(dim, dim, bias=False)

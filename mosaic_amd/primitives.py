@@ -138,23 +138,26 @@ def _weights_view(w: torch.Tensor, B: int, N: int, Hq: int, device) -> torch.Ten
 
 
 def mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
-                     block_attn_only, no_compression=False, *, return_block_indices=False):
+                     block_attn_only, no_compression=False, *, return_block_indices=False, out=None):
     """Three-branch block-sparse attention forward (primitives.py:54-89).
 
     Branch logic as in the reference: ``block_attn_only`` returns the local branch; with
     ``no_compression`` the local and selected branches are merged with renormalised weights;
     ``sparse_block_count == 0`` merges local and compressed with renormalised weights;
     otherwise ``o_ba*w0 + o_cmp*w1 + o_slc*w2``.  With ``return_block_indices`` the selected
-    block indices (int64 [B, N/sparse_block_size, Hk, K]) are returned as well.
+    block indices (int64 [B, N/sparse_block_size, Hk, K]) are returned as well.  ``out``
+    (keyword-only) is an optional preallocated bf16 [B, N, Hq, 64] destination whose head and
+    head_dim strides are 64 and 1 (e.g. the transposed view of a sequence-first buffer); the
+    kernel writes it in place.
     """
     out, idx, _ = _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
-                               block_attn_only, no_compression, return_block_indices, None)
+                               block_attn_only, no_compression, return_block_indices, None, out=out)
     return (out, idx) if return_block_indices else out
 
 
 def mosaic_attn_func_rope(q, k, v, weight_ba_cmp_slc, rope_cos, rope_sin, block_attn_size, sparse_block_size,
                           sparse_block_count, block_attn_only, no_compression=False, *, return_rotated=False,
-                          return_block_indices=False):
+                          return_block_indices=False, out=None):
     """mosaic_attn_func on q and k rotated by the 2-D RoPE, with the rotation fused into the
     op's pooling pass (primitives.py:193-195 followed by :54-89): q and k are read once,
     rotated, pooled and written rotated for the attention kernel.
@@ -162,17 +165,18 @@ def mosaic_attn_func_rope(q, k, v, weight_ba_cmp_slc, rope_cos, rope_sin, block_
     ``rope_cos`` / ``rope_sin`` are the RoPE module's ``cos_freqs`` / ``sin_freqs`` ([N, 32]
     fp32, primitives.py:115-123).  The result equals ``mosaic_attn_func(RoPE(q), RoPE(k), v,
     ...)``.  With ``return_rotated`` the rotated q and k ([B, N, H, 64] bf16) are returned
-    after the output (and before the indices, when those are asked for too).
+    after the output (and before the indices, when those are asked for too).  ``out`` as for
+    ``mosaic_attn_func``.
     """
     out, idx, rot = _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
                                  sparse_block_count, block_attn_only, no_compression, return_block_indices,
-                                 (rope_cos, rope_sin), return_rotated)
+                                 (rope_cos, rope_sin), return_rotated, out=out)
     res = (out,) + (rot if return_rotated else ()) + ((idx,) if return_block_indices else ())
     return res[0] if len(res) == 1 else res
 
 
 def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
-                 block_attn_only, no_compression, return_block_indices, rope, return_rotated=False):
+                 block_attn_only, no_compression, return_block_indices, rope, return_rotated=False, out=None):
     dtype = q.dtype
     q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     _check_gqa(q, k, v)
@@ -193,8 +197,14 @@ def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
     idx = None
     if return_block_indices and selects:
         idx = torch.empty(B, N // sparse_block_size, Hk, sparse_block_count, dtype=torch.int64, device=q.device)
-    out = _out_like(q)
+    if out is None:
+        out = _out_like(q)
+    elif (tuple(out.shape) != (B, N, Hq, d) or out.dtype != torch.bfloat16 or out.device != q.device
+          or out.stride(3) != 1 or out.stride(2) != d or out.stride(0) % 8 or out.stride(1) % 8
+          or out.data_ptr() % 16):
+        raise ValueError("out must be a bf16 [B, N, Hq, 64] view with contiguous heads and 16-byte rows")
     a = _bsa_args(q, k, v, w, out, block_attn_size, sparse_block_size, sparse_block_count, mode, idx)
+    a.out_stride_b, a.out_stride_n = out.stride(0), out.stride(1)
     L = _lib.lib()
     rot = ()
     if rope is not None:
@@ -296,22 +306,47 @@ class MosaicAttention(nn.Module):
             self._rope_shared = bool(torch.equal(tabs[0], tabs[2]) and torch.equal(tabs[1], tabs[3]))
         return self._rope_shared
 
+    def _projections(self, x):
+        """q, k, v and the gate logits from ONE GEMM over x: the four weights stacked (zero rows
+        pad the width to a multiple of 64, so every slice starts 16-byte aligned), instead of
+        four GEMMs that each read x (the gate projection alone, 36-60 outputs wide, ran ~10x
+        slower than its bytes allow as a separate skinny GEMM)."""
+        mods = [self.to_q, self.to_k, self.to_v]
+        if not self.block_attn_only:
+            mods.append(self.to_strategy_combine_mlp)
+        sizes = [m.out_features for m in mods]
+        pad = -sum(sizes) % 64
+        ws = [m.weight for m in mods]
+        if pad:
+            ws.append(ws[0].new_zeros(pad, ws[0].shape[1]))
+        y = torch.nn.functional.linear(x, torch.cat(ws, 0))
+        parts = y.split(sizes + ([pad] if pad else []), dim=-1)
+        return parts[0], parts[1], parts[2], (parts[3] if not self.block_attn_only else None)
+
     def forward(self, x):
         S_, B_ = x.shape[:2]
-        q = self.to_q(x).view(S_, B_, self.q_heads, -1).transpose(0, 1)
-        k = self.to_k(x).view(S_, B_, self.kv_heads, -1).transpose(0, 1)
-        v = self.to_v(x).view(S_, B_, self.kv_heads, -1).transpose(0, 1)
-        w = self.generate_strategy_weights(x)
+        q, k, v, logits = self._projections(x)
+        q = q.unflatten(-1, (self.q_heads, -1)).transpose(0, 1)
+        k = k.unflatten(-1, (self.kv_heads, -1)).transpose(0, 1)
+        v = v.unflatten(-1, (self.kv_heads, -1)).transpose(0, 1)
+        w = None
+        if logits is not None:      # generate_strategy_weights on the fused GEMM's slice
+            logits = logits.unflatten(-1, (self.q_heads, 3)).permute(3, 1, 0, 2)
+            w = torch.softmax(logits.float(), dim=0).type_as(x).unsqueeze(-1)
         args = dict(block_attn_size=self.block_attn_size, sparse_block_size=self.sparse_block_size,
                     sparse_block_count=self.sparse_block_count, block_attn_only=self.block_attn_only,
                     no_compression=self.no_compression)
+        # the kernel writes sequence-first rows ('b s h d -> s b (h d)', primitives.py:207), so
+        # to_o reads one contiguous [S*B, Hq*64] matrix (a transposed view would make the GEMM
+        # a batch of S tiny products)
+        o = torch.empty(S_, B_, self.q_heads * q.shape[-1], dtype=torch.bfloat16, device=x.device)
+        o_view = o.view(S_, B_, self.q_heads, -1).transpose(0, 1)
         if self.q_rope is not None and self._shared_rope_tables():
             # the rotation runs inside the op's pooling pass (one read of q and k)
-            out = mosaic_attn_func_rope(q, k, v, w, self.q_rope.cos_freqs, self.q_rope.sin_freqs, **args)
+            mosaic_attn_func_rope(q, k, v, w, self.q_rope.cos_freqs, self.q_rope.sin_freqs, **args, out=o_view)
         else:
             if self.q_rope is not None:
                 q = self.q_rope(q)
                 k = self.k_rope(k)
-            out = mosaic_attn_func(q=q, k=k, v=v, weight_ba_cmp_slc=w, **args)
-        out = out.transpose(0, 1).reshape(S_, B_, -1)
-        return self.to_o(out)
+            mosaic_attn_func(q=q, k=k, v=v, weight_ba_cmp_slc=w, **args, out=o_view)
+        return self.to_o(o.to(q.dtype))

@@ -1,0 +1,190 @@
+"""GPU parity of the model-level pieces (marked ``gpu``).
+
+* The fused RMSNorm (with and without the residual add) and SwiGLU gate kernels against
+  torch's own ops on the same device: torch's ``rms_norm`` / add / ``silu`` are what the
+  reference's modules call (primitives.py:102-105, 220-226).  Bars: the residual sum
+  bit-equal to torch's add; normalised outputs within one bf16 spacing (at most 2^-7 relative) and
+  fp32 outputs within 2e-6 relative; the gate within one bf16 spacing with >= 99% of the
+  elements bit-equal (only the exponential's last fp32 bits may differ).
+* The whole U-Net forward (mosaic.py:304-337) at a small configuration against the CPU
+  oracle ``oracle/unet_oracle.py`` (the reference's computation under bf16 autocast, einops
+  for every rearrange).  The selection count equals the number of blocks at every stage, so
+  the selected set is all blocks and no top-k tie can make the two differ.  The residual
+  output layers are re-initialised at full scale so that every attention and feed-forward
+  layer moves the output.  Bars: relative L2 2e-2 and max-abs 6e-2 of the output (whose
+  values are O(1)): the forward chains ~60 bf16-rounded ops and a bf16 spacing is 2^-8
+  relative; a layout or formula mistake gives O(1) relative error.
+"""
+
+import math
+
+import pytest
+import torch
+
+from mosaic_amd import fused
+from mosaic_amd.model import BottleneckConfig, ModelConfig, StageConfig, Transformer
+from oracle import unet_oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def rand(*shape, seed, scale=1.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def assert_close_rel(got, ref, rel_tol, what):
+    g, r = got.float().cpu(), ref.float().cpu()
+    assert g.shape == r.shape and got.dtype == ref.dtype, (g.shape, r.shape, got.dtype, ref.dtype)
+    assert torch.isfinite(g).all(), f"{what}: non-finite output"
+    bad = (g - r).abs() > rel_tol * r.abs() + 1e-30
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond {rel_tol} relative, max " \
+                          f"{((g - r).abs() / r.abs().clamp_min(1e-30)).max().item():.3e}"
+
+
+@pytest.mark.parametrize("cols", [256, 768, 1280, 4096])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("autocast", [False, True])
+@pytest.mark.parametrize("scale", [1.0, 1e-3])
+def test_rms_norm_matches_torch(cols, dtype, autocast, scale):
+    print(f"rms_norm cols={cols} dtype={dtype} autocast={autocast} scale={scale}", flush=True)
+    x = rand(3, 37, cols, seed=cols, scale=scale, dtype=dtype).to(DEV)
+    with torch.autocast(DEV, dtype=torch.bfloat16, enabled=autocast):
+        ref = torch.nn.functional.rms_norm(x, (cols,))
+        got = fused.rms_norm(x, None, None, out_dtype=fused.autocast_dtype(x))
+    assert_close_rel(got, ref, 2 ** -7 if ref.dtype == torch.bfloat16 else 2e-6, "rms_norm")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rms_norm_affine_and_residual(dtype):
+    print(f"rms_norm residual dtype={dtype}", flush=True)
+    cols = 768
+    x = rand(64, 5, cols, seed=1, dtype=dtype).to(DEV)
+    r = rand(64, 5, cols, seed=2, dtype=dtype).to(DEV)
+    w = (1 + rand(cols, seed=3, scale=0.3)).to(DEV)
+    ref_sum = x + r
+    ref = torch.nn.functional.rms_norm(ref_sum.float(), (cols,), w).to(dtype)
+    s, got = fused.rms_norm(x, w, None, out_dtype=dtype, residual=r)
+    assert torch.equal(s, ref_sum), "residual sum differs from torch's add"
+    assert_close_rel(got, ref, 2 ** -7 if dtype == torch.bfloat16 else 2e-6, "rms_norm affine")
+    # strided input rows (a [S, B, 2C] activation's first half)
+    wide = rand(64, 5, 2 * cols, seed=4, dtype=dtype).to(DEV)
+    view = wide[..., :cols]
+    got2 = fused.rms_norm(view, None, None, out_dtype=dtype)
+    ref2 = torch.nn.functional.rms_norm(view.float(), (cols,)).to(dtype)
+    assert_close_rel(got2, ref2, 2 ** -7 if dtype == torch.bfloat16 else 2e-6, "rms_norm strided")
+
+
+@pytest.mark.parametrize("noise", [True, False])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_swiglu_matches_torch(noise, dtype):
+    print(f"swiglu noise={noise} dtype={dtype}", flush=True)
+    S, B, hid = 50, 6, 3072
+    h = rand(S, B, 2 * hid, seed=5, scale=2.0, dtype=dtype).to(DEV)
+    n = rand(B, hid, seed=6, dtype=dtype).to(DEV) if noise else None
+    x1, x3 = h.chunk(2, dim=-1)
+    ref = torch.nn.functional.silu(x1 + (n.unsqueeze(0) if noise else 0)) * x3
+    got = fused.swiglu(h, n)
+    tol = 2 ** -7 if dtype == torch.bfloat16 else 2e-6
+    g, r = got.float().cpu(), ref.float().cpu()
+    assert got.dtype == ref.dtype and torch.isfinite(g).all()
+    bad = (g - r).abs() > tol * r.abs() + 1e-6
+    assert not bad.any(), f"{int(bad.sum())} gate values differ beyond one bf16 spacing"
+    if dtype == torch.bfloat16:
+        assert (got == ref).float().mean().item() >= 0.99
+
+
+@pytest.mark.parametrize("mode", ["full", "local", "no_compression", "no_selection"])
+def test_op_writes_sequence_first_rows(mode):
+    """The op's ``out=`` destination (a transposed view of a sequence-first [N, B, Hq*64]
+    buffer, as MosaicAttention passes it) receives exactly the contiguous result."""
+    from mosaic_amd.primitives import mosaic_attn_func
+    print(f"sequence-first out mode={mode}", flush=True)
+    B, N, Hq, Hk = 3, 1024, 8, 2
+    q = rand(B, N, Hq, 64, seed=20, dtype=torch.bfloat16).to(DEV)
+    k = rand(B, N, Hk, 64, seed=21, dtype=torch.bfloat16).to(DEV)
+    v = rand(B, N, Hk, 64, seed=22, dtype=torch.bfloat16).to(DEV)
+    w = torch.sigmoid(rand(3, B, N, Hq, 1, seed=23)).to(torch.bfloat16).to(DEV)
+    kw = dict(block_attn_size=256, sparse_block_size=64, sparse_block_count=0 if mode == "no_selection" else 4,
+              block_attn_only=mode == "local", no_compression=mode == "no_compression")
+    ref = mosaic_attn_func(q, k, v, w, **kw)
+    buf = torch.full((N, B, Hq * 64), float("nan"), dtype=torch.bfloat16, device=DEV)
+    got = mosaic_attn_func(q, k, v, w, **kw, out=buf.view(N, B, Hq, 64).transpose(0, 1))
+    assert got.data_ptr() == buf.data_ptr()
+    assert torch.equal(buf.view(N, B, Hq, 64).transpose(0, 1), ref)
+
+
+def tiny_config() -> ModelConfig:
+    """Three resolutions (nside 16 / 8 / 4: 3072 / 768 / 192 pixels), head_dim 64, GQA 4, with
+    the selection count equal to the block count at every stage."""
+    stages = [
+        StageConfig(nside=16, dim=256, num_heads=4, block_attn_size=256, sparse_block_size=64,
+                    sparse_block_count=48, encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
+        StageConfig(nside=8, dim=512, num_heads=8, block_attn_size=256, sparse_block_size=64,
+                    sparse_block_count=12, encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
+    ]
+    bottleneck = BottleneckConfig(nside=4, dim=512, num_heads=8, block_attn_size=64, sparse_block_size=64,
+                                  sparse_block_count=3, depth=1, mlp_ratio=2.0, gqa_ratio=4)
+    return ModelConfig(dim=256, num_heads=4, k_neighbors=8, qk_norm=False, rope=True, rope_theta=10000,
+                       sparse_every=1, variables=[f"v{i}" for i in range(5)], static_variables=["a", "b", "c"],
+                       qkv_compress_ratio=1, cg_stage_cfgs=stages, bottleneck_cfg=bottleneck,
+                       num_history_steps=2, noise_dim=32, rmsnorm_elementwise_affine=False)
+
+
+def build_tiny(seed=0):
+    torch.manual_seed(seed)
+    cfg = tiny_config()
+    model = Transformer(cfg, seed=11)
+    g = torch.Generator().manual_seed(seed + 1)
+    for name, p in model.named_parameters():          # residual outputs at full scale
+        if name.endswith(("to_o.weight", "w2.weight", "proj_x.weight", "proj_pos.weight")) and "interp" not in name:
+            p.data = torch.randn(p.shape, generator=g) / math.sqrt(p.shape[1])
+    lon = torch.linspace(0, 345, 24)
+    lat = torch.linspace(-90, 90, 13)
+    model.initialize_interpolation(lon, lat)
+    model.initialize_static_vars(torch.randn(24, 13, 3, generator=g), lon, lat)
+    return cfg, model.to(DEV).eval()
+
+
+def test_unet_forward_matches_oracle():
+    print("unet tiny forward vs oracle", flush=True)
+    cfg, model = build_tiny()
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(1, 1, 2, 24, 13, 5, generator=g)
+    dyt = torch.rand(1, 1, 2, generator=g)
+    S = 2
+    with torch.no_grad(), torch.autocast(DEV, dtype=torch.bfloat16):
+        out = model(x.to(DEV), dyt.to(DEV), S)
+        probe = {dt: torch.nn.functional.rms_norm(torch.zeros(1, 8, dtype=dt, device=DEV), (8,)).dtype
+                 for dt in (torch.bfloat16, torch.float32)}
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(11)
+    noise = torch.randn((S, cfg.noise_dim), generator=gen, device=DEV, dtype=torch.float32).cpu()
+    ref = unet_oracle.forward(model.state_dict(), cfg, x, dyt, S, noise, probe)
+    got = out.float().cpu()
+    r = ref.float()
+    assert got.shape == r.shape == (1, S, 24, 13, 5), (got.shape, r.shape)
+    assert torch.isfinite(got).all()
+    rel = ((got - r).norm() / r.norm()).item()
+    err = (got - r).abs().max().item()
+    print(f"unet tiny: rel_l2 {rel:.3e} max_abs {err:.3e} |ref| max {r.abs().max().item():.3f}", flush=True)
+    assert rel <= 2e-2 and err <= 6e-2, f"rel_l2 {rel:.3e} max_abs {err:.3e}"
+
+
+def test_unet_forward_members_independent():
+    """Each member's forecast depends only on its own noise row: running the members one at
+    a time (the model draws one noise row per sample) gives the batched result."""
+    print("unet tiny member independence", flush=True)
+    cfg, model = build_tiny(seed=3)
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(1, 1, 2, 24, 13, 5, generator=g).to(DEV)
+    dyt = torch.rand(1, 1, 2, generator=g).to(DEV)
+    with torch.no_grad(), torch.autocast(DEV, dtype=torch.bfloat16):
+        model.noise_generator.generator = None
+        both = model(x, dyt, 2).float()
+        model.noise_generator.generator = None
+        first = model(x, dyt, 1).float()
+    rel = ((both[:, :1] - first).norm() / first.norm()).item()
+    assert rel <= 2e-2, rel
