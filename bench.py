@@ -234,6 +234,38 @@ def interp_leg(L, args, dev, stream):
     return res
 
 
+def bwd_leg(L, q, k, v, wl, args, dev, stream):
+    """Backward of the selected branch (MosaicAttnFunction.backward, ops.py:437-554) on the
+    workload's q/k/v with a random top-K selection per (query block, kv head).  FLOPs per
+    (64-query tile, 64-key tile, head): 3 products of 2*64^3 for grad q (q'k, do.v, dS.k) and 4
+    for grad k / v (k.q', v.do, P.do, dS.q')."""
+    from mosaic_amd.ops import mosaic_attn_bwd, mosaic_attn_fwd
+    B, N, Hq, d = q.shape
+    Hk = k.shape[2]
+    bs, K = wl.sparse_block_size, wl.sparse_block_count
+    nb = N // bs
+    g = torch.Generator().manual_seed(args.seed)
+    idx = torch.stack([torch.randperm(nb, generator=g)[:K] for _ in range(B * nb * Hk)]).view(B, nb, Hk, K).to(dev)
+    do = torch.randn(B, N, Hq, d, generator=torch.Generator(device=dev).manual_seed(args.seed), device=dev,
+                     dtype=torch.bfloat16)
+    o, lse = mosaic_attn_fwd(q, k, v, idx, bs, 0.125)
+    for _ in range(3):
+        mosaic_attn_bwd(q, k, v, o, lse, do, 0.125, idx, bs)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(5, args.steps // 10)
+    e0.record(stream)
+    for _ in range(n):
+        mosaic_attn_bwd(q, k, v, o, lse, do, 0.125, idx, bs)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    units = B * Hq * (N // 64) * (K * bs // 64)
+    flops = units * 7 * 2 * 64 ** 3
+    return {"ms": round(ms, 4), "flops": flops, "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "calls": n}
+
+
 def unet_leg(args, dev):
     """One forecast step of the full U-Net (mosaic.py:304-337) with the shipped era5 preset
     (inference.py:71-103, 286-302; 214,184,448 parameters, random init as the model initialises
@@ -326,6 +358,7 @@ def main():
     ap.add_argument("--rope-fused", action="store_true")
     ap.add_argument("--interp", action="store_true")
     ap.add_argument("--interp-batch", type=int, default=24)
+    ap.add_argument("--bwd", action="store_true", help="also time the selected-branch backward")
     ap.add_argument("--no-unet", action="store_true", help="skip the 24-member U-Net step")
     ap.add_argument("--unet-only", action="store_true", help="time only the U-Net step (prints its JSON)")
     ap.add_argument("--unet-members", type=int, default=24)
@@ -467,6 +500,8 @@ def main():
         result["rope_fused"] = rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream)
     if args.interp:
         result["knn_interp"] = interp_leg(L, args, dev, stream)
+    if args.bwd:
+        result["selected_bwd"] = bwd_leg(L, q, k, v, wl, args, dev, stream)
     if not args.no_unet:
         leg = unet_leg(args, dev)
         result["unet_24_member_step_ms"] = leg["ms_per_step"] if leg["members"] == 24 else None

@@ -154,6 +154,24 @@ MOSAIC_API int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd 
                            int32_t block_size, int32_t block_count, float softmax_scale,
                            void* out, float* lse, void* stream);
 
+/*
+ * Backward of the selected-branch attention.  Replaces MosaicAttnFunction.backward /
+ * mosaic_attn_bwd (ops.py:541-554, 437-507) and its grad-q, block-mask and grad-k/v kernels
+ * (ops.py:179-273, 276-297, 300-434): given the forward's inputs, its output out (bf16
+ * [B, N, Hq, 64] contiguous), its lse (fp32 [B, N, Hq], base 2) and grad_out (strided like q),
+ * writes grad_q (bf16 [B, N, Hq, 64]), grad_k and grad_v (bf16 [B, N, Hk, 64]), all
+ * contiguous.  Keys that no query block selected get zero gradients.  block_indices as for
+ * mosaic_sparse_attn_fwd (entries outside [0, N/bs) are skipped); N / block_size <= 4096.
+ * workspace: mosaic_sparse_attn_bwd_workspace_size() bytes (the per-row delta = o . do).
+ */
+MOSAIC_API size_t mosaic_sparse_attn_bwd_workspace_size(int32_t batch, int32_t seq_len, int32_t num_q_heads);
+MOSAIC_API int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const void* out,
+                                      const float* lse, mosaic_bnhd grad_out, const int64_t* block_indices,
+                                      int32_t batch, int32_t seq_len, int32_t num_q_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                      int32_t block_count, float softmax_scale, void* grad_q, void* grad_k,
+                                      void* grad_v, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Local attention inside contiguous blocks.  Replaces block_attention (primitives.py:28-32),
    i.e. flash_attn_func on [(B*N/bs), bs, H, d] views.  out: bf16 [B, N, Hq, 64] contiguous. */
 MOSAIC_API int mosaic_block_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, int32_t batch,

@@ -30,6 +30,8 @@ EXPORTED_SYMBOLS = (
     "mosaic_bsa_fwd_profiled",
     "mosaic_bsa_fwd_rope",
     "mosaic_knn_interp_fwd",
+    "mosaic_sparse_attn_bwd_workspace_size",
+    "mosaic_sparse_attn_bwd",
     "mosaic_rms_norm_fwd",
     "mosaic_swiglu_fwd",
     "mosaic_sparse_attn_fwd",
@@ -93,6 +95,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_rms_norm_fwd.restype = c_int
     lib.mosaic_swiglu_fwd.argtypes = [c_vp, c_i32, c_i64, c_i32, c_i64, c_vp, c_i32, c_vp, c_vp]
     lib.mosaic_swiglu_fwd.restype = c_int
+    lib.mosaic_sparse_attn_bwd_workspace_size.argtypes = [c_i32, c_i32, c_i32]
+    lib.mosaic_sparse_attn_bwd_workspace_size.restype = c_size
+    lib.mosaic_sparse_attn_bwd.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_vp, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32,
+                                           c_i32, c_i32, c_i32, c_f, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]
+    lib.mosaic_sparse_attn_bwd.restype = c_int
     lib.mosaic_sparse_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
                                            c_i32, c_i32, c_f, c_vp, c_vp, c_vp]
     lib.mosaic_sparse_attn_fwd.restype = c_int

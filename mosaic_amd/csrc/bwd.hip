@@ -1,0 +1,331 @@
+// bwd.hip -- backward of the selected-block attention (gfx950).
+//
+// Replaces MosaicAttnFunction.backward / mosaic_attn_bwd (ops.py:437-507, 541-554) and its
+// kernels (ops.py:179-273 grad q, 276-297 block mask, 300-434 grad k / v) with the same
+// arithmetic and rounding points:
+//   q'    = bf16((q * scale) * log2 e)                      (ops.py:236-237, 412-414)
+//   delta = bf16(sum_d bf16(o * do))                        (ops.py:458, eager bf16 ops)
+//   dq    = bf16(((sum over selected keys of bf16(P ln2 (dP - delta)) k) * scale) * log2 e)
+//           with P = exp2(q'.k - lse), dP = do.v            (ops.py:265-273)
+//   dv    = sum over the queries that selected the key of bf16(P) do
+//   dk    = sum of bf16(P (dP - delta) ln2) q'              (ops.py:425-431)
+// Products run on v_mfma_f32_32x32x16_bf16 with fp32 accumulation.
+//
+// The reference's grad-k/v program scans a dense [B, Hk, nb, nb] boolean block mask for every
+// key block.  Here each key-tile workgroup marks, in LDS, the query blocks whose selection row
+// holds its block (one pass over the [nb, K] index rows of its kv head) and then walks the
+// marked blocks in ascending order -- the reference's loop order, without the mask tensor.
+//
+// Workgroups are 4 waves.  Each phase of a 64 x 64 tile step gives every wave one 32 x 32
+// quadrant; operands come from LDS rows (16-byte reads), with transposed copies of the
+// operands whose MFMA B side runs along the token dimension.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "bsa_common.h"
+#include "mosaic_bsa.h"
+
+namespace mosaic {
+
+namespace {
+
+constexpr float kLn2 = 0.69314718056f;   // ops.py:197
+constexpr int kLd = 72;                  // LDS row stride in bf16 (144 bytes: 16-byte aligned rows)
+constexpr int kMaxBwdBlocks = 4096;      // query blocks a key tile can mark (LDS flags)
+
+struct BwdParams {
+    const bf16_t* q; int64_t q_sb, q_sn, q_sh;
+    const bf16_t* k; int64_t k_sb, k_sn, k_sh;
+    const bf16_t* v; int64_t v_sb, v_sn, v_sh;
+    const bf16_t* go; int64_t go_sb, go_sn, go_sh;
+    const bf16_t* o;        // forward output [B, N, Hq, 64] contiguous
+    const float* lse;       // [B, N, Hq] base-2 log-sum-exp of the scaled logits
+    float* delta;           // [B, N, Hq] (workspace)
+    const int64_t* idx;     // [B, nb, Hk, K]
+    bf16_t* dq; bf16_t* dk; bf16_t* dv;   // contiguous [B, N, H, 64]
+    int B, N, Hq, Hk, G, bs, K, nb;
+    float scale;
+};
+
+__device__ __forceinline__ void unpack8(const uint4& u, float f[8]) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { f[2 * i] = bf_lo(w[i]); f[2 * i + 1] = bf_hi(w[i]); }
+}
+__device__ __forceinline__ uint4 pack8(const float f[8]) {
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                      pack_bf16x2(f[6], f[7]));
+}
+__device__ __forceinline__ bf16x8 lds8(const bf16_t* p) { return as_bf16x8(*reinterpret_cast<const uint4*>(p)); }
+
+// Stage 64 rows x 64 dims of a [B, N, H, 64] tensor into LDS (row-major, optionally also
+// transposed), scaling to q' when QSCALE.  256 threads, two 16-byte chunks each.
+template <bool QSCALE, bool TRANSPOSE>
+__device__ __forceinline__ void stage_rows(const bf16_t* base, int64_t sn, bf16_t* rows, bf16_t* cols,
+                                           float scale) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        const int r = c >> 3, c8 = (c & 7) * 8;
+        uint4 u = ld16(base + (int64_t)r * sn + c8);
+        if (QSCALE || TRANSPOSE) {
+            float f[8];
+            unpack8(u, f);
+            if (QSCALE) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) f[e] = (f[e] * scale) * kLog2e;
+                u = pack8(f);
+                unpack8(u, f);
+            }
+            if (TRANSPOSE) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) cols[(c8 + e) * kLd + r] = (bf16_t)(pack_bf16x2(f[e], 0.f) & 0xffffu);
+            }
+        }
+        *reinterpret_cast<uint4*>(rows + r * kLd + c8) = u;
+    }
+}
+
+// D(32x32) += A(32 x 64) B(64 x 32) with A rows and B columns read as 16-byte LDS runs:
+// a_rows[m][k], b_rows[n][k] (both "row = output index, 64 contiguous k").
+__device__ __forceinline__ f32x16 mma_32x32x64(const bf16_t* a_rows, const bf16_t* b_rows, f32x16 acc, int lane) {
+    const int r = lane & 31, kh = 8 * (lane >> 5);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+        acc = mfma32(lds8(a_rows + r * kLd + 16 * kk + kh), lds8(b_rows + r * kLd + 16 * kk + kh), acc);
+    return acc;
+}
+
+// ------------------------------------------------------------------ delta
+__global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
+    // one wave per 8 (b, n, h) rows; lane l: row l / 8, dims 8 (l % 8) .. +7
+    const int64_t rows = (int64_t)p.B * p.N * p.Hq;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+    if (row >= rows) return;
+    const int h = (int)(row % p.Hq);
+    const int64_t bn = row / p.Hq;
+    const int n = (int)(bn % p.N), b = (int)(bn / p.N);
+    const int c8 = (lane & 7) * 8;
+    float o[8], g[8];
+    unpack8(ld16(p.o + row * 64 + c8), o);
+    unpack8(ld16(p.go + (int64_t)b * p.go_sb + (int64_t)n * p.go_sn + (int64_t)h * p.go_sh + c8), g);
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += round_bf16(o[e] * g[e]);
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    if ((lane & 7) == 0) p.delta[row] = round_bf16(s);
+}
+
+// ------------------------------------------------------------------ grad q
+// grid (N / 64 query tiles, Hq, B)
+__global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
+    __shared__ __attribute__((aligned(16))) bf16_t Qs[64 * kLd], Gs[64 * kLd], Ks[64 * kLd], Kt[64 * kLd],
+        Vs[64 * kLd], Ds[64 * kLd];
+    __shared__ float lse_s[64], dl_s[64];
+    const int qt = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
+    const int c = j / p.G;
+    const int n0 = qt * 64;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    stage_rows<true, false>(p.q + (int64_t)b * p.q_sb + (int64_t)n0 * p.q_sn + (int64_t)j * p.q_sh, p.q_sn, Qs,
+                            nullptr, p.scale);
+    stage_rows<false, false>(p.go + (int64_t)b * p.go_sb + (int64_t)n0 * p.go_sn + (int64_t)j * p.go_sh, p.go_sn,
+                             Gs, nullptr, 0.f);
+    if (threadIdx.x < 64) {
+        const int64_t r = ((int64_t)b * p.N + n0 + threadIdx.x) * p.Hq + j;
+        lse_s[threadIdx.x] = p.lse[r];
+        dl_s[threadIdx.x] = p.delta[r];
+    }
+    const int64_t* sel = p.idx + (((int64_t)b * p.nb + n0 / p.bs) * p.Hk + c) * p.K;
+    const int rh = w & 1, kh = w >> 1;   // phase 2: query half, key half
+    const int dh = w >> 1;               // phase 3: dim half (query half rh)
+    f32x16 acc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    const int tiles = p.bs / 64;
+    for (int i = 0; i < p.K; ++i) {
+        const int64_t u = sel[i];
+        if (u < 0 || u >= p.nb) continue;   // uniform across the workgroup
+        for (int t = 0; t < tiles; ++t) {
+            const int key0 = (int)u * p.bs + 64 * t;
+            __syncthreads();   // previous step's readers of Ks / Kt / Vs / Ds are done
+            stage_rows<false, true>(p.k + (int64_t)b * p.k_sb + (int64_t)key0 * p.k_sn + (int64_t)c * p.k_sh,
+                                    p.k_sn, Ks, Kt, 0.f);
+            stage_rows<false, false>(p.v + (int64_t)b * p.v_sb + (int64_t)key0 * p.v_sn + (int64_t)c * p.v_sh,
+                                     p.v_sn, Vs, nullptr, 0.f);
+            __syncthreads();
+            f32x16 s, dp;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
+            s = mma_32x32x64(Qs + 32 * rh * kLd, Ks + 32 * kh * kLd, s, lane);
+            dp = mma_32x32x64(Gs + 32 * rh * kLd, Vs + 32 * kh * kLd, dp, lane);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int r = 32 * rh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                const float pr = exp2f(s[e] - lse_s[r]) * kLn2;
+                const float ds = pr * (dp[e] - dl_s[r]);
+                Ds[r * kLd + 32 * kh + (lane & 31)] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
+            }
+            __syncthreads();
+            acc = mma_32x32x64(Ds + 32 * rh * kLd, Kt + 32 * dh * kLd, acc, lane);
+        }
+    }
+    bf16_t* out = p.dq + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int r = 32 * rh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        out[(int64_t)r * p.Hq * 64 + 32 * dh + (lane & 31)] =
+            (bf16_t)(pack_bf16x2((acc[e] * p.scale) * kLog2e, 0.f) & 0xffffu);
+    }
+}
+
+// ------------------------------------------------------------------ grad k, grad v
+// grid (N / 64 key tiles, Hk, B)
+__global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
+    __shared__ __attribute__((aligned(16))) bf16_t Ks[64 * kLd], Vs[64 * kLd], Qs[64 * kLd], Qt[64 * kLd],
+        Gs[64 * kLd], Gt[64 * kLd], Ps[64 * kLd], Ds[64 * kLd];
+    __shared__ float lse_s[64], dl_s[64];
+    __shared__ uint8_t mark[kMaxBwdBlocks];
+    const int kt = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int key0 = kt * 64;
+    const int64_t u = key0 / p.bs;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    // query blocks whose selection row (kv head c) holds block u
+    for (int t = threadIdx.x; t < p.nb; t += 256) {
+        const int64_t* row = p.idx + (((int64_t)b * p.nb + t) * p.Hk + c) * p.K;
+        bool hit = false;
+        for (int i = 0; i < p.K; ++i) hit |= row[i] == u;
+        mark[t] = hit;
+    }
+    stage_rows<false, false>(p.k + (int64_t)b * p.k_sb + (int64_t)key0 * p.k_sn + (int64_t)c * p.k_sh, p.k_sn, Ks,
+                             nullptr, 0.f);
+    stage_rows<false, false>(p.v + (int64_t)b * p.v_sb + (int64_t)key0 * p.v_sn + (int64_t)c * p.v_sh, p.v_sn, Vs,
+                             nullptr, 0.f);
+    __syncthreads();
+    const int kh = w >> 1, qh = w & 1;   // phase 2: key half, query half
+    const int dh = w & 1;                // phase 3: dim half (key half kh)
+    f32x16 dk, dv;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { dk[e] = 0.f; dv[e] = 0.f; }
+    const int tiles = p.bs / 64;
+    for (int t = 0; t < p.nb; ++t) {
+        if (!mark[t]) continue;           // uniform: every thread reads the same flag
+        for (int tt = 0; tt < tiles; ++tt) {
+            const int n0 = t * p.bs + 64 * tt;
+            for (int g = 0; g < p.G; ++g) {
+                const int j = c * p.G + g;
+                __syncthreads();   // previous step's readers are done with Qs .. Ds
+                stage_rows<true, true>(p.q + (int64_t)b * p.q_sb + (int64_t)n0 * p.q_sn + (int64_t)j * p.q_sh,
+                                       p.q_sn, Qs, Qt, p.scale);
+                stage_rows<false, true>(p.go + (int64_t)b * p.go_sb + (int64_t)n0 * p.go_sn + (int64_t)j * p.go_sh,
+                                        p.go_sn, Gs, Gt, 0.f);
+                if (threadIdx.x < 64) {
+                    const int64_t r = ((int64_t)b * p.N + n0 + threadIdx.x) * p.Hq + j;
+                    lse_s[threadIdx.x] = p.lse[r];
+                    dl_s[threadIdx.x] = p.delta[r];
+                }
+                __syncthreads();
+                f32x16 s, dp;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
+                s = mma_32x32x64(Ks + 32 * kh * kLd, Qs + 32 * qh * kLd, s, lane);    // S^T: keys x queries
+                dp = mma_32x32x64(Vs + 32 * kh * kLd, Gs + 32 * qh * kLd, dp, lane);  // dP^T
+                const int qc = 32 * qh + (lane & 31);
+                const float l2 = lse_s[qc], dl = dl_s[qc];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int kr = 32 * kh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                    const float pr = exp2f(s[e] - l2);
+                    const float ds = pr * (dp[e] - dl) * kLn2;
+                    Ps[kr * kLd + qc] = (bf16_t)(pack_bf16x2(pr, 0.f) & 0xffffu);
+                    Ds[kr * kLd + qc] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
+                }
+                __syncthreads();
+                dv = mma_32x32x64(Ps + 32 * kh * kLd, Gt + 32 * dh * kLd, dv, lane);
+                dk = mma_32x32x64(Ds + 32 * kh * kLd, Qt + 32 * dh * kLd, dk, lane);
+            }
+        }
+    }
+    const int64_t base = (((int64_t)b * p.N + key0) * p.Hk + c) * 64;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int kr = 32 * kh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int64_t off = base + (int64_t)kr * p.Hk * 64 + 32 * dh + (lane & 31);
+        p.dk[off] = (bf16_t)(pack_bf16x2(dk[e], 0.f) & 0xffffu);
+        p.dv[off] = (bf16_t)(pack_bf16x2(dv[e], 0.f) & 0xffffu);
+    }
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+int check_rows(const mosaic_bnhd& t) {
+    if (t.ptr == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(t.ptr) || t.stride_b % 8 || t.stride_n % 8 || t.stride_h % 8) return MOSAIC_ERR_ALIGNMENT;
+    return MOSAIC_OK;
+}
+
+}  // namespace
+}  // namespace mosaic
+
+using namespace mosaic;
+
+extern "C" {
+
+size_t mosaic_sparse_attn_bwd_workspace_size(int32_t batch, int32_t seq_len, int32_t num_q_heads) {
+    if (batch <= 0 || seq_len <= 0 || num_q_heads <= 0) return 0;
+    return ((size_t)batch * seq_len * num_q_heads * sizeof(float) + 255) / 256 * 256;
+}
+
+int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const void* out, const float* lse,
+                           mosaic_bnhd grad_out, const int64_t* block_indices, int32_t batch, int32_t seq_len,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                           int32_t block_count, float softmax_scale, void* grad_q, void* grad_k, void* grad_v,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    if (batch <= 0 || seq_len <= 0) return MOSAIC_ERR_SHAPE;
+    if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
+    if (num_q_heads <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return MOSAIC_ERR_HEADS;
+    if (block_size <= 0 || block_size % 64 || seq_len % block_size) return MOSAIC_ERR_BLOCK_SIZE;
+    if (block_count <= 0 || block_count > kMaxSelected) return MOSAIC_ERR_BLOCK_COUNT;
+    if (seq_len / block_size > kMaxBwdBlocks) return MOSAIC_ERR_UNSUPPORTED;
+    for (const mosaic_bnhd* t : {&q, &k, &v, &grad_out})
+        if (int e = check_rows(*t)) return e;
+    if (!out || !lse || !block_indices || !grad_q || !grad_k || !grad_v) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(out) || !aligned16(grad_q) || !aligned16(grad_k) || !aligned16(grad_v)) return MOSAIC_ERR_ALIGNMENT;
+    const size_t need = mosaic_sparse_attn_bwd_workspace_size(batch, seq_len, num_q_heads);
+    if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)) return MOSAIC_ERR_WORKSPACE;
+    if ((int64_t)seq_len / 64 > 0x7fffffff || batch > 65535 || num_q_heads > 65535) return MOSAIC_ERR_SHAPE;
+
+    BwdParams p{};
+    p.q = static_cast<const bf16_t*>(q.ptr); p.q_sb = q.stride_b; p.q_sn = q.stride_n; p.q_sh = q.stride_h;
+    p.k = static_cast<const bf16_t*>(k.ptr); p.k_sb = k.stride_b; p.k_sn = k.stride_n; p.k_sh = k.stride_h;
+    p.v = static_cast<const bf16_t*>(v.ptr); p.v_sb = v.stride_b; p.v_sn = v.stride_n; p.v_sh = v.stride_h;
+    p.go = static_cast<const bf16_t*>(grad_out.ptr);
+    p.go_sb = grad_out.stride_b; p.go_sn = grad_out.stride_n; p.go_sh = grad_out.stride_h;
+    p.o = static_cast<const bf16_t*>(out);
+    p.lse = lse;
+    p.delta = static_cast<float*>(workspace);
+    p.idx = block_indices;
+    p.dq = static_cast<bf16_t*>(grad_q); p.dk = static_cast<bf16_t*>(grad_k); p.dv = static_cast<bf16_t*>(grad_v);
+    p.B = batch; p.N = seq_len; p.Hq = num_q_heads; p.Hk = num_kv_heads; p.G = num_q_heads / num_kv_heads;
+    p.bs = block_size; p.K = block_count; p.nb = seq_len / block_size;
+    p.scale = softmax_scale > 0.f ? softmax_scale : 0.125f;   // head_dim^-0.5 for head_dim 64
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    void* args[] = {&p};
+    const int64_t rows = (int64_t)batch * seq_len * num_q_heads;
+    const int64_t dgrid = (rows + 31) / 32;
+    if (dgrid > 0x7fffffff) return MOSAIC_ERR_SHAPE;
+    if (hipLaunchKernel((const void*)&bwd_delta_kernel, dim3((unsigned)dgrid), dim3(256), args, 0, s) != hipSuccess)
+        return MOSAIC_ERR_LAUNCH;
+    if (hipLaunchKernel((const void*)&bwd_dq_kernel, dim3(seq_len / 64, num_q_heads, batch), dim3(256), args, 0, s) !=
+        hipSuccess)
+        return MOSAIC_ERR_LAUNCH;
+    if (hipLaunchKernel((const void*)&bwd_dkv_kernel, dim3(seq_len / 64, num_kv_heads, batch), dim3(256), args, 0,
+                        s) != hipSuccess)
+        return MOSAIC_ERR_LAUNCH;
+    return MOSAIC_OK;
+}
+
+}  // extern "C"

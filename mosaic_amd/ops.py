@@ -1,12 +1,13 @@
-"""Selected-branch attention: the MI355X drop-in for the reference's ops.py forward.
+"""Selected-branch attention: the MI355X drop-in for the reference's ops.py.
 
 Same names and arguments as the reference:
   * ``mosaic_sparse_attn(q, k, v, block_indices, block_size, softmax_scale=None)``
     (ops.py:557-566): ``softmax_scale`` defaults to ``head_dim ** -0.5``.
-  * ``MosaicAttnFunction`` (ops.py:510-554): forward runs the HIP kernel; backward is not
-    implemented (training gradients are outside this library) and raises.
+  * ``MosaicAttnFunction`` (ops.py:510-554): forward and backward run HIP kernels.
   * ``mosaic_attn_fwd(q, k, v, block_indices, block_size, softmax_scale)`` (ops.py:137-176)
     returns ``(output, lse)`` with lse the base-2 log-sum-exp, fp32 [B, N, Hq].
+  * ``mosaic_attn_bwd(q, k, v, output, lse, grad_o, softmax_scale, block_indices,
+    block_size)`` (ops.py:437-507) returns ``(grad_q, grad_k, grad_v)``.
 
 q [B, N, Hq, 64], k/v [B, N, Hk, 64] on a ROCm device; block_indices int64 [B, N/bs, Hk, K].
 Work is enqueued on the current stream.  The computation is bf16 (like the reference kernel,
@@ -69,18 +70,54 @@ def mosaic_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_ind
     return out, lse
 
 
+def mosaic_attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, output: torch.Tensor, lse: torch.Tensor,
+                    grad_o: torch.Tensor, softmax_scale: float, block_indices: torch.Tensor, block_size: int):
+    """(grad_q, grad_k, grad_v) of the selected-branch attention (ops.py:437-507), in q's / k's /
+    v's dtypes; keys no query block selected get zero gradients."""
+    dtypes = (q.dtype, k.dtype, v.dtype)
+    q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    go = _as_bf16_bnhd(grad_o, "grad_o")
+    _check_gqa(q, k, v)
+    B, N, Hq, d = q.shape
+    Hk = k.shape[2]
+    if tuple(go.shape) != (B, N, Hq, d):
+        raise ValueError(f"grad_o shape {tuple(go.shape)} != {(B, N, Hq, d)}")
+    o = output.to(torch.bfloat16).contiguous()
+    lse = lse.to(torch.float32).contiguous()
+    idx = block_indices.to(device=q.device, dtype=torch.int64).contiguous()
+    gq = torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=q.device)
+    gk = torch.empty(B, N, Hk, d, dtype=torch.bfloat16, device=q.device)
+    gv = torch.empty(B, N, Hk, d, dtype=torch.bfloat16, device=q.device)
+    L = _lib.lib()
+    nbytes = L.mosaic_sparse_attn_bwd_workspace_size(B, N, Hq)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    st = L.mosaic_sparse_attn_bwd(bnhd(q), bnhd(k), bnhd(v), o.data_ptr(), lse.data_ptr(), bnhd(go), idx.data_ptr(),
+                                  B, N, Hq, Hk, d, int(block_size), int(idx.shape[-1]), float(softmax_scale),
+                                  gq.data_ptr(), gk.data_ptr(), gv.data_ptr(), ws.data_ptr(), ws.numel(),
+                                  stream_of(q))
+    _lib.check(st, "mosaic_sparse_attn_bwd")
+    return gq.to(dtypes[0]), gk.to(dtypes[1]), gv.to(dtypes[2])
+
+
 class MosaicAttnFunction(torch.autograd.Function):
-    """Autograd wrapper of the selected-branch forward (ops.py:510-554)."""
+    """Autograd function of the selected-branch attention (ops.py:510-554): the forward saves
+    q, k, v, the output, its LSE and the indices; the backward runs the HIP backward."""
 
     @staticmethod
     def forward(ctx, q, k, v, block_indices, block_size, softmax_scale):
         dtype = q.dtype
-        output, _ = mosaic_attn_fwd(q, k, v, block_indices, block_size, softmax_scale)
+        output, lse = mosaic_attn_fwd(q, k, v, block_indices, block_size, softmax_scale)
+        ctx.save_for_backward(q, k, v, output, lse, block_indices)
+        ctx.block_size = block_size
+        ctx.softmax_scale = softmax_scale
         return output.to(dtype)
 
     @staticmethod
     def backward(ctx, grad_o):
-        raise NotImplementedError("mosaic_amd implements the forward pass only")
+        q, k, v, output, lse, block_indices = ctx.saved_tensors
+        gq, gk, gv = mosaic_attn_bwd(q, k, v, output, lse, grad_o.contiguous(), ctx.softmax_scale,
+                                     block_indices, ctx.block_size)
+        return gq, gk, gv, None, None, None
 
 
 def mosaic_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,

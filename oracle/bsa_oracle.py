@@ -20,6 +20,9 @@ reference's own bf16 rounding points:
                                                     online softmax in top-k order, P rounded
                                                     to bf16 before PV, LSE in base 2
   * ``mosaic_attn_func``   primitives.py:54-89      branch logic, variants and bf16 merge
+  * ``sparse_attn_bwd``    ops.py:179-507           selected-branch backward: grad q over the
+                                                    selected blocks, grad k / v over the
+                                                    queries whose block selected the key
 
 Parity pinning (each function is checked against something other than its own formula by
 tests/test_oracle.py): einops itself for the strided mean, brute-force masked dense
@@ -160,6 +163,59 @@ def sparse_attn_fwd(q, k, v, block_indices, block_size: int, softmax_scale: floa
     lse_out = torch.zeros(B, nb, bs, Hk, G)
     lse_out[:, qsel] = lse.permute(0, 1, 4, 2, 3)
     return out.reshape(B, N, Hq, d), lse_out.reshape(B, N, Hq)
+
+
+LN2 = 0.69314718056   # ops.py:197
+
+
+def sparse_attn_bwd(q, k, v, o, lse, grad_o, block_indices, block_size: int, softmax_scale: float | None = None):
+    """Selected-branch backward (ops.py:179-507): returns (dq, dk, dv) in q's / k's dtype.
+
+    Rounding points of the reference kernels: q' = bf16((q * scale) * log2 e) (ops.py:237,
+    412-414); delta = bf16(sum(bf16(o * do))) (ops.py:458, eager bf16 ops); grad q: P =
+    exp2(q'.k - lse) * ln2, dS = bf16(P (dP - delta)), dq = bf16((sum dS k * scale) * log2 e)
+    (ops.py:265-273); grad k/v over every query whose block selected the key (the block mask,
+    ops.py:276-297): P = exp2(k.q' - lse), dv += bf16(P) do, dS = bf16(P (dP - delta) ln2),
+    dk += dS q' (ops.py:425-431).  Grad q loops over the index entries (ops.py:244), so a block
+    listed twice in a row counts twice there, while the boolean block mask counts it once
+    for grad k / v.  Dense N x N masked matrices: for test sizes only.
+    """
+    B, N, Hq, d = q.shape
+    Hk = k.shape[2]
+    G = Hq // Hk
+    bs = block_size
+    nb = N // bs
+    scale = d ** -0.5 if softmax_scale is None else softmax_scale
+    bf = torch.bfloat16
+    qs = ((q.float() * scale) * LOG2E).to(bf).float()
+    kf, vf, gf = k.float(), v.float(), grad_o.to(bf).float()
+    delta = (o.to(bf) * grad_o.to(bf)).sum(dim=-1).to(bf).float()           # B N Hq
+    idx = block_indices.long()
+    # mask[b, c, t, u]: query block t selected key block u for kv head c (the block mask)
+    count = torch.zeros(B, Hk, nb, nb)
+    valid = (idx >= 0) & (idx < nb)
+    bb, tt, cc, ii = torch.nonzero(valid, as_tuple=True)
+    count.index_put_((bb, cc, tt, idx[bb, tt, cc, ii]), torch.ones(bb.numel()), accumulate=True)
+    cnt = count.repeat_interleave(bs, dim=2).repeat_interleave(bs, dim=3)    # B Hk N N entries per key
+    tok = cnt > 0                                                            # the block mask
+    dq = torch.zeros(B, N, Hq, d)
+    dk = torch.zeros(B, N, Hk, d)
+    dv = torch.zeros(B, N, Hk, d)
+    for b in range(B):
+        for j in range(Hq):
+            c = j // G
+            m = tok[b, c]
+            s = qs[b, :, j] @ kf[b, :, c].t()                                   # N x N fp32
+            dp = gf[b, :, j] @ vf[b, :, c].t()
+            x = torch.where(m, s - lse[b, :, j, None].float(), torch.full_like(s, float("-inf")))
+            p = torch.exp2(x)
+            dl = delta[b, :, j, None]
+            ds_q = (p * LN2 * (dp - dl)).to(bf).float()                         # ops.py:266-269
+            dq[b, :, j] = (((ds_q * cnt[b, c]) @ kf[b, :, c]) * scale) * LOG2E  # ops.py:244, 270-272
+            dv[b, :, c] += p.to(bf).float().t() @ gf[b, :, j]                   # ops.py:427
+            ds_k = (p * (dp - dl) * LN2).to(bf).float()                         # ops.py:429
+            dk[b, :, c] += ds_k.t() @ qs[b, :, j]                               # ops.py:430
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
 
 
 def compressed_attention(q, k, v, sparse_block_size: int):
