@@ -7,7 +7,7 @@ with the input side's RoPE fused into its pooling pass.  All compute runs in lib
 (built with ``python -m mosaic_amd.build``) through its C ABI (include/mosaic_bsa.h).
 """
 
-from .ops import MosaicAttnFunction, mosaic_attn_fwd, mosaic_sparse_attn
+from .ops import MosaicAttnFunction, mosaic_attn_bwd, mosaic_attn_fwd, mosaic_sparse_attn
 from .primitives import (
     MosaicAttention,
     RoPE,
@@ -21,7 +21,7 @@ from .primitives import (
 from .healpix import get_healpix_grid, pix2ang_nest
 
 __all__ = [
-    "MosaicAttnFunction", "mosaic_attn_fwd", "mosaic_sparse_attn", "MosaicAttention", "RoPE",
+    "MosaicAttnFunction", "mosaic_attn_bwd", "mosaic_attn_fwd", "mosaic_sparse_attn", "MosaicAttention", "RoPE",
     "attn_topk", "block_attention", "dense_attention", "mosaic_attn_func", "mosaic_attn_func_rope", "pool_mean",
     "get_healpix_grid", "pix2ang_nest",
 ]

@@ -60,16 +60,25 @@ __device__ __forceinline__ uint4 pack8(const float f[8]) {
 }
 __device__ __forceinline__ bf16x8 lds8(const bf16_t* p) { return as_bf16x8(*reinterpret_cast<const uint4*>(p)); }
 
-// Stage 64 rows x 64 dims of a [B, N, H, 64] tensor into LDS (row-major, optionally also
-// transposed), scaling to q' when QSCALE.  256 threads, two 16-byte chunks each.
+// A 64-row x 64-dim tile of a [B, N, H, 64] tensor moves global -> registers -> LDS in two
+// steps, so the loads of the next tile are in flight while the current one is computed.
+// 256 threads, two 16-byte chunks each: chunk c = thread + 256 i is row c / 8, dims 8 (c % 8).
+__device__ __forceinline__ void load_rows(const bf16_t* base, int64_t sn, uint4 reg[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        reg[i] = ld16(base + (int64_t)(c >> 3) * sn + (c & 7) * 8);
+    }
+}
+
+// Registers -> LDS rows (row-major, optionally also transposed), scaled to q' when QSCALE.
 template <bool QSCALE, bool TRANSPOSE>
-__device__ __forceinline__ void stage_rows(const bf16_t* base, int64_t sn, bf16_t* rows, bf16_t* cols,
-                                           float scale) {
+__device__ __forceinline__ void store_rows(const uint4 reg[2], bf16_t* rows, bf16_t* cols, float scale) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int c = threadIdx.x + 256 * i;
         const int r = c >> 3, c8 = (c & 7) * 8;
-        uint4 u = ld16(base + (int64_t)r * sn + c8);
+        uint4 u = reg[i];
         if (QSCALE || TRANSPOSE) {
             float f[8];
             unpack8(u, f);
@@ -86,6 +95,14 @@ __device__ __forceinline__ void stage_rows(const bf16_t* base, int64_t sn, bf16_
         }
         *reinterpret_cast<uint4*>(rows + r * kLd + c8) = u;
     }
+}
+
+template <bool QSCALE, bool TRANSPOSE>
+__device__ __forceinline__ void stage_rows(const bf16_t* base, int64_t sn, bf16_t* rows, bf16_t* cols,
+                                           float scale) {
+    uint4 reg[2];
+    load_rows(base, sn, reg);
+    store_rows<QSCALE, TRANSPOSE>(reg, rows, cols, scale);
 }
 
 // D(32x32) += A(32 x 64) B(64 x 32) with A rows and B columns read as 16-byte LDS runs:
@@ -146,33 +163,41 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
     f32x16 acc;
 #pragma unroll
     for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+    // steps: the 64-key tiles of the valid selected blocks, in top-k order
     const int tiles = p.bs / 64;
-    for (int i = 0; i < p.K; ++i) {
-        const int64_t u = sel[i];
-        if (u < 0 || u >= p.nb) continue;   // uniform across the workgroup
-        for (int t = 0; t < tiles; ++t) {
-            const int key0 = (int)u * p.bs + 64 * t;
-            __syncthreads();   // previous step's readers of Ks / Kt / Vs / Ds are done
-            stage_rows<false, true>(p.k + (int64_t)b * p.k_sb + (int64_t)key0 * p.k_sn + (int64_t)c * p.k_sh,
-                                    p.k_sn, Ks, Kt, 0.f);
-            stage_rows<false, false>(p.v + (int64_t)b * p.v_sb + (int64_t)key0 * p.v_sn + (int64_t)c * p.v_sh,
-                                     p.v_sn, Vs, nullptr, 0.f);
-            __syncthreads();
-            f32x16 s, dp;
+    auto next_valid = [&](int i) {   // first entry >= i holding a block in range (uniform)
+        while (i < p.K && (sel[i] < 0 || sel[i] >= p.nb)) ++i;
+        return i;
+    };
+    int i = next_valid(0), t = 0;
+    uint4 kr[2], vr[2];
+    auto load_kv = [&](int i_, int t_) {
+        const int key0 = (int)sel[i_] * p.bs + 64 * t_;
+        load_rows(p.k + (int64_t)b * p.k_sb + (int64_t)key0 * p.k_sn + (int64_t)c * p.k_sh, p.k_sn, kr);
+        load_rows(p.v + (int64_t)b * p.v_sb + (int64_t)key0 * p.v_sn + (int64_t)c * p.v_sh, p.v_sn, vr);
+    };
+    if (i < p.K) load_kv(i, 0);
+    while (i < p.K) {
+        __syncthreads();   // previous step's readers of Ks / Kt / Vs / Ds are done
+        store_rows<false, true>(kr, Ks, Kt, 0.f);
+        store_rows<false, false>(vr, Vs, nullptr, 0.f);
+        if (++t == tiles) { t = 0; i = next_valid(i + 1); }
+        if (i < p.K) load_kv(i, t);   // next step's tiles, in flight during this step
+        __syncthreads();
+        f32x16 s, dp;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
-            s = mma_32x32x64(Qs + 32 * rh * kLd, Ks + 32 * kh * kLd, s, lane);
-            dp = mma_32x32x64(Gs + 32 * rh * kLd, Vs + 32 * kh * kLd, dp, lane);
+        for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
+        s = mma_32x32x64(Qs + 32 * rh * kLd, Ks + 32 * kh * kLd, s, lane);
+        dp = mma_32x32x64(Gs + 32 * rh * kLd, Vs + 32 * kh * kLd, dp, lane);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int r = 32 * rh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                const float pr = exp2f(s[e] - lse_s[r]) * kLn2;
-                const float ds = pr * (dp[e] - dl_s[r]);
-                Ds[r * kLd + 32 * kh + (lane & 31)] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
-            }
-            __syncthreads();
-            acc = mma_32x32x64(Ds + 32 * rh * kLd, Kt + 32 * dh * kLd, acc, lane);
+        for (int e = 0; e < 16; ++e) {
+            const int r = 32 * rh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const float pr = exp2f(s[e] - lse_s[r]) * kLn2;
+            const float ds = pr * (dp[e] - dl_s[r]);
+            Ds[r * kLd + 32 * kh + (lane & 31)] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
         }
+        __syncthreads();
+        acc = mma_32x32x64(Ds + 32 * rh * kLd, Kt + 32 * dh * kLd, acc, lane);
     }
     bf16_t* out = p.dq + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
 #pragma unroll
@@ -211,44 +236,59 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
     f32x16 dk, dv;
 #pragma unroll
     for (int e = 0; e < 16; ++e) { dk[e] = 0.f; dv[e] = 0.f; }
+    // steps: (marked query block t, its 64-row tile tt, query head g of the group), ascending
     const int tiles = p.bs / 64;
-    for (int t = 0; t < p.nb; ++t) {
-        if (!mark[t]) continue;           // uniform: every thread reads the same flag
-        for (int tt = 0; tt < tiles; ++tt) {
-            const int n0 = t * p.bs + 64 * tt;
-            for (int g = 0; g < p.G; ++g) {
-                const int j = c * p.G + g;
-                __syncthreads();   // previous step's readers are done with Qs .. Ds
-                stage_rows<true, true>(p.q + (int64_t)b * p.q_sb + (int64_t)n0 * p.q_sn + (int64_t)j * p.q_sh,
-                                       p.q_sn, Qs, Qt, p.scale);
-                stage_rows<false, true>(p.go + (int64_t)b * p.go_sb + (int64_t)n0 * p.go_sn + (int64_t)j * p.go_sh,
-                                        p.go_sn, Gs, Gt, 0.f);
-                if (threadIdx.x < 64) {
-                    const int64_t r = ((int64_t)b * p.N + n0 + threadIdx.x) * p.Hq + j;
-                    lse_s[threadIdx.x] = p.lse[r];
-                    dl_s[threadIdx.x] = p.delta[r];
-                }
-                __syncthreads();
-                f32x16 s, dp;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
-                s = mma_32x32x64(Ks + 32 * kh * kLd, Qs + 32 * qh * kLd, s, lane);    // S^T: keys x queries
-                dp = mma_32x32x64(Vs + 32 * kh * kLd, Gs + 32 * qh * kLd, dp, lane);  // dP^T
-                const int qc = 32 * qh + (lane & 31);
-                const float l2 = lse_s[qc], dl = dl_s[qc];
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int kr = 32 * kh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                    const float pr = exp2f(s[e] - l2);
-                    const float ds = pr * (dp[e] - dl) * kLn2;
-                    Ps[kr * kLd + qc] = (bf16_t)(pack_bf16x2(pr, 0.f) & 0xffffu);
-                    Ds[kr * kLd + qc] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
-                }
-                __syncthreads();
-                dv = mma_32x32x64(Ps + 32 * kh * kLd, Gt + 32 * dh * kLd, dv, lane);
-                dk = mma_32x32x64(Ds + 32 * kh * kLd, Qt + 32 * dh * kLd, dk, lane);
-            }
+    auto next_marked = [&](int t) {   // first marked block >= t (uniform LDS reads)
+        while (t < p.nb && !mark[t]) ++t;
+        return t;
+    };
+    int t = next_marked(0), tt = 0, g = 0;
+    uint4 qr[2], gr[2];
+    float lr = 0.f, dr = 0.f;
+    auto load_q = [&](int t_, int tt_, int g_) {
+        const int n0 = t_ * p.bs + 64 * tt_;
+        const int j = c * p.G + g_;
+        load_rows(p.q + (int64_t)b * p.q_sb + (int64_t)n0 * p.q_sn + (int64_t)j * p.q_sh, p.q_sn, qr);
+        load_rows(p.go + (int64_t)b * p.go_sb + (int64_t)n0 * p.go_sn + (int64_t)j * p.go_sh, p.go_sn, gr);
+        if (threadIdx.x < 64) {
+            const int64_t r = ((int64_t)b * p.N + n0 + threadIdx.x) * p.Hq + j;
+            lr = p.lse[r];
+            dr = p.delta[r];
         }
+    };
+    if (t < p.nb) load_q(t, 0, 0);
+    while (t < p.nb) {
+        __syncthreads();   // previous step's readers are done with Qs .. Ds
+        store_rows<true, true>(qr, Qs, Qt, p.scale);
+        store_rows<false, true>(gr, Gs, Gt, 0.f);
+        if (threadIdx.x < 64) {
+            lse_s[threadIdx.x] = lr;
+            dl_s[threadIdx.x] = dr;
+        }
+        if (++g == p.G) {
+            g = 0;
+            if (++tt == tiles) { tt = 0; t = next_marked(t + 1); }
+        }
+        if (t < p.nb) load_q(t, tt, g);   // next step's rows, in flight during this step
+        __syncthreads();
+        f32x16 s, dp;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
+        s = mma_32x32x64(Ks + 32 * kh * kLd, Qs + 32 * qh * kLd, s, lane);    // S^T: keys x queries
+        dp = mma_32x32x64(Vs + 32 * kh * kLd, Gs + 32 * qh * kLd, dp, lane);  // dP^T
+        const int qc = 32 * qh + (lane & 31);
+        const float l2 = lse_s[qc], dl = dl_s[qc];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int kr = 32 * kh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+            const float pr = exp2f(s[e] - l2);
+            const float ds = pr * (dp[e] - dl) * kLn2;
+            Ps[kr * kLd + qc] = (bf16_t)(pack_bf16x2(pr, 0.f) & 0xffffu);
+            Ds[kr * kLd + qc] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
+        }
+        __syncthreads();
+        dv = mma_32x32x64(Ps + 32 * kh * kLd, Gt + 32 * dh * kLd, dv, lane);
+        dk = mma_32x32x64(Ds + 32 * kh * kLd, Qt + 32 * dh * kLd, dk, lane);
     }
     const int64_t base = (((int64_t)b * p.N + key0) * p.Hk + c) * 64;
 #pragma unroll
