@@ -209,21 +209,45 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
 }
 
 // ------------------------------------------------------------------ grad k, grad v
-// grid (N / 64 key tiles, Hk, B)
+// grid (N / 64 key tiles, Hk, B).  Wave w = (key half kh = w / 2, query half qh = w % 2).  Per
+// step a wave forms S = q' k^T and dP = do v^T for its 32 queries x 32 keys; P and dS stay in
+// registers, where the accumulator layout (lane: one key column, 16 query rows) is exactly the
+// MFMA B operand of dV^T += do^T P and dK^T += q'^T dS with k running over those query rows;
+// the A operands (do^T, q'^T) are read from the transposed LDS copies in the same row order.
+// The two waves of a key half sum their partial dV^T / dK^T once, at the end.
+__device__ __forceinline__ bf16x8 lds_rows_perm(const bf16_t* row, int q0) {
+    // 4 + 4 consecutive elements at q0 .. q0+3 and q0+8 .. q0+11: the accumulator row order
+    const uint2 lo = *reinterpret_cast<const uint2*>(row + q0);
+    const uint2 hi = *reinterpret_cast<const uint2*>(row + q0 + 8);
+    return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
 __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
-    __shared__ __attribute__((aligned(16))) bf16_t Ks[64 * kLd], Vs[64 * kLd], Qs[64 * kLd], Qt[64 * kLd],
-        Gs[64 * kLd], Gt[64 * kLd], Ps[64 * kLd], Ds[64 * kLd];
+    __shared__ __attribute__((aligned(16))) bf16_t smem[6 * 64 * kLd];
     __shared__ float lse_s[64], dl_s[64];
     __shared__ uint8_t mark[kMaxBwdBlocks];
+    bf16_t* Ks = smem;
+    bf16_t* Vs = smem + 64 * kLd;
+    bf16_t* Qs = smem + 2 * 64 * kLd;
+    bf16_t* Qt = smem + 3 * 64 * kLd;
+    bf16_t* Gs = smem + 4 * 64 * kLd;
+    bf16_t* Gt = smem + 5 * 64 * kLd;
     const int kt = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int key0 = kt * 64;
     const int64_t u = key0 / p.bs;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    // query blocks whose selection row (kv head c) holds block u
+    // query blocks whose selection row (kv head c) holds block u: eight entries per step, all
+    // loads of a step issued before any compare
     for (int t = threadIdx.x; t < p.nb; t += 256) {
         const int64_t* row = p.idx + (((int64_t)b * p.nb + t) * p.Hk + c) * p.K;
         bool hit = false;
-        for (int i = 0; i < p.K; ++i) hit |= row[i] == u;
+        for (int i0 = 0; i0 < p.K; i0 += 8) {
+            int64_t e[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) e[i] = i0 + i < p.K ? row[i0 + i] : -1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hit |= e[i] == u;
+        }
         mark[t] = hit;
     }
     stage_rows<false, false>(p.k + (int64_t)b * p.k_sb + (int64_t)key0 * p.k_sn + (int64_t)c * p.k_sh, p.k_sn, Ks,
@@ -231,11 +255,11 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
     stage_rows<false, false>(p.v + (int64_t)b * p.v_sb + (int64_t)key0 * p.v_sn + (int64_t)c * p.v_sh, p.v_sn, Vs,
                              nullptr, 0.f);
     __syncthreads();
-    const int kh = w >> 1, qh = w & 1;   // phase 2: key half, query half
-    const int dh = w & 1;                // phase 3: dim half (key half kh)
-    f32x16 dk, dv;
+    const int kh = w >> 1, qh = w & 1;
+    const int hq = 4 * (lane >> 5);         // this lane's row offset inside each group of 8 rows
+    f32x16 dkT[2], dvT[2];                  // [d block]: rows d = 32 db + row(e), column key 32 kh + lane % 32
 #pragma unroll
-    for (int e = 0; e < 16; ++e) { dk[e] = 0.f; dv[e] = 0.f; }
+    for (int e = 0; e < 16; ++e) { dkT[0][e] = 0.f; dkT[1][e] = 0.f; dvT[0][e] = 0.f; dvT[1][e] = 0.f; }
     // steps: (marked query block t, its 64-row tile tt, query head g of the group), ascending
     const int tiles = p.bs / 64;
     auto next_marked = [&](int t) {   // first marked block >= t (uniform LDS reads)
@@ -258,7 +282,7 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
     };
     if (t < p.nb) load_q(t, 0, 0);
     while (t < p.nb) {
-        __syncthreads();   // previous step's readers are done with Qs .. Ds
+        __syncthreads();   // previous step's readers are done with Qs .. Gt
         store_rows<true, true>(qr, Qs, Qt, p.scale);
         store_rows<false, true>(gr, Gs, Gt, 0.f);
         if (threadIdx.x < 64) {
@@ -274,29 +298,50 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
         f32x16 s, dp;
 #pragma unroll
         for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
-        s = mma_32x32x64(Ks + 32 * kh * kLd, Qs + 32 * qh * kLd, s, lane);    // S^T: keys x queries
-        dp = mma_32x32x64(Vs + 32 * kh * kLd, Gs + 32 * qh * kLd, dp, lane);  // dP^T
-        const int qc = 32 * qh + (lane & 31);
-        const float l2 = lse_s[qc], dl = dl_s[qc];
+        s = mma_32x32x64(Qs + 32 * qh * kLd, Ks + 32 * kh * kLd, s, lane);    // S: queries x keys
+        dp = mma_32x32x64(Gs + 32 * qh * kLd, Vs + 32 * kh * kLd, dp, lane);  // dP
+        bf16x8 pb[2], db[2];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const int kr = 32 * kh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            const float pr = exp2f(s[e] - l2);
-            const float ds = pr * (dp[e] - dl) * kLn2;
-            Ps[kr * kLd + qc] = (bf16_t)(pack_bf16x2(pr, 0.f) & 0xffffu);
-            Ds[kr * kLd + qc] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
+            const int q = 32 * qh + 8 * (e >> 2) + hq + (e & 3);
+            const float pr = exp2f(s[e] - lse_s[q]);
+            const float ds = pr * (dp[e] - dl_s[q]) * kLn2;
+            pb[e >> 3][e & 7] = (__bf16)pr;
+            db[e >> 3][e & 7] = (__bf16)ds;
         }
-        __syncthreads();
-        dv = mma_32x32x64(Ps + 32 * kh * kLd, Gt + 32 * dh * kLd, dv, lane);
-        dk = mma_32x32x64(Ds + 32 * kh * kLd, Qt + 32 * dh * kLd, dk, lane);
-    }
-    const int64_t base = (((int64_t)b * p.N + key0) * p.Hk + c) * 64;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int kr = 32 * kh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        const int64_t off = base + (int64_t)kr * p.Hk * 64 + 32 * dh + (lane & 31);
-        p.dk[off] = (bf16_t)(pack_bf16x2(dk[e], 0.f) & 0xffffu);
-        p.dv[off] = (bf16_t)(pack_bf16x2(dv[e], 0.f) & 0xffffu);
+        for (int dblk = 0; dblk < 2; ++dblk) {
+            const bf16_t* grow = Gt + (32 * dblk + (lane & 31)) * kLd;
+            const bf16_t* qrow = Qt + (32 * dblk + (lane & 31)) * kLd;
+#pragma unroll
+            for (int ch = 0; ch < 2; ++ch) {
+                const int q0 = 32 * qh + 16 * ch + hq;
+                dvT[dblk] = mfma32(lds_rows_perm(grow, q0), pb[ch], dvT[dblk]);
+                dkT[dblk] = mfma32(lds_rows_perm(qrow, q0), db[ch], dkT[dblk]);
+            }
+        }
+    }
+    // sum the two query halves' partials: qh = 1 parks its accumulators in LDS
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(smem) + (kh * 64 + lane) * 64;
+    if (qh == 1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            red[e] = dkT[0][e]; red[16 + e] = dkT[1][e]; red[32 + e] = dvT[0][e]; red[48 + e] = dvT[1][e];
+        }
+    }
+    __syncthreads();
+    if (qh == 0) {
+        const int64_t base = (((int64_t)b * p.N + key0 + 32 * kh + (lane & 31)) * p.Hk + c) * 64;
+#pragma unroll
+        for (int dblk = 0; dblk < 2; ++dblk) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int d = 32 * dblk + 8 * (e >> 2) + hq + (e & 3);
+                p.dk[base + d] = (bf16_t)(pack_bf16x2(dkT[dblk][e] + red[16 * dblk + e], 0.f) & 0xffffu);
+                p.dv[base + d] = (bf16_t)(pack_bf16x2(dvT[dblk][e] + red[32 + 16 * dblk + e], 0.f) & 0xffffu);
+            }
+        }
     }
 }
 
