@@ -141,3 +141,50 @@ def test_knn_interp_entry_validates():
     assert call(num_to=0) == 8 and call(batch=-1) == 8
     assert call(wq=FAKE + 8) == 7 and call(out=FAKE + 2) == 7 and call(rel=FAKE + 2) == 7
     assert call(kk=_lib.Bnhd(FAKE + 2, 3 * 64, 2 * 3 * 64, 64)) == 7
+
+
+def test_backward_entry_validates():
+    L = _lib.lib()
+    t = _lib.Bnhd(FAKE, 0, 64 * 4, 64)
+    ws = L.mosaic_sparse_attn_bwd_workspace_size(1, 256, 4)
+    assert ws == (256 * 4 * 4 + 255) // 256 * 256
+
+    def call(q=t, out=FAKE, lse=FAKE, idx=FAKE, N=256, Hq=4, Hk=1, d=64, bs=64, K=2, gq=FAKE, w=FAKE, wsb=ws):
+        return L.mosaic_sparse_attn_bwd(q, t, t, out, lse, t, idx, 1, N, Hq, Hk, d, bs, K, 0.0, gq, FAKE, FAKE,
+                                        w, wsb, None)
+    assert call(d=32) == 2
+    assert call(Hq=4, Hk=3) == 3
+    assert call(bs=96) == 4 and call(N=200) == 4
+    assert call(K=0) == 5
+    assert call(N=64 * 5000) == 11                       # more query blocks than the LDS marks hold
+    assert call(out=None) == 1 and call(lse=None) == 1 and call(idx=None) == 1 and call(gq=None) == 1
+    assert call(q=_lib.Bnhd(FAKE + 2, 0, 256, 64)) == 7 and call(gq=FAKE + 4) == 7
+    assert call(w=None) == 6 and call(wsb=ws - 1) == 6
+
+
+def test_fused_elementwise_entries_validate():
+    L = _lib.lib()
+    F32, BF = _lib.DTYPE_F32, _lib.DTYPE_BF16
+    # rms_norm(x, residual, dtype, rows, cols, x_stride, r_stride, weight, eps, sum_out, out, out_dtype, stream)
+    assert L.mosaic_rms_norm_fwd(FAKE, None, BF, 0, 768, 768, 0, None, 0.0, None, FAKE, BF, None) == 8
+    assert L.mosaic_rms_norm_fwd(FAKE, None, 5, 4, 768, 768, 0, None, 0.0, None, FAKE, BF, None) == 11
+    assert L.mosaic_rms_norm_fwd(FAKE, None, BF, 4, 770, 770, 0, None, 0.0, None, FAKE, BF, None) == 11
+    assert L.mosaic_rms_norm_fwd(FAKE, None, BF, 4, 8192, 8192, 0, None, 0.0, None, FAKE, BF, None) == 11
+    assert L.mosaic_rms_norm_fwd(FAKE, FAKE, BF, 4, 768, 768, 768, None, 0.0, None, FAKE, BF, None) == 1
+    assert L.mosaic_rms_norm_fwd(None, None, BF, 4, 768, 768, 0, None, 0.0, None, FAKE, BF, None) == 1
+    assert L.mosaic_rms_norm_fwd(FAKE + 2, None, BF, 4, 768, 768, 0, None, 0.0, None, FAKE, BF, None) == 7
+    assert L.mosaic_rms_norm_fwd(FAKE, None, BF, 4, 768, 772, 0, None, 0.0, None, FAKE, F32, None) == 7
+    # swiglu(h, dtype, rows, hidden, h_stride, noise, noise_rows, out, stream)
+    assert L.mosaic_swiglu_fwd(FAKE, BF, 0, 3072, 6144, None, 0, FAKE, None) == 8
+    assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3070, 6140, None, 0, FAKE, None) == 11
+    assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3072, 6000, None, 0, FAKE, None) == 8
+    assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3072, 6144, FAKE, 0, FAKE, None) == 8
+    assert L.mosaic_swiglu_fwd(None, BF, 4, 3072, 6144, None, 0, FAKE, None) == 1
+    assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3072, 6144, FAKE + 8, 2, FAKE, None) == 7
+
+
+def test_bsa_fwd_output_strides_validate():
+    L = _lib.lib()
+    a = _args()
+    a.out_stride_n = 20 * 64 + 4                       # rows must stay 16-byte aligned
+    assert L.mosaic_bsa_fwd(ctypes.byref(a), None, 0, None) == 7
