@@ -213,25 +213,34 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
 // step a wave forms S = q' k^T and dP = do v^T for its 32 queries x 32 keys; P and dS stay in
 // registers, where the accumulator layout (lane: one key column, 16 query rows) is exactly the
 // MFMA B operand of dV^T += do^T P and dK^T += q'^T dS with k running over those query rows;
-// the A operands (do^T, q'^T) are read from the transposed LDS copies in the same row order.
+// the A operands (do^T, q'^T) come from transposing LDS reads of the row-major tiles in the
+// same row order, so no transposed copy is staged.
 // The two waves of a key half sum their partial dV^T / dK^T once, at the end.
-__device__ __forceinline__ bf16x8 lds_rows_perm(const bf16_t* row, int q0) {
-    // 4 + 4 consecutive elements at q0 .. q0+3 and q0+8 .. q0+11: the accumulator row order
-    const uint2 lo = *reinterpret_cast<const uint2*>(row + q0);
-    const uint2 hi = *reinterpret_cast<const uint2*>(row + q0 + 8);
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// MFMA A operand of the transpose of a row-major LDS tile T[token][dim] (row stride kLd): lane
+// l receives dim d0 + l % 32 for tokens t0 + 4 (l / 32) + 0..3 and t0 + 8 + 4 (l / 32) + 0..3,
+// the accumulator row order of P and dS.  ds_read_b64_tr_b16 hands lane 4a + b of each
+// 16-lane group element b of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12, so
+// lane s of a group addresses token 4 (l / 32) + s / 4, dims 16 ((l / 16) % 2) + 4 (s % 4).
+__device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t* T, int t0, int d0, int lane) {
+    const int s = lane & 15;
+    const bf16_t* p = T + (t0 + 4 * (lane >> 5) + (s >> 2)) * kLd + d0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+    const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                   (__attribute__((address_space(3))) v4i16*)(p)));
+    const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                   (__attribute__((address_space(3))) v4i16*)(p + 8 * kLd)));
     return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
 __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
-    __shared__ __attribute__((aligned(16))) bf16_t smem[6 * 64 * kLd];
+    __shared__ __attribute__((aligned(16))) bf16_t smem[4 * 64 * kLd];   // also the final 32 KB reduction
     __shared__ float lse_s[64], dl_s[64];
     __shared__ uint8_t mark[kMaxBwdBlocks];
     bf16_t* Ks = smem;
     bf16_t* Vs = smem + 64 * kLd;
     bf16_t* Qs = smem + 2 * 64 * kLd;
-    bf16_t* Qt = smem + 3 * 64 * kLd;
-    bf16_t* Gs = smem + 4 * 64 * kLd;
-    bf16_t* Gt = smem + 5 * 64 * kLd;
+    bf16_t* Gs = smem + 3 * 64 * kLd;
     const int kt = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int key0 = kt * 64;
     const int64_t u = key0 / p.bs;
@@ -282,9 +291,9 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
     };
     if (t < p.nb) load_q(t, 0, 0);
     while (t < p.nb) {
-        __syncthreads();   // previous step's readers are done with Qs .. Gt
-        store_rows<true, true>(qr, Qs, Qt, p.scale);
-        store_rows<false, true>(gr, Gs, Gt, 0.f);
+        __syncthreads();   // previous step's readers are done with Qs / Gs
+        store_rows<true, false>(qr, Qs, nullptr, p.scale);
+        store_rows<false, false>(gr, Gs, nullptr, 0.f);
         if (threadIdx.x < 64) {
             lse_s[threadIdx.x] = lr;
             dl_s[threadIdx.x] = dr;
@@ -311,13 +320,11 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
         }
 #pragma unroll
         for (int dblk = 0; dblk < 2; ++dblk) {
-            const bf16_t* grow = Gt + (32 * dblk + (lane & 31)) * kLd;
-            const bf16_t* qrow = Qt + (32 * dblk + (lane & 31)) * kLd;
 #pragma unroll
             for (int ch = 0; ch < 2; ++ch) {
-                const int q0 = 32 * qh + 16 * ch + hq;
-                dvT[dblk] = mfma32(lds_rows_perm(grow, q0), pb[ch], dvT[dblk]);
-                dkT[dblk] = mfma32(lds_rows_perm(qrow, q0), db[ch], dkT[dblk]);
+                const int q0 = 32 * qh + 16 * ch;
+                dvT[dblk] = mfma32(lds_tr_operand(Gs, q0, 32 * dblk, lane), pb[ch], dvT[dblk]);
+                dkT[dblk] = mfma32(lds_tr_operand(Qs, q0, 32 * dblk, lane), db[ch], dkT[dblk]);
             }
         }
     }
