@@ -138,11 +138,37 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
     if ((lane & 7) == 0) p.delta[row] = round_bf16(s);
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// MFMA A operand of the transpose of a row-major LDS tile T[token][dim] (row stride kLd): lane
+// l receives dim d0 + l % 32 for tokens t0 + 4 (l / 32) + 0..3 and t0 + 8 + 4 (l / 32) + 0..3,
+// the accumulator row order of P and dS.  ds_read_b64_tr_b16 hands lane 4a + b of each
+// 16-lane group element b of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12, so
+// lane s of a group addresses token 4 (l / 32) + s / 4, dims 16 ((l / 16) % 2) + 4 (s % 4).
+__device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t* T, int t0, int d0, int lane) {
+    const int s = lane & 15;
+    const bf16_t* p = T + (t0 + 4 * (lane >> 5) + (s >> 2)) * kLd + d0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+    const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                   (__attribute__((address_space(3))) v4i16*)(p)));
+    const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                   (__attribute__((address_space(3))) v4i16*)(p + 8 * kLd)));
+    return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
+// The same row order from a row-major tile read along its rows: elements k0 + 4 (l / 32) + 0..3
+// and k0 + 8 + 4 (l / 32) + 0..3 of row r.
+__device__ __forceinline__ bf16x8 lds_row_perm(const bf16_t* T, int r, int k0, int lane) {
+    const bf16_t* p = T + r * kLd + k0 + 4 * (lane >> 5);
+    const uint2 lo = *reinterpret_cast<const uint2*>(p);
+    const uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
+    return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
 // ------------------------------------------------------------------ grad q
 // grid (N / 64 query tiles, Hq, B)
 __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
-    __shared__ __attribute__((aligned(16))) bf16_t Qs[64 * kLd], Gs[64 * kLd], Ks[64 * kLd], Kt[64 * kLd],
-        Vs[64 * kLd], Ds[64 * kLd];
+    __shared__ __attribute__((aligned(16))) bf16_t Qs[64 * kLd], Gs[64 * kLd], Ks[64 * kLd], Vs[64 * kLd],
+        Ds[64 * kLd];
     __shared__ float lse_s[64], dl_s[64];
     const int qt = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
     const int c = j / p.G;
@@ -178,8 +204,8 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
     };
     if (i < p.K) load_kv(i, 0);
     while (i < p.K) {
-        __syncthreads();   // previous step's readers of Ks / Kt / Vs / Ds are done
-        store_rows<false, true>(kr, Ks, Kt, 0.f);
+        __syncthreads();   // previous step's readers of Ks / Vs / Ds are done
+        store_rows<false, false>(kr, Ks, nullptr, 0.f);
         store_rows<false, false>(vr, Vs, nullptr, 0.f);
         if (++t == tiles) { t = 0; i = next_valid(i + 1); }
         if (i < p.K) load_kv(i, t);   // next step's tiles, in flight during this step
@@ -197,7 +223,12 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
             Ds[r * kLd + 32 * kh + (lane & 31)] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
         }
         __syncthreads();
-        acc = mma_32x32x64(Ds + 32 * rh * kLd, Kt + 32 * dh * kLd, acc, lane);
+        // dQ += dS k: A = dS rows and B = k^T (transposing reads of the row-major k tile), both
+        // with the keys of each 16-key step in the order 4 (l / 32) + 0..3, 8 + 4 (l / 32) + 0..3
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+            acc = mfma32(lds_row_perm(Ds, 32 * rh + (lane & 31), 16 * kk, lane),
+                         lds_tr_operand(Ks, 16 * kk, 32 * dh, lane), acc);
     }
     bf16_t* out = p.dq + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
 #pragma unroll
@@ -216,23 +247,6 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
 // the A operands (do^T, q'^T) come from transposing LDS reads of the row-major tiles in the
 // same row order, so no transposed copy is staged.
 // The two waves of a key half sum their partial dV^T / dK^T once, at the end.
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-
-// MFMA A operand of the transpose of a row-major LDS tile T[token][dim] (row stride kLd): lane
-// l receives dim d0 + l % 32 for tokens t0 + 4 (l / 32) + 0..3 and t0 + 8 + 4 (l / 32) + 0..3,
-// the accumulator row order of P and dS.  ds_read_b64_tr_b16 hands lane 4a + b of each
-// 16-lane group element b of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12, so
-// lane s of a group addresses token 4 (l / 32) + s / 4, dims 16 ((l / 16) % 2) + 4 (s % 4).
-__device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t* T, int t0, int d0, int lane) {
-    const int s = lane & 15;
-    const bf16_t* p = T + (t0 + 4 * (lane >> 5) + (s >> 2)) * kLd + d0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
-    const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                   (__attribute__((address_space(3))) v4i16*)(p)));
-    const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                   (__attribute__((address_space(3))) v4i16*)(p + 8 * kLd)));
-    return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-}
-
 __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
     __shared__ __attribute__((aligned(16))) bf16_t smem[4 * 64 * kLd];   // also the final 32 KB reduction
     __shared__ float lse_s[64], dl_s[64];
