@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 2
+#define MOSAIC_BSA_ABI_VERSION 3
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -42,7 +42,8 @@ typedef enum {
     MOSAIC_ERR_SHAPE = 8,          /* non-positive or too large sizes                     */
     MOSAIC_ERR_LAUNCH = 9,         /* the HIP runtime rejected a kernel launch            */
     MOSAIC_ERR_MODE = 10,          /* unknown mode                                        */
-    MOSAIC_ERR_UNSUPPORTED = 11    /* valid request outside the library's limits          */
+    MOSAIC_ERR_UNSUPPORTED = 11,   /* valid request outside the library's limits          */
+    MOSAIC_ERR_SCRATCH_LIMIT = 12  /* mosaic_bsa_fwd_noalloc: workspace > static scratch  */
 } mosaic_status;
 
 /* Branch combination, matching mosaic_attn_func (primitives.py:54-89). */
@@ -102,6 +103,23 @@ MOSAIC_API size_t mosaic_bsa_workspace_size(const mosaic_bsa_args* args);
    mosaic_bsa_workspace_size(args) bytes, 256-byte aligned.  stream: hipStream_t. */
 MOSAIC_API int mosaic_bsa_fwd(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes,
                    void* stream);
+
+/* Size of the static device scratch that mosaic_bsa_fwd_noalloc uses as its workspace. */
+#define MOSAIC_BSA_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+
+/* mosaic_bsa_fwd without a workspace argument, for callers that cannot allocate device memory
+   (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+   counterpart in the reference.  The caller still passes inputs and outputs; the workspace is
+   a static device array of MOSAIC_BSA_NOALLOC_SCRATCH_BYTES, one copy per GPU, held from the
+   library's load until the process ends.  Its address is resolved once per device, on the
+   first call with that device current; the call runs on the current device, and stream must
+   belong to it.  Nothing is allocated and nothing synchronises the host.  A request whose
+   mosaic_bsa_workspace_size() exceeds the scratch returns MOSAIC_ERR_SCRATCH_LIMIT before any
+   launch (128 MiB covers e.g. N = 196608 with 12/3 heads and 64-token blocks, or 24 members of
+   N = 12288 with 16/4 heads).  Every call on one GPU shares that GPU's array, which keeps the
+   last call's contents: calls that overlap on one GPU (unordered streams, or threads) race
+   and corrupt each other's results. */
+MOSAIC_API int mosaic_bsa_fwd_noalloc(const mosaic_bsa_args* args, void* stream);
 
 /* As mosaic_bsa_fwd, recording events[0..4] (hipEvent_t) on the stream before the pooling
    kernel, before the compressed/score kernel, before the top-k kernel, before the attention

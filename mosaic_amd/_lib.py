@@ -12,13 +12,17 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # mosaic_bsa_mode
 MODE_FULL = 0
 MODE_LOCAL_ONLY = 1
 MODE_NO_COMPRESSION = 2
 MODE_NO_SELECTION = 3
+
+# mosaic_status values the Python side names
+ERR_SCRATCH_LIMIT = 12
+NOALLOC_SCRATCH_BYTES = 128 << 20
 
 # mosaic_dtype
 DTYPE_F32 = 0
@@ -27,6 +31,7 @@ DTYPE_BF16 = 1
 EXPORTED_SYMBOLS = (
     "mosaic_bsa_workspace_size",
     "mosaic_bsa_fwd",
+    "mosaic_bsa_fwd_noalloc",
     "mosaic_bsa_fwd_profiled",
     "mosaic_bsa_fwd_rope",
     "mosaic_knn_interp_fwd",
@@ -82,6 +87,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_bsa_workspace_size.restype = c_size
     lib.mosaic_bsa_fwd.argtypes = [P(BsaArgs), c_vp, c_size, c_vp]
     lib.mosaic_bsa_fwd.restype = c_int
+    lib.mosaic_bsa_fwd_noalloc.argtypes = [P(BsaArgs), c_vp]
+    lib.mosaic_bsa_fwd_noalloc.restype = c_int
     lib.mosaic_bsa_fwd_profiled.argtypes = [P(BsaArgs), c_vp, c_size, c_vp, P(c_vp)]
     lib.mosaic_bsa_fwd_profiled.restype = c_int
     lib.mosaic_bsa_fwd_rope.argtypes = [P(BsaArgs), c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]

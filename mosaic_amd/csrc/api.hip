@@ -5,12 +5,19 @@
 //   pool (q, k, v -> pooled)  ->  cmp (compressed attention partials + selection scores)
 //   ->  top-k (indices)  ->  attn (local + selected + merge)
 // Nothing here allocates device memory or synchronises the host.
+#include <atomic>
 #include <cmath>
+#include <mutex>
 
 #include "bsa_common.h"
 #include "mosaic_bsa.h"
 
 using namespace mosaic;
+
+// Workspace of mosaic_bsa_fwd_noalloc: a static device array, one copy per GPU, alive until the
+// process ends.  Its host-side name is only a handle for hipGetSymbolAddress; kernels receive
+// the device address that call returns (scratch_of_current_device).
+static __device__ __align__(256) unsigned char scratch[MOSAIC_BSA_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -134,6 +141,29 @@ AttnParams attn_params(const mosaic_bnhd& q, const mosaic_bnhd& k, const mosaic_
 }
 
 int launch_status(hipError_t e) { return e == hipSuccess ? MOSAIC_OK : MOSAIC_ERR_LAUNCH; }
+
+// Device address of `scratch` on the current device, resolved once per device (each GPU holds
+// its own copy of the array at its own address) and cached.
+constexpr int kMaxDevices = 256;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+int scratch_of_current_device(void** out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return MOSAIC_ERR_LAUNCH;
+    if (dev >= kMaxDevices) return MOSAIC_ERR_UNSUPPORTED;
+    void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+        if (p == nullptr) {
+            if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return MOSAIC_ERR_LAUNCH;
+            g_scratch_ptr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return MOSAIC_OK;
+}
 
 int record(void* const* events, int i, hipStream_t s) {
     if (events == nullptr || events[i] == nullptr) return MOSAIC_OK;
@@ -286,6 +316,16 @@ size_t mosaic_bsa_workspace_size(const mosaic_bsa_args* args) {
 
 int mosaic_bsa_fwd(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes, void* stream) {
     return bsa_forward(args, workspace, workspace_bytes, stream, nullptr);
+}
+
+int mosaic_bsa_fwd_noalloc(const mosaic_bsa_args* args, void* stream) {
+    if (int e = validate(args)) return e;
+    const size_t need = layout_of(args).total;
+    if (need > MOSAIC_BSA_NOALLOC_SCRATCH_BYTES) return MOSAIC_ERR_SCRATCH_LIMIT;
+    void* ws = nullptr;
+    if (need > 0)
+        if (int e = scratch_of_current_device(&ws)) return e;
+    return bsa_forward(args, ws, need, stream, nullptr);
 }
 
 int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes, void* stream,
@@ -448,9 +488,10 @@ const char* mosaic_bsa_strerror(int status) {
         case MOSAIC_ERR_WORKSPACE: return "workspace missing, too small or not 256-byte aligned";
         case MOSAIC_ERR_ALIGNMENT: return "bf16 rows must be 16-byte aligned (pointer and strides multiples of 8 elements)";
         case MOSAIC_ERR_SHAPE: return "invalid sizes";
-        case MOSAIC_ERR_LAUNCH: return "kernel launch failed";
+        case MOSAIC_ERR_LAUNCH: return "the HIP runtime rejected a kernel launch or call";
         case MOSAIC_ERR_MODE: return "unknown mode";
         case MOSAIC_ERR_UNSUPPORTED: return "outside the library's limits (query heads per kv head <= 16, blocks <= 8192, selected blocks <= 1024)";
+        case MOSAIC_ERR_SCRATCH_LIMIT: return "the request needs more workspace than the static scratch of mosaic_bsa_fwd_noalloc (128 MiB)";
         default: return "unknown status";
     }
 }

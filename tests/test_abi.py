@@ -35,7 +35,7 @@ def test_abi_version_and_strerror():
     L = _lib.lib()
     assert L.mosaic_bsa_abi_version() == _lib.ABI_VERSION
     assert _lib.strerror(0) == "ok"
-    for code in range(1, 12):
+    for code in range(1, 13):
         assert _lib.strerror(code) not in ("ok", "unknown status")
     assert _lib.strerror(999) == "unknown status"
 
@@ -92,6 +92,17 @@ def test_workspace_size_and_missing_workspace():
     assert L.mosaic_bsa_fwd(ctypes.byref(a), FAKE, n - 1, None) == 6    # too small
     local = _args(mode=_lib.MODE_LOCAL_ONLY, weights=None)
     assert L.mosaic_bsa_workspace_size(ctypes.byref(local)) == 0
+
+
+def test_noalloc_entry_validates_before_touching_the_device():
+    L = _lib.lib()
+    assert L.mosaic_bsa_fwd_noalloc(ctypes.byref(_args(head_dim=32)), None) == 2
+    assert L.mosaic_bsa_fwd_noalloc(ctypes.byref(_args(out=None)), None) == 1
+    # N = 393216 in 64-token blocks: the selection scores alone are 5 * 6144 * 6144 * 2 bytes
+    big = _args(seq_len=393216)
+    assert L.mosaic_bsa_workspace_size(ctypes.byref(big)) > _lib.NOALLOC_SCRATCH_BYTES
+    assert L.mosaic_bsa_fwd_noalloc(ctypes.byref(big), None) == _lib.ERR_SCRATCH_LIMIT
+    assert "static scratch" in _lib.strerror(_lib.ERR_SCRATCH_LIMIT)
 
 
 def test_fused_rope_entry_validates():
