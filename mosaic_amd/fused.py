@@ -18,7 +18,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .ops import stream_of
+from .ops import forward_only, stream_of
 
 __all__ = ["RMSNorm", "rms_norm", "swiglu", "autocast_dtype"]
 
@@ -59,6 +59,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
     Returns ``out`` (dtype ``out_dtype``, default x's), or ``(x + residual, out)`` when a
     residual is given; the sum has x's dtype, rounded as torch's add rounds.
     """
+    forward_only("fused.rms_norm", x, weight, residual)
     if not x.is_cuda:
         raise ValueError("fused.rms_norm needs a ROCm device tensor")
     if residual is not None and residual.dtype != x.dtype:
@@ -74,7 +75,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
     out = torch.empty(shape, dtype=out_dtype, device=x.device)
     w = None
     if weight is not None:
-        w = weight.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        w = weight.to(device=x.device, dtype=torch.float32).contiguous()
     r2, rs, s_out = None, 0, None
     if residual is not None:
         r2, rs = _rows(residual.expand(shape))
@@ -90,6 +91,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
 def swiglu(h: torch.Tensor, noise: torch.Tensor | None = None) -> torch.Tensor:
     """``silu(x1 + noise) * x3`` for ``x1, x3 = h.chunk(2, -1)``; h is ``[S, B, 2*hidden]``
     (sequence-first) and noise, if given, ``[B, hidden]`` (one row per batch member)."""
+    forward_only("fused.swiglu", h, noise)
     if not h.is_cuda:
         raise ValueError("fused.swiglu needs a ROCm device tensor")
     if h.dtype not in _DT:
@@ -113,7 +115,9 @@ def swiglu(h: torch.Tensor, noise: torch.Tensor | None = None) -> torch.Tensor:
 class RMSNorm(nn.RMSNorm):
     """``torch.nn.RMSNorm`` (same parameters and eps rule) whose forward on a ROCm device is
     one fused kernel: fp32 statistics, output in the autocast dtype when autocast is on (the
-    module's output dtype under the reference's bf16 autocast), else in the input's dtype."""
+    module's output dtype under the reference's bf16 autocast), else in the input's dtype.
+    Forward-only on the device: with grad mode on and an input or the weight requiring grad it
+    raises rather than return an output without a graph."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.is_cuda:

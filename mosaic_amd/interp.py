@@ -18,7 +18,7 @@ import torch.nn as nn
 
 from . import _lib
 from .fused import RMSNorm
-from .ops import stream_of
+from .ops import forward_only, stream_of
 
 
 def rad_to_xyz(lonlat: torch.Tensor) -> torch.Tensor:
@@ -51,8 +51,12 @@ def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel
     [S_to, B, H, 64] bf16: for each target, softmax over its K neighbours of
     ``to_q(rel_pos) . k * scale``, applied to v.
     """
+    forward_only("knn_attention", k, v, rel_pos, w_q)
     if k.dim() != 4 or k.shape != v.shape or k.shape[-1] != 64:
         raise ValueError(f"k and v must both be [S_from, B, H, 64], got {tuple(k.shape)} and {tuple(v.shape)}")
+    if torch.float16 in (k.dtype, v.dtype):
+        raise TypeError("k / v are float16: the kernel computes in bfloat16 (run the model under "
+                        "torch.autocast(..., dtype=torch.bfloat16), or convert the inputs)")
     if k.device.type != "cuda":
         raise ValueError("k and v must be on a ROCm device")
     S_from, B, H, d = k.shape

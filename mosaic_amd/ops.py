@@ -11,8 +11,10 @@ Same names and arguments as the reference:
 
 q [B, N, Hq, 64], k/v [B, N, Hk, 64] on a ROCm device; block_indices int64 [B, N/bs, Hk, K].
 Work is enqueued on the current stream.  The computation is bf16 (like the reference kernel,
-which casts q/k/v to bf16, ops.py:92,115-116); other input dtypes are converted to bf16 and
-the output is returned in q's dtype (ops.py:538).
+which casts q/k/v to bf16, ops.py:92,115-116); fp16 and fp32 inputs are converted to bf16 and
+the output is returned in q's dtype (ops.py:538).  As in the reference, ``MosaicAttnFunction``
+is marked ``torch.amp.custom_fwd`` / ``custom_bwd`` (ops.py:513, 541), so its backward runs
+under the forward's autocast state.
 """
 
 from __future__ import annotations
@@ -22,9 +24,35 @@ import torch
 from . import _lib
 
 
-def _as_bf16_bnhd(t: torch.Tensor, name: str) -> torch.Tensor:
+def forward_only(what: str, *tensors) -> None:
+    """Raise where autograd would need a backward that ``what`` does not have.
+
+    The three-branch op, the local / dense / pooling pieces, the fused norm and gate and the
+    k-NN interpolation have no backward here (the reference differentiates them through
+    flash-attn and eager torch); only the selected branch (``mosaic_sparse_attn``) does.  Rather
+    than return outputs cut off from the graph, these ops refuse inputs that require grad while
+    grad mode is on.
+    """
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors):
+        raise RuntimeError(
+            f"{what} has no backward in mosaic_amd: call it under torch.no_grad() or "
+            "torch.inference_mode(), or on tensors that do not require grad (the selected branch, "
+            "mosaic_sparse_attn, is differentiable)")
+
+
+def _as_bf16_bnhd(t: torch.Tensor, name: str, allow_fp16: bool = False) -> torch.Tensor:
+    """t as a bf16 [B, N, H, d] device tensor with 16-byte rows (copying only if needed).
+
+    float16 is refused unless ``allow_fp16``: the kernels compute in bf16, and where the
+    reference computes in fp16 (flash-attn under fp16 autocast) converting would silently drop
+    three mantissa bits.  The selected branch converts fp16 to bf16 as the reference's own
+    kernel does (ops.py:92, 115-116), so it allows it.
+    """
     if t.dim() != 4:
         raise ValueError(f"{name} must be [B, N, H, d], got shape {tuple(t.shape)}")
+    if t.dtype == torch.float16 and not allow_fp16:
+        raise TypeError(f"{name} is float16: these kernels compute in bfloat16 (run the model under "
+                        "torch.autocast(..., dtype=torch.bfloat16), or convert the inputs)")
     if t.device.type != "cuda":
         raise ValueError(f"{name} must be on a ROCm device, got {t.device}")
     if t.dtype != torch.bfloat16:
@@ -52,7 +80,7 @@ def _check_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
 def mosaic_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_indices: torch.Tensor,
                     block_size: int, softmax_scale: float):
     """(output bf16 [B, N, Hq, d], lse fp32 [B, N, Hq]) of the selected-branch attention."""
-    q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    q, k, v = (_as_bf16_bnhd(t, n, allow_fp16=True) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     _check_gqa(q, k, v)
     B, N, Hq, d = q.shape
     Hk = k.shape[2]
@@ -75,15 +103,24 @@ def mosaic_attn_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, output: t
     """(grad_q, grad_k, grad_v) of the selected-branch attention (ops.py:437-507), in q's / k's /
     v's dtypes; keys no query block selected get zero gradients."""
     dtypes = (q.dtype, k.dtype, v.dtype)
-    q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
-    go = _as_bf16_bnhd(grad_o, "grad_o")
+    q, k, v = (_as_bf16_bnhd(t, n, allow_fp16=True) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    go = _as_bf16_bnhd(grad_o, "grad_o", allow_fp16=True)
     _check_gqa(q, k, v)
     B, N, Hq, d = q.shape
     Hk = k.shape[2]
     if tuple(go.shape) != (B, N, Hq, d):
         raise ValueError(f"grad_o shape {tuple(go.shape)} != {(B, N, Hq, d)}")
-    o = output.to(torch.bfloat16).contiguous()
-    lse = lse.to(torch.float32).contiguous()
+    # the kernels index these as contiguous [B, N, Hq, 64], [B, N, Hq] and [B, N/bs, Hk, K]
+    if tuple(output.shape) != (B, N, Hq, d):
+        raise ValueError(f"output shape {tuple(output.shape)} != {(B, N, Hq, d)}")
+    if tuple(lse.shape) != (B, N, Hq):
+        raise ValueError(f"lse shape {tuple(lse.shape)} != {(B, N, Hq)}")
+    if block_size <= 0 or N % block_size:
+        raise ValueError(f"block_size {block_size} must divide the sequence length {N}")
+    if block_indices.dim() != 4 or tuple(block_indices.shape[:3]) != (B, N // block_size, Hk):
+        raise ValueError(f"block_indices shape {tuple(block_indices.shape)} != {(B, N // block_size, Hk, '*')}")
+    o = output.to(device=q.device, dtype=torch.bfloat16).contiguous()
+    lse = lse.to(device=q.device, dtype=torch.float32).contiguous()
     idx = block_indices.to(device=q.device, dtype=torch.int64).contiguous()
     gq = torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=q.device)
     gk = torch.empty(B, N, Hk, d, dtype=torch.bfloat16, device=q.device)
@@ -104,6 +141,7 @@ class MosaicAttnFunction(torch.autograd.Function):
     q, k, v, the output, its LSE and the indices; the backward runs the HIP backward."""
 
     @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
     def forward(ctx, q, k, v, block_indices, block_size, softmax_scale):
         dtype = q.dtype
         output, lse = mosaic_attn_fwd(q, k, v, block_indices, block_size, softmax_scale)
@@ -113,6 +151,7 @@ class MosaicAttnFunction(torch.autograd.Function):
         return output.to(dtype)
 
     @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, grad_o):
         q, k, v, output, lse, block_indices = ctx.saved_tensors
         gq, gk, gv = mosaic_attn_bwd(q, k, v, output, lse, grad_o.contiguous(), ctx.softmax_scale,

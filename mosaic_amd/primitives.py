@@ -23,7 +23,7 @@ import torch.nn as nn
 
 from . import _lib
 from .healpix import rope_tables
-from .ops import _as_bf16_bnhd, _check_gqa, bnhd, mosaic_sparse_attn, stream_of
+from .ops import _as_bf16_bnhd, _check_gqa, bnhd, forward_only, mosaic_sparse_attn, stream_of
 
 __all__ = [
     "block_attention", "dense_attention", "pool_mean", "attn_topk", "mosaic_attn_func",
@@ -37,6 +37,7 @@ def _out_like(q: torch.Tensor) -> torch.Tensor:
 
 def block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_size: int) -> torch.Tensor:
     """Attention inside contiguous blocks of ``block_size`` tokens (primitives.py:28-32)."""
+    forward_only("block_attention", q, k, v)
     dtype = q.dtype
     q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     _check_gqa(q, k, v)
@@ -50,6 +51,7 @@ def block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_siz
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
     """Full-sequence attention (flash_attn_func defaults), the dense baseline."""
+    forward_only("dense_attention", q, k, v)
     dtype = q.dtype
     q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     _check_gqa(q, k, v)
@@ -63,6 +65,7 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.
 
 def pool_mean(x: torch.Tensor, block_size: int) -> torch.Tensor:
     """reduce(x, 'b (nb bs) h d -> b nb h d', 'mean', bs=block_size) in bf16 (primitives.py:65)."""
+    forward_only("pool_mean", x)
     x = _as_bf16_bnhd(x, "x")
     B, N, H, d = x.shape
     if N % block_size:
@@ -177,6 +180,7 @@ def mosaic_attn_func_rope(q, k, v, weight_ba_cmp_slc, rope_cos, rope_sin, block_
 
 def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
                  block_attn_only, no_compression, return_block_indices, rope, return_rotated=False, out=None):
+    forward_only("mosaic_attn_func", q, k, v, weight_ba_cmp_slc, *(rope or ()))
     dtype = q.dtype
     q, k, v = (_as_bf16_bnhd(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
     _check_gqa(q, k, v)
@@ -286,6 +290,9 @@ class MosaicAttention(nn.Module):
         self.q_rope = RoPE(head_dim, config.rope_theta) if config.rope else None
         self.k_rope = RoPE(head_dim, config.rope_theta) if config.rope else None
         self.to_strategy_combine_mlp = None if block_attn_only else nn.Linear(config.dim, 3 * q_heads, bias=False)
+        # a list to append each call's selected block indices to (int64 [B, N/bs, Hk, K], None
+        # without selection), or None; tests use it to evaluate a checker on the same selection
+        self.record_block_indices = None
 
     def generate_strategy_weights(self, x):
         """Softmax over the 3 branch logits per head, channel index h*3 + s (primitives.py:173-180)."""
@@ -341,12 +348,17 @@ class MosaicAttention(nn.Module):
         # a batch of S tiny products)
         o = torch.empty(S_, B_, self.q_heads * q.shape[-1], dtype=torch.bfloat16, device=x.device)
         o_view = o.view(S_, B_, self.q_heads, -1).transpose(0, 1)
+        record = self.record_block_indices is not None
         if self.q_rope is not None and self._shared_rope_tables():
             # the rotation runs inside the op's pooling pass (one read of q and k)
-            mosaic_attn_func_rope(q, k, v, w, self.q_rope.cos_freqs, self.q_rope.sin_freqs, **args, out=o_view)
+            res = mosaic_attn_func_rope(q, k, v, w, self.q_rope.cos_freqs, self.q_rope.sin_freqs, **args,
+                                        out=o_view, return_block_indices=record)
         else:
             if self.q_rope is not None:
                 q = self.q_rope(q)
                 k = self.k_rope(k)
-            mosaic_attn_func(q=q, k=k, v=v, weight_ba_cmp_slc=w, **args, out=o_view)
+            res = mosaic_attn_func(q=q, k=k, v=v, weight_ba_cmp_slc=w, **args, out=o_view,
+                                   return_block_indices=record)
+        if record:
+            self.record_block_indices.append(res[1])
         return self.to_o(o.to(q.dtype))

@@ -10,7 +10,8 @@ reference's own bf16 rounding points:
   * ``pool_mean``          primitives.py:65-66,76   einops ``reduce(..., 'mean')`` on bf16 -> bf16
   * ``dense_attention``    primitives.py:31,77      flash_attn_func defaults: scale d^-0.5,
                                                     non-causal, GQA head i -> kv head i // G;
-                                                    fp32 softmax, output rounded to bf16
+                                                    fp32 logits and row sums, P rounded to
+                                                    bf16 before P.V, output rounded to bf16
   * ``block_attention``    primitives.py:28-32      attention inside contiguous blocks
   * ``topk_scores``        primitives.py:35-49      repeat_interleave K, bf16 matmul, strided
                                                     '(g h)' mean over query heads (bf16)
@@ -58,9 +59,14 @@ def pool_mean(x: torch.Tensor, block_size: int) -> torch.Tensor:
 
 
 def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float | None = None):
-    """softmax(q k^T * scale) v with GQA, fp32 math, output in q's dtype (flash_attn_func defaults).
+    """softmax(q k^T * scale) v with GQA as flash_attn_func computes it, output in q's dtype.
 
-    q [B, T, Hq, d], k/v [B, S, Hk, d]; query head i uses kv head i // (Hq/Hk).
+    q [B, T, Hq, d], k/v [B, S, Hk, d]; query head i uses kv head i // (Hq/Hk).  flash-attn's
+    published algorithm (primitives.py:31,77 call it with its defaults): fp32 logits, P =
+    exp(s - m) in fp32 with m the row maximum, P rounded to the input dtype for the P.V
+    product (fp32 accumulate), the fp32 row sum of the unrounded P as the divisor.  flash-attn
+    takes m as a running maximum over key tiles; the final row maximum used here gives the
+    same rounding error bound per element.
     """
     B, T, Hq, d = q.shape
     Hk = k.shape[2]
@@ -70,8 +76,8 @@ def dense_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
     kf = k.float().repeat_interleave(G, dim=2).permute(0, 2, 3, 1)   # B Hq d S
     vf = v.float().repeat_interleave(G, dim=2).permute(0, 2, 1, 3)   # B Hq S d
     s = torch.matmul(qf, kf) * scale
-    p = torch.softmax(s, dim=-1)
-    o = torch.matmul(p, vf)                                   # B Hq T d
+    p = torch.exp(s - s.amax(dim=-1, keepdim=True))
+    o = torch.matmul(p.to(q.dtype).float(), vf) / p.sum(dim=-1, keepdim=True)   # B Hq T d
     return o.permute(0, 2, 1, 3).to(q.dtype)
 
 
@@ -218,14 +224,6 @@ def sparse_attn_bwd(q, k, v, o, lse, grad_o, block_indices, block_size: int, sof
     return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
 
 
-def compressed_attention(q, k, v, sparse_block_size: int):
-    """Compressed branch (primitives.py:65-66,76-78): returns (o_cmp per block, q_cmp, k_cmp)."""
-    q_cmp = pool_mean(q, sparse_block_size)
-    k_cmp = pool_mean(k, sparse_block_size)
-    v_cmp = pool_mean(v, sparse_block_size)
-    return dense_attention(q_cmp, k_cmp, v_cmp), q_cmp, k_cmp
-
-
 def mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
                      sparse_block_count, block_attn_only, no_compression=False,
                      block_indices=None, return_parts=False):
@@ -351,7 +349,7 @@ def softmax_scale_default(d: int) -> float:
 
 __all__ = [
     "LOG2E", "pool_mean", "dense_attention", "block_attention", "topk_scores", "attn_topk",
-    "sparse_attn_fwd", "compressed_attention", "mosaic_attn_func", "mosaic_attn_func_blocks",
+    "sparse_attn_fwd", "mosaic_attn_func", "mosaic_attn_func_blocks",
     "selection_band_check",
     "flops", "softmax_scale_default",
 ]

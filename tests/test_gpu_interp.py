@@ -125,7 +125,10 @@ def test_cross_attention_interpolate_module():
     m.initialize_interpolation_scheme(ll, hp)
     m = m.to(DEV).to(torch.bfloat16)
     x = torch.randn(len(ll), 2, 192, device=DEV).to(torch.bfloat16)
-    y = m(x)
+    with pytest.raises(RuntimeError, match="no backward"):   # parameters require grad
+        m(x)
+    with torch.no_grad():
+        y = m(x)
     # the same torch projections around the oracle's gather-attention
     with torch.no_grad():
         kv = m.to_kv(m.kv_norm(x))

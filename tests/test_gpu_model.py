@@ -8,8 +8,9 @@
   elements bit-equal (only the exponential's last fp32 bits may differ).
 * The whole U-Net forward (mosaic.py:304-337) at a small configuration against the CPU
   oracle ``oracle/unet_oracle.py`` (the reference's computation under bf16 autocast, einops
-  for every rearrange).  The selection count equals the number of blocks at every stage, so
-  the selected set is all blocks and no top-k tie can make the two differ.  The residual
+  for every rearrange), once with the selection count equal to the number of blocks at every
+  stage and once with top-k over a fraction of them (the oracle then runs on the device's
+  recorded selections, so blocks swapped inside the tie band cannot make the two differ).  The residual
   output layers are re-initialised at full scale so that every attention and feed-forward
   layer moves the output.  Bars: relative L2 2e-2 and max-abs 6e-2 of the output (whose
   values are O(1)): the forward chains ~60 bf16-rounded ops and a bf16 spacing is 2^-8
@@ -23,6 +24,7 @@ import torch
 
 from mosaic_amd import fused
 from mosaic_amd.model import BottleneckConfig, ModelConfig, StageConfig, Transformer
+from mosaic_amd.primitives import MosaicAttention
 from oracle import unet_oracle
 
 pytestmark = pytest.mark.gpu
@@ -116,26 +118,30 @@ def test_op_writes_sequence_first_rows(mode):
     assert torch.equal(buf.view(N, B, Hq, 64).transpose(0, 1), ref)
 
 
-def tiny_config() -> ModelConfig:
-    """Three resolutions (nside 16 / 8 / 4: 3072 / 768 / 192 pixels), head_dim 64, GQA 4, with
-    the selection count equal to the block count at every stage."""
+def tiny_config(selective: bool = False) -> ModelConfig:
+    """Three resolutions (nside 16 / 8 / 4: 3072 / 768 / 192 pixels), head_dim 64, GQA 4.  By
+    default the selection count equals the block count at every stage (selection keeps every
+    block); ``selective`` keeps 6 of 48, 4 of 12 and 2 of 3 blocks with local blocks of 4, 4 and
+    3 selection blocks, as the shipped model's bs_l = 8 bs and K < N / bs do."""
+    K = (6, 4, 2) if selective else (48, 12, 3)
+    bl_last = 192 if selective else 64
     stages = [
         StageConfig(nside=16, dim=256, num_heads=4, block_attn_size=256, sparse_block_size=64,
-                    sparse_block_count=48, encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
+                    sparse_block_count=K[0], encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
         StageConfig(nside=8, dim=512, num_heads=8, block_attn_size=256, sparse_block_size=64,
-                    sparse_block_count=12, encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
+                    sparse_block_count=K[1], encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
     ]
-    bottleneck = BottleneckConfig(nside=4, dim=512, num_heads=8, block_attn_size=64, sparse_block_size=64,
-                                  sparse_block_count=3, depth=1, mlp_ratio=2.0, gqa_ratio=4)
+    bottleneck = BottleneckConfig(nside=4, dim=512, num_heads=8, block_attn_size=bl_last, sparse_block_size=64,
+                                  sparse_block_count=K[2], depth=1, mlp_ratio=2.0, gqa_ratio=4)
     return ModelConfig(dim=256, num_heads=4, k_neighbors=8, qk_norm=False, rope=True, rope_theta=10000,
                        sparse_every=1, variables=[f"v{i}" for i in range(5)], static_variables=["a", "b", "c"],
                        qkv_compress_ratio=1, cg_stage_cfgs=stages, bottleneck_cfg=bottleneck,
                        num_history_steps=2, noise_dim=32, rmsnorm_elementwise_affine=False)
 
 
-def build_tiny(seed=0):
+def build_tiny(seed=0, selective=False):
     torch.manual_seed(seed)
-    cfg = tiny_config()
+    cfg = tiny_config(selective)
     model = Transformer(cfg, seed=11)
     g = torch.Generator().manual_seed(seed + 1)
     for name, p in model.named_parameters():          # residual outputs at full scale
@@ -148,9 +154,17 @@ def build_tiny(seed=0):
     return cfg, model.to(DEV).eval()
 
 
-def test_unet_forward_matches_oracle():
-    print("unet tiny forward vs oracle", flush=True)
-    cfg, model = build_tiny()
+@pytest.mark.parametrize("selective", [False, True], ids=["all_blocks", "top_k_of_blocks"])
+def test_unet_forward_matches_oracle(selective):
+    """The tiny U-Net against the CPU oracle of the whole forward.  The oracle runs on the
+    device's selections (recorded per attention call), so blocks swapped inside the top-k tie
+    band do not count against the output."""
+    print(f"unet tiny forward vs oracle (selective={selective})", flush=True)
+    cfg, model = build_tiny(selective=selective)
+    recorded = []
+    for m in model.modules():
+        if isinstance(m, MosaicAttention):
+            m.record_block_indices = recorded
     g = torch.Generator().manual_seed(7)
     x = torch.randn(1, 1, 2, 24, 13, 5, generator=g)
     dyt = torch.rand(1, 1, 2, generator=g)
@@ -159,10 +173,12 @@ def test_unet_forward_matches_oracle():
         out = model(x.to(DEV), dyt.to(DEV), S)
         probe = {dt: torch.nn.functional.rms_norm(torch.zeros(1, 8, dtype=dt, device=DEV), (8,)).dtype
                  for dt in (torch.bfloat16, torch.float32)}
+    assert len(recorded) == 5 and all(i is not None for i in recorded)
+    assert [i.shape[-1] for i in recorded] == ([6, 4, 2, 4, 6] if selective else [48, 12, 3, 12, 48])
     gen = torch.Generator(device=DEV)
     gen.manual_seed(11)
     noise = torch.randn((S, cfg.noise_dim), generator=gen, device=DEV, dtype=torch.float32).cpu()
-    ref = unet_oracle.forward(model.state_dict(), cfg, x, dyt, S, noise, probe)
+    ref = unet_oracle.forward(model.state_dict(), cfg, x, dyt, S, noise, probe, block_indices=recorded)
     got = out.float().cpu()
     r = ref.float()
     assert got.shape == r.shape == (1, S, 24, 13, 5), (got.shape, r.shape)
@@ -188,3 +204,70 @@ def test_unet_forward_members_independent():
         first = model(x, dyt, 1).float()
     rel = ((both[:, :1] - first).norm() / first.norm()).item()
     assert rel <= 2e-2, rel
+
+
+def test_era5_step_24_members_properties():
+    """The full U-Net at its shipped settings (era5 preset, inference.py:71-88: local blocks of
+    1024, selection blocks of 128, top-24 / 12 / 4 of 384 / 96 / 24 blocks; 24 members on the
+    240 x 121 grid) has no affordable CPU oracle, so it is checked through properties:
+      * finite output of the right shape, and a repeated step gives the same bits;
+      * members are independent: the residual outputs and noise maps are re-initialised at
+        full scale (the model starts them near zero) so each member's forecast depends on its
+        noise row (members differ by O(1)), and reversing the noise rows reverses the members'
+        outputs to within 2e-2 relative L2 (not bit-exactly: a member's rows then sit elsewhere
+        in the library GEMMs, whose reduction split can depend on the output tile, and the
+        last-bit differences grow through the 14 blocks; a member-mixing mistake gives O(1));
+      * selection is on the model path: every attention call keeps K < N / bs distinct,
+        in-range blocks per row."""
+    from mosaic_amd.model import era5_config
+    print("era5 U-Net step, 24 members", flush=True)
+    cfg = era5_config()
+    torch.manual_seed(0)
+    model = Transformer(cfg)
+    g = torch.Generator().manual_seed(1)
+    for name, p in model.named_parameters():
+        if name.endswith(("to_o.weight", "w2.weight", "noise_bias.weight", "to_noise.weight")) and "interp" not in name:
+            p.data = torch.randn(p.shape, generator=g) / math.sqrt(p.shape[1])
+    lon, lat = torch.linspace(0, 358.5, 240), torch.linspace(-90, 90, 121)
+    model.initialize_interpolation(lon, lat)
+    model.initialize_static_vars(torch.randn(240, 121, 3, generator=g), lon, lat)
+    model = model.to(DEV).eval()
+    x = torch.randn(1, 1, 2, 240, 121, 82, generator=g).to(DEV)
+    dyt = torch.rand(1, 1, 2, generator=g).to(DEV)
+    z = torch.randn(24, cfg.noise_dim, generator=g).to(DEV)
+    ng = model.noise_generator
+    rows = {"z": z}
+    ng.forward = lambda n, device, dtype: ng.to_noise(rows["z"][:n].to(dtype))
+    recorded = []
+    for m in model.modules():
+        if isinstance(m, MosaicAttention):
+            m.record_block_indices = recorded
+    with torch.no_grad(), torch.autocast(DEV, dtype=torch.bfloat16):
+        a = model(x, dyt, 24)
+        calls = list(recorded)
+        for m in model.modules():
+            if isinstance(m, MosaicAttention):
+                m.record_block_indices = None
+        b = model(x, dyt, 24)
+        rows["z"] = z.flip(0)
+        c = model(x, dyt, 24)
+    torch.cuda.synchronize()
+    print("era5 step: forwards done", flush=True)
+    assert a.shape == (1, 24, 240, 121, 82)
+    assert torch.isfinite(a.float()).all()
+    assert torch.equal(a, b), "a repeated step differs"
+    af = a.float()
+    spread = ((af[:, 0] - af[:, 1]).norm() / af[:, 0].norm()).item()
+    assert spread > 5e-2, f"members barely differ ({spread:.2e}): the check below would have no power"
+    flip = ((c.float().flip(1) - af).norm() / af.norm()).item()
+    print(f"era5 step: member spread {spread:.3e}, reversed-noise difference {flip:.3e}", flush=True)
+    assert flip <= 2e-2, flip
+    # 4 + 4 encoder, 2 bottleneck, 2 + 2 decoder blocks (shallower stages first on the way down)
+    expect_K = [24] * 4 + [12] * 4 + [4] * 2 + [12] * 2 + [24] * 2
+    assert [i.shape[-1] for i in calls] == expect_K
+    for idx, K in zip(calls, expect_K):
+        nb = idx.shape[1]
+        assert K < nb
+        i = idx.cpu()
+        assert int(i.min()) >= 0 and int(i.max()) < nb
+        assert (i.sort(-1).values.diff(dim=-1) > 0).all(), "a selection row repeats a block"

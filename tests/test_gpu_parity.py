@@ -10,9 +10,11 @@ import pytest
 import torch
 
 import mosaic_amd as M
-from mosaic_amd.inputs import BOTTLENECK_NSIDE16, STAGE1_NSIDE64, STAGE2_NSIDE32_B24, Workload, make_inputs
+from mosaic_amd.inputs import (BOTTLENECK_NSIDE16, STAGE1_NSIDE64, STAGE2_NSIDE32_B24, Workload, make_inputs,
+                               scaling_workload)
 from mosaic_amd.healpix import apply_rope, get_healpix_grid, rope_tables
 from oracle import bsa_oracle as O
+from structured_inputs import compressed_only_inputs, pooled_logit_std
 
 pytestmark = pytest.mark.gpu
 
@@ -57,6 +59,19 @@ def test_block_attention(N, Hq, Hk, bs_l):
     q, k, v = rand(1, N, Hq, 64, seed=2), rand(1, N, Hk, 64, seed=3), rand(1, N, Hk, 64, seed=4)
     got = M.block_attention(*dev(q, k, v), bs_l)
     close(got, O.block_attention(q, k, v, bs_l))
+
+
+@pytest.mark.parametrize("nside", [32, 64])
+def test_dense_attention_sweep_sizes(nside):
+    """The dense baseline of the scaling sweep (flash_attn_func over the whole sequence) at
+    N = 12288 and 49152, 12/3 heads: a sample of query rows against the oracle."""
+    print(f"dense attention nside {nside}", flush=True)
+    wl = scaling_workload(nside)
+    q, k, v, _ = make_inputs(wl, seed=2)
+    out = M.dense_attention(*dev(q, k, v)).cpu()
+    assert torch.isfinite(out.float()).all()
+    rows = torch.randperm(wl.seq_len, generator=torch.Generator().manual_seed(3))[:192].sort().values
+    close(out[:, rows], O.dense_attention(q[:, rows], k, v))
 
 
 def test_dense_attention():
@@ -177,6 +192,28 @@ def test_mosaic_attn_func_many_selected_blocks():
     close(got_rows, ref_rows)
 
 
+@pytest.mark.parametrize("B,N,Hq,Hk", [(1, 3072, 20, 5), (24, 12288, 16, 4)],
+                         ids=["nb48_two_key_splits", "b24_nb192_one_key_split"])
+def test_compressed_branch_alone(B, N, Hq, Hk):
+    """Gates (0, 1, 0) on block-structured inputs: the output is the compressed branch (pooled
+    attention over all blocks, primitives.py:65-66,76-78) broadcast over each block's tokens.
+    The pooled logits have std > 2, so a branch that ignored its logits, mis-scaled them or
+    read the wrong pooled v block fails the bar (tests/test_oracle.py shows it on the same
+    inputs).  The grids cover the kernel's two key splits (48 blocks) and one split (24
+    members of 192 blocks)."""
+    print(f"compressed branch B={B} N={N} heads {Hq}/{Hk}", flush=True)
+    bs = 64
+    q, k, v, w = compressed_only_inputs(B, N, Hq, Hk, bs, seed=0)
+    qc, kc, vc = (O.pool_mean(t, bs) for t in (q, k, v))
+    assert pooled_logit_std(qc, kc) >= 2.0
+    ref = O.dense_attention(qc, kc, vc)
+    nb = N // bs
+    for K in (4, 0):    # full path, and sparse_block_count == 0: (o_ba*0 + o_cmp*1)/(0+1+1e-8)
+        out = M.mosaic_attn_func(*dev(q, k, v, w), 64, bs, K, False).view(B, nb, bs, Hq, 64)
+        assert torch.equal(out, out[:, :, :1].expand_as(out)), "rows of a block differ"
+        close(out[:, :, 0], ref)
+
+
 def test_mosaic_attn_func_variants():
     wl = BOTTLENECK_NSIDE16
     q, k, v, w = make_inputs(wl, seed=1)
@@ -279,10 +316,13 @@ def test_deterministic():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("wl,nsample", [(STAGE1_NSIDE64, 24), (STAGE2_NSIDE32_B24, 6)], ids=["nside64", "nside32_b24"])
+@pytest.mark.parametrize("wl,nsample", [(STAGE1_NSIDE64, 24), (STAGE2_NSIDE32_B24, 6), (scaling_workload(32), 16),
+                                         (scaling_workload(128), 16)],
+                         ids=["nside64", "nside32_b24", "sweep_nside32", "sweep_nside128"])
 def test_full_size_workloads(wl, nsample):
     """Full-size workloads: indices of every row by the band rule; output rows of a sample of
     query blocks against the oracle; finite everywhere."""
+    print(f"full-size workload {wl.name}", flush=True)
     q, k, v, w = make_inputs(wl, seed=0)
     out, idx = _run_full(q, k, v, w, wl.block_attn_size, wl.sparse_block_size, wl.sparse_block_count)
     assert torch.isfinite(out.float()).all()
@@ -309,7 +349,10 @@ def test_mosaic_attention_module_runs():
     m = m.to(DEV).to(torch.bfloat16)
     x = torch.randn(768, 2, 768, device=DEV, dtype=torch.bfloat16)
     assert m._shared_rope_tables()
-    y = m(x)   # RoPE fused into the op's pooling pass
-    assert y.shape == x.shape and torch.isfinite(y.float()).all()
-    m._shared_rope_tables = lambda: False
-    assert torch.equal(m(x), y)   # RoPE modules, then the op
+    with pytest.raises(RuntimeError, match="no backward"):   # the projections' outputs require grad
+        m(x)
+    with torch.no_grad():
+        y = m(x)   # RoPE fused into the op's pooling pass
+        assert y.shape == x.shape and torch.isfinite(y.float()).all()
+        m._shared_rope_tables = lambda: False
+        assert torch.equal(m(x), y)   # RoPE modules, then the op

@@ -129,5 +129,7 @@ def test_module_scheme_on_cpu():
     nb, rel = _scheme(ll, hp, 8)
     assert torch.equal(m.neighbors, nb) and torch.equal(m.rel_pos, rel)
     assert set(m.state_dict()) >= {"neighbors", "rel_pos"}
-    with pytest.raises(ValueError):   # the gather-attention runs on the device only
+    with torch.no_grad(), pytest.raises(ValueError):   # the gather-attention runs on the device only
+        m(torch.zeros(84, 1, 128))
+    with pytest.raises(RuntimeError, match="no backward"):   # to_q / to_kv weights require grad
         m(torch.zeros(84, 1, 128))

@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from oracle import bsa_oracle as O
+from structured_inputs import compressed_only_inputs, pooled_logit_std
 
 bf16 = torch.bfloat16
 
@@ -248,6 +249,71 @@ def test_merge_closed_forms():
     assert (out.float() - avg).abs().max().item() < 1e-2
     # block_attn_only returns the local branch
     assert torch.equal(O.mosaic_attn_func(q, k, v, None, 64, 64, 2, True), parts["o_ba"])
+
+
+# ----------------------------------------------------------------------------- compressed branch
+def _fails_bar(got, ref, max_abs=2e-2, rel_l2=1e-2):
+    d = got.float() - ref.float()
+    return d.abs().max().item() > max_abs or (d.norm() / ref.float().norm()).item() > rel_l2
+
+
+@pytest.mark.parametrize("B,N,Hq,Hk", [(1, 3072, 20, 5), (2, 12288, 16, 4)])
+def test_compressed_branch_mutants_fail_on_structured_inputs(B, N, Hq, Hk):
+    """On block-structured inputs the compressed branch's logits matter: a branch that ignores
+    them, mis-scales them or reads the wrong pooled v block fails the output bar, so the GPU
+    test of the branch (gates (0, 1, 0)) has power."""
+    q, k, v, w = compressed_only_inputs(B, N, Hq, Hk, 64, seed=0)
+    qc, kc, vc = (O.pool_mean(t, 64) for t in (q, k, v))
+    assert pooled_logit_std(qc, kc) >= 2.0
+    ref = O.dense_attention(qc, kc, vc)
+    # float64 softmax attention on the pooled tensors (flash-attn without any rounding)
+    G = Hq // Hk
+    s = torch.einsum("bthd,buhd->bhtu", qc.double(), kc.double().repeat_interleave(G, 2)) / 8.0
+    exact = torch.einsum("bhtu,buhd->bthd", torch.softmax(s, -1), vc.double().repeat_interleave(G, 2))
+    assert not _fails_bar(ref, exact, max_abs=1e-2, rel_l2=4e-3)
+    uniform = vc.float().mean(1, keepdim=True).repeat_interleave(G, 2).expand_as(ref).to(bf16)
+    assert _fails_bar(uniform, ref)
+    assert _fails_bar(O.dense_attention(qc, kc, vc, scale=4 * 64 ** -0.5), ref)
+    assert _fails_bar(O.dense_attention(qc, kc, vc, scale=0.25 * 64 ** -0.5), ref)
+    assert _fails_bar(O.dense_attention(qc, kc, vc.roll(1, dims=1)), ref)     # v_cmp off by one block
+    assert _fails_bar(O.dense_attention(qc, kc.roll(1, dims=2), vc.roll(1, dims=2)), ref)  # wrong kv head
+    # gates (0, 1, 0): the full op is the compressed branch broadcast over each block's tokens
+    if B == 1:
+        out = O.mosaic_attn_func(q, k, v, w, 64, 64, 4, False)
+        assert torch.equal(out, ref.repeat_interleave(64, dim=1))
+
+
+# ----------------------------------------------------------------------------- sampled full path
+@pytest.mark.parametrize("B,N,Hq,Hk,bl,bs,K", [
+    (1, 1024, 4, 2, 64, 64, 3),       # bs_l == bs
+    (2, 1024, 6, 3, 256, 64, 4),      # bs_l > bs, B > 1
+    (1, 1024, 4, 1, 64, 128, 2),      # bs_l < bs
+    (2, 2048, 8, 2, 1024, 128, 5),    # the model's ratio bs_l = 8 bs, B > 1
+])
+def test_blocks_oracle_equals_full_oracle(B, N, Hq, Hk, bl, bs, K):
+    """mosaic_attn_func_blocks (the checker of the full-size GPU tests, which cannot afford the
+    whole oracle) reproduces the rows of mosaic_attn_func for the requested query blocks, for
+    every relation of the local and sparse block sizes."""
+    g = torch.Generator().manual_seed(B * 1000 + bl + bs)
+    q = torch.randn(B, N, Hq, 64, generator=g).to(bf16)
+    k = torch.randn(B, N, Hk, 64, generator=g).to(bf16)
+    v = torch.randn(B, N, Hk, 64, generator=g).to(bf16)
+    w = torch.sigmoid(torch.randn(3, B, N, Hq, generator=g)).to(bf16).unsqueeze(-1)
+    full, parts = O.mosaic_attn_func(q, k, v, w, bl, bs, K, False, return_parts=True)
+    nb = N // bs
+    blocks = torch.tensor([0, 3, nb // 2 + 1, nb - 1])
+    rows, bparts = O.mosaic_attn_func_blocks(q, k, v, w, bl, bs, K, blocks)
+    assert torch.equal(bparts["block_indices"], parts["block_indices"])
+    want = torch.cat([full[:, i * bs:(i + 1) * bs] for i in blocks.tolist()], dim=1)
+    d = (rows.float() - want.float()).abs()
+    # identical arithmetic up to fp32 summation order: at most one bf16 spacing apart, rarely
+    assert d.max().item() <= 2 ** -6 and (d > 0).float().mean().item() < 1e-3
+    # with the device's indices passed in (here: a permutation of the oracle's), rows follow them
+    perm = parts["block_indices"].flip(-1)
+    rows2, _ = O.mosaic_attn_func_blocks(q, k, v, w, bl, bs, K, blocks, block_indices=perm)
+    full2 = O.mosaic_attn_func(q, k, v, w, bl, bs, K, False, block_indices=perm)
+    want2 = torch.cat([full2[:, i * bs:(i + 1) * bs] for i in blocks.tolist()], dim=1)
+    assert (rows2.float() - want2.float()).abs().max().item() <= 2 ** -6
 
 
 # ----------------------------------------------------------------------------- band rule
