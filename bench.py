@@ -7,8 +7,11 @@ Workload (default): Nside 64 stage-1 attention forward -- N = 49152 tokens, batc
 
 A step is one full forward (pooling, compressed attention + selection scores, top-k, fused
 local/selected attention with the merge) through the C ABI on inputs already resident in HBM.
-W warm-up steps, then K timed steps bracketed by device synchronisation; per-kernel durations
-come from HIP events recorded between the kernels of every timed step, on the launch stream.
+W warm-up steps, then untimed calls for --settle-s seconds (the clock settles at its
+power-limited level), then exactly K timed steps bracketed by device synchronisation with a HIP
+event before each step on the launch stream: ``value`` is the median per-call time,
+``ms_per_step_mean`` the mean.  Per-kernel durations come from a second pass of K steps with
+HIP events recorded between the kernels of every step, on the launch stream.
 
 Prints one JSON line.  Options: --gpus (only 1 is supported: the op runs on one GPU),
 --steps, --warmup, --workload {nside64, nside64_model, nside32_b24, nside16, nside32_sweep,
@@ -17,7 +20,8 @@ attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v), --
 times the op with the input side's RoPE fused into its pooling pass, mosaic_bsa_fwd_rope,
 against eager torch RoPE followed by the op, both on unrotated q/k), --interp (also times the
 k-nearest-neighbour cross-attention between the model's lat-lon and HEALPix grids,
-mosaic_knn_interp_fwd, at --interp-batch members).  Unless --no-unet, the line also carries
+mosaic_knn_interp_fwd, at --interp-batch members), --branches (also times the local and the
+selected branch as standalone kernels).  Unless --no-unet, the line also carries
 one forecast step of the full U-Net at --unet-members ensemble members (default 24:
 ``unet_24_member_step_ms``, the metric's second half); --unet-only times only that step.
 """
@@ -315,6 +319,51 @@ def unet_leg(args, dev):
             "data": "synthetic N(0,1) input and static fields, random-init weights (no checkpoint offline)"}
 
 
+def branches_leg(L, a, q, k, v, wl, args, stream):
+    """The local and selected branches as standalone kernels on the workload's q/k/v, for
+    per-branch MFMA figures: block_attention (primitives.py:28-32) through mosaic_block_attn_fwd,
+    and the selected branch (ops.py:20-134) through mosaic_sparse_attn_fwd on the indices the op
+    itself selects.  FLOPs: 4*B*Hq*64*N*bs_l (local), 4*B*Hq*64*N*K*bs (selected)."""
+    B, N, Hq, d = q.shape
+    Hk = k.shape[2]
+    bs, bl, K = wl.sparse_block_size, wl.block_attn_size, wl.sparse_block_count
+    sp = stream.cuda_stream
+    out = torch.empty_like(q)
+    idx = torch.empty(B, N // bs, Hk, K, dtype=torch.int64, device=q.device)
+    lse = torch.empty(B, N, Hq, dtype=torch.float32, device=q.device)
+    ia = _lib.BsaArgs.from_buffer_copy(a)
+    ia.out, ia.block_indices_out = out.data_ptr(), idx.data_ptr()
+    ws = torch.empty(L.mosaic_bsa_workspace_size(ctypes.byref(ia)) + 256, dtype=torch.uint8, device=q.device)
+    ws_ptr = (ws.data_ptr() + 255) // 256 * 256
+    _lib.check(L.mosaic_bsa_fwd(ctypes.byref(ia), ws_ptr, ws.numel() - 256, sp), "mosaic_bsa_fwd")
+
+    def local():
+        _lib.check(L.mosaic_block_attn_fwd(bnhd(q), bnhd(k), bnhd(v), B, N, Hq, Hk, d, bl, 0.0, out.data_ptr(), sp),
+                   "mosaic_block_attn_fwd")
+
+    def selected():
+        _lib.check(L.mosaic_sparse_attn_fwd(bnhd(q), bnhd(k), bnhd(v), idx.data_ptr(), B, N, Hq, Hk, d, bs, K, 0.0,
+                                            out.data_ptr(), lse.data_ptr(), sp), "mosaic_sparse_attn_fwd")
+
+    res = {}
+    for name, fn, flops in (("local", local, 4 * B * Hq * d * N * bl), ("selected", selected, 4 * B * Hq * d * N * K * bs)):
+        for _ in range(5):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / args.steps
+        tf = flops / (ms * 1e-3) / 1e12
+        res[name] = {"ms": round(ms, 4), "flops": flops, "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+    res["selected"]["kernel"] = "bsa_attn_kernel selected-only (running-reference path, writes the LSE)"
+    res["local"]["kernel"] = "bsa_attn_kernel local-only"
+    return res
+
+
 def cpu_baseline(wl, q, k, v, w):
     """The CPU oracle (torch restatement of the reference path) on the full workload."""
     from oracle import bsa_oracle as O
@@ -351,6 +400,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-s", type=float, default=2.0,
+                    help="untimed calls for this many seconds after the warm-up (reported as 'settle')")
+    ap.add_argument("--branches", action="store_true",
+                    help="also time the local branch alone (mosaic_block_attn_fwd) and the selected branch "
+                         "alone (mosaic_sparse_attn_fwd on the op's own indices)")
     ap.add_argument("--workload", default="nside64", choices=sorted(WORKLOADS))
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -413,18 +467,31 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # settle: untimed calls for --settle-s seconds, so the timed calls run at the sustained
+    # (power-limited) clock rather than during its ramp
+    t0 = time.perf_counter()
+    n_settle = 0
+    while time.perf_counter() - t0 < args.settle_s:
+        for _ in range(50):
+            step()
+        n_settle += 50
+        torch.cuda.synchronize()
+    settle = {"seconds": round(time.perf_counter() - t0, 2), "calls": n_settle}
 
-    # timed region 1: plain entry point, whole-step time
-    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # timed region 1: exactly K calls of the plain entry point, a HIP event before each and
+    # one after the last, on the launch stream; per-call durations and their median
+    evs1 = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
-    t_start.record(stream)
     wall0 = time.perf_counter()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        evs1[i].record(stream)
         step()
-    t_end.record(stream)
+    evs1[-1].record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - wall0) * 1e3 / args.steps
-    ms = t_start.elapsed_time(t_end) / args.steps
+    per_call = [evs1[i].elapsed_time(evs1[i + 1]) for i in range(args.steps)]
+    ms_mean = evs1[0].elapsed_time(evs1[-1]) / args.steps
+    ms = statistics.median(per_call)
 
     # timed region 2: same steps through the profiled entry point (events between kernels)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
@@ -444,6 +511,7 @@ def main():
 
     fl = flop_counts(wl)
     by = byte_counts(wl)
+    traffic = profiled_traffic(wl.name)
     attn_ms = per_kernel["attn"]
     attn_tflops = fl["attn"] / (attn_ms * 1e-3) / 1e12
     tflops = fl["total"] / (ms * 1e-3) / 1e12
@@ -455,6 +523,9 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "ms_per_step_mean": round(ms_mean, 4),
+        "ms_per_call_min_max": [round(min(per_call), 4), round(max(per_call), 4)],
+        "settle": settle,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -471,8 +542,13 @@ def main():
         "secondary": {
             "pool_hbm_gbs": round(by["pool"] / (per_kernel["pool"] * 1e-3) / 1e9, 1),
             "pool_hbm_frac": round(by["pool"] / (per_kernel["pool"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-            "selected_gather_gbs": round(by["selected_gather"] / (attn_ms * 1e-3) / 1e9, 1),
+            # K/V tile bytes the selected branch requests (604 MB at Nside 64), per second of the
+            # attention kernel: served mostly from L2 / MALL, not an HBM rate
+            "selected_tile_request_gbs": round(by["selected_gather"] / (attn_ms * 1e-3) / 1e9, 1),
             "cmp_scores_tflops": round(fl["cmp_scores"] / (per_kernel["cmp_scores"] * 1e-3) / 1e12, 2),
+            # counter-measured bytes the attention kernel moves past L2 (FETCH_SIZE + WRITE_SIZE of
+            # the committed counter summary) per second of its live duration
+            "attn_fabric_gbs": round(traffic / (attn_ms * 1e-3) / 1e9, 1) if traffic else None,
         },
         "roofline": {
             "kernel": "bsa_attn_kernel (fused local + selected + merge)",
@@ -481,7 +557,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": profiled_traffic(wl.name),
+            "traffic": traffic,
             "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)",
             "flops_per_launch": fl["attn"],
         },
@@ -502,6 +578,8 @@ def main():
         result["knn_interp"] = interp_leg(L, args, dev, stream)
     if args.bwd:
         result["selected_bwd"] = bwd_leg(L, q, k, v, wl, args, dev, stream)
+    if args.branches:
+        result["branches"] = branches_leg(L, a, q, k, v, wl, args, stream)
     if not args.no_unet:
         leg = unet_leg(args, dev)
         result["unet_24_member_step_ms"] = leg["ms_per_step"] if leg["members"] == 24 else None
