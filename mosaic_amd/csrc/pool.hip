@@ -20,12 +20,17 @@
 namespace mosaic {
 namespace {
 
+// ROPE: 0 no rotation; 1 rotation with the block's table rows staged in LDS; 2 rotation with
+// the table rows read from global memory (blocks too large for the LDS staging).  Separate
+// instantiations keep the LDS reads ds_read instructions (a runtime choice between the two
+// address spaces compiled to generic loads).
+template <int ROPE>
 __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
     const int t = blockIdx.x, b = blockIdx.y;
     // RoPE tables of the block's tokens, read once per workgroup: [token][8 float4] of cos,
     // then of sin (every head of a token uses the same row)
     extern __shared__ float4 rope_rows[];
-    if (p.rope_cos != nullptr && p.rope_lds && t < p.nb) {
+    if (ROPE == 1 && t < p.nb) {
         const float4* c4 = reinterpret_cast<const float4*>(p.rope_cos) + (int64_t)t * p.bs * 8;
         const float4* s4 = reinterpret_cast<const float4*>(p.rope_sin) + (int64_t)t * p.bs * 8;
         for (int i = threadIdx.x; i < 16 * p.bs; i += blockDim.x)
@@ -67,16 +72,20 @@ __global__ __launch_bounds__(256) void pool_kernel(PoolParams p) {
         const int64_t sn = p.sn[which];
         const bf16_t* src = p.x[which] + b * p.sb[which] + (int64_t)t * p.bs * sn + (int64_t)hd * p.sh[which] + ch * 8;
         // RoPE of this thread's 4 pairs (frequencies 4 ch .. 4 ch + 3) of token n of the block
-        const bool rope = p.rope_cos != nullptr && which < 2;
+        const bool rope = ROPE != 0 && which < 2;
         const int64_t tok0 = (int64_t)t * p.bs;
         bf16_t* rdst = rope && p.rot[which] != nullptr
                            ? p.rot[which] + (((int64_t)b * p.nb * p.bs + tok0) * p.heads[which] + hd) * kHeadDim + ch * 8
                            : nullptr;
         auto rotate = [&](uint4 v, int n) __attribute__((always_inline)) -> uint4 {
-            const float4 c = p.rope_lds ? rope_rows[n * 8 + ch]
-                                        : *reinterpret_cast<const float4*>(p.rope_cos + (tok0 + n) * 32 + 4 * ch);
-            const float4 s = p.rope_lds ? rope_rows[8 * p.bs + n * 8 + ch]
-                                        : *reinterpret_cast<const float4*>(p.rope_sin + (tok0 + n) * 32 + 4 * ch);
+            float4 c, s;
+            if constexpr (ROPE == 1) {
+                c = rope_rows[n * 8 + ch];
+                s = rope_rows[8 * p.bs + n * 8 + ch];
+            } else {
+                c = *reinterpret_cast<const float4*>(p.rope_cos + (tok0 + n) * 32 + 4 * ch);
+                s = *reinterpret_cast<const float4*>(p.rope_sin + (tok0 + n) * 32 + 4 * ch);
+            }
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
             const float cf[4] = {c.x, c.y, c.z, c.w}, sf[4] = {s.x, s.y, s.z, s.w};
             uint32_t o[4];
@@ -139,7 +148,9 @@ hipError_t launch_pool(const PoolParams& p, hipStream_t s) {
     void* args[] = {&q};
     const int tgrid = (p.kfrag || p.vfrag) ? p.nb_pad : p.nb;
     const size_t lds = q.rope_lds ? (size_t)p.bs * 256 : 0;
-    return hipLaunchKernel((const void*)pool_kernel, dim3(tgrid, p.B), dim3(256), args, lds, s);
+    const void* fn = p.rope_cos == nullptr ? (const void*)pool_kernel<0>
+                   : q.rope_lds ? (const void*)pool_kernel<1> : (const void*)pool_kernel<2>;
+    return hipLaunchKernel(fn, dim3(tgrid, p.B), dim3(256), args, lds, s);
 }
 
 }  // namespace mosaic

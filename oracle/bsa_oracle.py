@@ -24,6 +24,8 @@ reference's own bf16 rounding points:
   * ``sparse_attn_bwd``    ops.py:179-507           selected-branch backward: grad q over the
                                                     selected blocks, grad k / v over the
                                                     queries whose block selected the key
+  * ``sparse_attn_bwd_blocks`` (same lines)         the same for a sample of query and key
+                                                    blocks, gathering only selected blocks
 
 Parity pinning (each function is checked against something other than its own formula by
 tests/test_oracle.py): einops itself for the strided mean, brute-force masked dense
@@ -224,6 +226,69 @@ def sparse_attn_bwd(q, k, v, o, lse, grad_o, block_indices, block_size: int, sof
     return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
 
 
+def sparse_attn_bwd_blocks(q, k, v, o, lse, grad_o, block_indices, block_size: int, q_blocks, k_blocks,
+                           softmax_scale: float | None = None):
+    """Selected-branch backward (ops.py:179-507) for a sample of blocks, gathering only the
+    selected key blocks, so full-size problems fit: returns (dq rows of the query blocks
+    ``q_blocks`` [B, len(q_blocks) * bs, Hq, d], dk and dv rows of the key blocks ``k_blocks``
+    [B, len(k_blocks) * bs, Hk, d]), with the arithmetic and rounding points of
+    ``sparse_attn_bwd``.  grad q walks the selection entries of each query block in order
+    (ops.py:244, duplicates counted); grad k / v walks, per kv head, the query blocks whose
+    selection row holds the key block (the boolean block mask, ops.py:276-297, 367-370) in
+    ascending order.
+    """
+    B, N, Hq, d = q.shape
+    Hk = k.shape[2]
+    G = Hq // Hk
+    bs = block_size
+    nb = N // bs
+    scale = d ** -0.5 if softmax_scale is None else softmax_scale
+    bf = torch.bfloat16
+    idx = block_indices.long()
+    qb, kb = [int(x) for x in q_blocks], [int(x) for x in k_blocks]
+
+    def rows(x, i):
+        return x[:, i * bs:(i + 1) * bs].float()
+
+    def qs_rows(i):   # ops.py:237: q' = bf16((q * scale) * log2 e)
+        return ((rows(q, i) * scale) * LOG2E).to(bf).float()
+
+    def delta_rows(i):   # ops.py:458: bf16(sum(bf16(o * do)))
+        return (o[:, i * bs:(i + 1) * bs].to(bf) * grad_o[:, i * bs:(i + 1) * bs].to(bf)).sum(-1).to(bf).float()
+
+    dq = torch.zeros(B, len(qb) * bs, Hq, d)
+    for n, i in enumerate(qb):
+        qs, g, dl, ls = qs_rows(i), rows(grad_o.to(bf), i), delta_rows(i), rows(lse, i)
+        for b in range(B):
+            for j in range(Hq):
+                c = j // G
+                acc = torch.zeros(bs, d)
+                for u in idx[b, i, c].tolist():
+                    if not 0 <= u < nb:
+                        continue
+                    kt, vt = k[b, u * bs:(u + 1) * bs, c].float(), v[b, u * bs:(u + 1) * bs, c].float()
+                    p = torch.exp2(qs[b, :, j] @ kt.t() - ls[b, :, j, None])
+                    dp = g[b, :, j] @ vt.t()
+                    ds = (p * LN2 * (dp - dl[b, :, j, None])).to(bf).float()     # ops.py:266-269
+                    acc += ds @ kt
+                dq[b, n * bs:(n + 1) * bs, j] = (acc * scale) * LOG2E           # ops.py:270-272
+    dk = torch.zeros(B, len(kb) * bs, Hk, d)
+    dv = torch.zeros(B, len(kb) * bs, Hk, d)
+    for n, u in enumerate(kb):
+        for b in range(B):
+            for c in range(Hk):
+                kt, vt = k[b, u * bs:(u + 1) * bs, c].float(), v[b, u * bs:(u + 1) * bs, c].float()
+                for t in (idx[b, :, c] == u).any(-1).nonzero().flatten().tolist():   # ascending
+                    qs, g, dl, ls = qs_rows(t)[b], rows(grad_o.to(bf), t)[b], delta_rows(t)[b], rows(lse, t)[b]
+                    for j in range(c * G, (c + 1) * G):
+                        p = torch.exp2(qs[:, j] @ kt.t() - ls[:, j, None])
+                        dp = g[:, j] @ vt.t()
+                        dv[b, n * bs:(n + 1) * bs, c] += p.to(bf).float().t() @ g[:, j]          # ops.py:427
+                        ds = (p * (dp - dl[:, j, None]) * LN2).to(bf).float()                    # ops.py:429
+                        dk[b, n * bs:(n + 1) * bs, c] += ds.t() @ qs[:, j]                       # ops.py:430
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
+
+
 def mosaic_attn_func(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size,
                      sparse_block_count, block_attn_only, no_compression=False,
                      block_indices=None, return_parts=False):
@@ -349,7 +414,7 @@ def softmax_scale_default(d: int) -> float:
 
 __all__ = [
     "LOG2E", "pool_mean", "dense_attention", "block_attention", "topk_scores", "attn_topk",
-    "sparse_attn_fwd", "mosaic_attn_func", "mosaic_attn_func_blocks",
+    "sparse_attn_fwd", "sparse_attn_bwd", "sparse_attn_bwd_blocks", "mosaic_attn_func", "mosaic_attn_func_blocks",
     "selection_band_check",
     "flops", "softmax_scale_default",
 ]

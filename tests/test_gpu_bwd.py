@@ -18,14 +18,17 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def case(seed, B, N, Hq, Hk, bs, K):
+def case(seed, B, N, Hq, Hk, bs, K, argsort=False):
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(B, N, Hq, 64, generator=g).to(torch.bfloat16)
     k = torch.randn(B, N, Hk, 64, generator=g).to(torch.bfloat16)
     v = torch.randn(B, N, Hk, 64, generator=g).to(torch.bfloat16)
     do = torch.randn(B, N, Hq, 64, generator=g).to(torch.bfloat16)
     nb = N // bs
-    idx = torch.stack([torch.randperm(nb, generator=g)[:K] for _ in range(B * nb * Hk)]).view(B, nb, Hk, K)
+    if argsort:   # K distinct random blocks per row, drawn for all rows at once
+        idx = torch.rand(B, nb, Hk, nb, generator=g).argsort(-1)[..., :K].contiguous()
+    else:
+        idx = torch.stack([torch.randperm(nb, generator=g)[:K] for _ in range(B * nb * Hk)]).view(B, nb, Hk, K)
     return q, k, v, do, idx
 
 
@@ -54,6 +57,34 @@ def test_sparse_attn_bwd_matches_oracle(B, N, Hq, Hk, bs, K):
     rq, rk, rv = O.sparse_attn_bwd(q, k, v, o.cpu(), lse.cpu(), do, idx, bs, 0.125)
     for name, gg, rr in (("dq", gq, rq), ("dk", gk, rk), ("dv", gv, rv)):
         check(gg, rr, name)
+
+
+@pytest.mark.parametrize("B,nside,Hq,Hk,K,nsample", [(1, 64, 12, 3, 16, 8), (4, 32, 16, 4, 16, 4)],
+                         ids=["nside64", "nside32_b4"])
+def test_sparse_attn_bwd_full_size_sampled(B, nside, Hq, Hk, K, nsample):
+    """The benchmarked size (N = 49152 with 768 blocks) and 4 members of N = 12288: the sampled
+    block oracle (pinned on the CPU against the dense-mask oracle) checks grad q on a sample of
+    query blocks and grad k / v on a sample of key blocks, including the most-selected key
+    block (the longest walk of the grad k / v kernel)."""
+    N, bs = 12 * nside * nside, 64
+    nb = N // bs
+    print(f"bwd full size B={B} N={N} Hq={Hq} Hk={Hk} K={K}", flush=True)
+    q, k, v, do, idx = case(nside + B, B, N, Hq, Hk, bs, K, argsort=True)
+    qd, kd, vd, dod, idxd = (t.to(DEV) for t in (q, k, v, do, idx))
+    o, lse = mosaic_attn_fwd(qd, kd, vd, idxd, bs, 0.125)
+    gq, gk, gv = mosaic_attn_bwd(qd, kd, vd, o, lse, dod, 0.125, idxd, bs)
+    gq, gk, gv, o, lse = (t.cpu() for t in (gq, gk, gv, o, lse))
+    g = torch.Generator().manual_seed(5)
+    qb = torch.randperm(nb, generator=g)[:nsample].sort().values.tolist()
+    counts = torch.bincount(idx[0].flatten(), minlength=nb)
+    kb = sorted(set(torch.randperm(nb, generator=g)[:nsample - 1].tolist() + [int(counts.argmax())]))
+    rows = lambda x, blocks: torch.cat([x[:, i * bs:(i + 1) * bs] for i in blocks], dim=1)
+    for b in sorted({0, B - 1}):   # members are independent: the first and the last one
+        m = slice(b, b + 1)
+        rq, rk, rv = O.sparse_attn_bwd_blocks(q[m], k[m], v[m], o[m], lse[m], do[m], idx[m], bs, qb, kb, 0.125)
+        check(rows(gq[m], qb), rq, f"dq member {b}")
+        check(rows(gk[m], kb), rk, f"dk member {b}")
+        check(rows(gv[m], kb), rv, f"dv member {b}")
 
 
 def test_sparse_attn_bwd_skips_invalid_and_unselected():

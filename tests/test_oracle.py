@@ -391,3 +391,25 @@ def test_sparse_attn_bwd_unselected_keys_zero_and_full_selection():
     ref = _exact_grads(q, k, v, do, idx, 64)
     for gg, rr in zip(got, ref):
         assert ((gg.double() - rr).norm() / rr.norm()).item() < 1.5e-2
+
+
+@pytest.mark.parametrize("seed,B,Hq,Hk,bs,K", [(3, 1, 4, 2, 64, 3), (4, 2, 4, 1, 128, 2), (5, 1, 6, 3, 64, 5)])
+def test_sparse_attn_bwd_blocks_equals_dense_oracle(seed, B, Hq, Hk, bs, K):
+    """The sampled backward (the checker of the full-size GPU test) reproduces the dense-mask
+    oracle's gradients on the sampled blocks, with duplicated and out-of-range entries in the
+    selection rows (counted twice in grad q, once in grad k / v; skipped)."""
+    q, k, v, do, idx = _bwd_case(seed, B=B, N=512, Hq=Hq, Hk=Hk, bs=bs, K=K)
+    nb = 512 // bs
+    o, lse = O.sparse_attn_fwd(q, k, v, idx, bs)   # any consistent o / lse serve both backwards
+    idx = idx.clone()
+    idx[0, 0, 0, 1] = idx[0, 0, 0, 0]          # a duplicate
+    idx[0, nb - 1, Hk - 1, 0] = nb + 3          # out of range: skipped
+    ref = O.sparse_attn_bwd(q, k, v, o, lse, do, idx, bs)
+    qb, kb = [0, nb - 1], [0, idx[0, 0, 0, 0].item(), nb - 1]
+    got = O.sparse_attn_bwd_blocks(q, k, v, o, lse, do, idx, bs, qb, kb)
+    for g, r, blocks in zip(got, ref, (qb, kb, kb)):
+        want = torch.cat([r[:, i * bs:(i + 1) * bs] for i in blocks], dim=1).float()
+        d = (g.float() - want).abs()
+        # the same products summed in another order: at most one bf16 spacing, rarely
+        assert (d <= 2 ** -7 * want.abs() + 1e-6).all(), d.max().item()
+        assert (d > 0).float().mean().item() < 1e-2
