@@ -112,6 +112,75 @@ __device__ __forceinline__ uint32_t wave_max_all_u32(uint32_t x) {
     return max((uint32_t)b[0], (uint32_t)b[1]);
 }
 
+// ---------------------------------------------------------------------------------------
+// Top-k of one row of bf16 selection scores held by a wave: torch.topk(k, largest=True,
+// sorted=True) of attn_topk (primitives.py:50).  Lane l holds raw[i] = the bf16 bits of the
+// score of block u = l + 64 i (blocks u >= nb are ignored).  Each score becomes a 32-bit key
+// (order-preserving image of the bf16 bits << 16 | (0xffff - u)), so one unsigned max picks the
+// largest score and, among equal scores, the lowest block index.  K rounds of a wave
+// max-reduction emit the indices in descending score order (the order of exactly tied scores is
+// unspecified in torch).  The wave max runs on DPP within each 16-lane row, then across rows
+// with the two lane-swap permutes, leaving the maximum in every lane: no LDS or scalar round
+// trips inside a selection round.  Indices go to idx32 / idx64 (either may be null) at
+// out0 .. out0 + K - 1.
+
+__device__ __forceinline__ uint32_t order16(uint32_t bits) {
+    return (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u);
+}
+
+// Insert x into the descending list (b0 >= b1 >= b2 >= b3); the smallest falls off.
+__device__ __forceinline__ void insert4(uint32_t& b0, uint32_t& b1, uint32_t& b2, uint32_t& b3, uint32_t x) {
+    uint32_t t = max(b0, x); x = min(b0, x); b0 = t;
+    t = max(b1, x); x = min(b1, x); b1 = t;
+    t = max(b2, x); x = min(b2, x); b2 = t;
+    b3 = max(b3, x);
+}
+
+template <int PL>
+__device__ __forceinline__ void select_topk(const uint32_t (&raw)[PL], int nb, int K, int lane, int64_t out0,
+                                            int32_t* idx32, int64_t* idx64) {
+    uint32_t key[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+        const int u = lane + 64 * i;
+        key[i] = (u < nb) ? ((order16(raw[i]) << 16) | (0xffffu - (uint32_t)u)) : 0u;
+    }
+    // Each lane keeps its four largest remaining keys.  Keys leave the wave in descending
+    // order, so a lane's emitted keys are always its largest ones: after emitting key x the
+    // lane's remaining keys are exactly those below x, and the buffer is refilled from them
+    // only when all four buffered keys have been emitted.
+    uint32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) insert4(b0, b1, b2, b3, key[i]);
+
+    int mine = 0;  // lane (kk mod 64) keeps the kk-th index for one coalesced store
+    for (int kk = 0; kk < K; ++kk) {
+        const uint32_t mx = wave_max_all_u32(b0);
+        const int u = (int)(0xffffu - (mx & 0xffffu));
+        const bool win = b0 == mx;
+        if (win) {
+            b0 = b1;
+            b1 = b2;
+            b2 = b3;
+            b3 = 0;
+        }
+        if (PL > 4 && __builtin_amdgcn_ballot_w64(win && b0 == 0)) {
+            if (win && b0 == 0) {
+#pragma unroll
+                for (int i = 0; i < PL; ++i) insert4(b0, b1, b2, b3, key[i] < mx ? key[i] : 0u);
+            }
+        }
+        if ((kk & 63) == lane) mine = u;
+        if ((kk & 63) == 63 || kk == K - 1) {
+            const int base = kk & ~63;
+            if (lane <= kk - base) {
+                if (idx32) idx32[out0 + base + lane] = mine;
+                if (idx64) idx64[out0 + base + lane] = mine;
+            }
+        }
+    }
+}
+
 // 2-D RoPE of one bf16 pair (x0, x1) packed in a word, by angle (c = cos, s = sin):
 // (x0 c - x1 s, x1 c + x0 s) in fp32 with both products and the sum rounded separately (no
 // fused multiply-add), as the reference's elementwise tensor ops round them

@@ -1,31 +1,12 @@
 // topk.hip -- per-row top-k block selection over the bf16 selection scores (gfx950).
 //
 // Replaces scores.topk(k=block_count, dim=-1, largest=True) of attn_topk
-// (primitives.py:50).  One wave per row (b, h, t).  Each score becomes a 32-bit key
-// (order-preserving image of the bf16 bits << 16 | (0xffff - u)), so one unsigned max picks
-// the largest score and, among equal scores, the lowest block index.  K rounds of a wave
-// max-reduction emit the indices in descending score order (torch's sorted=True order; the
-// order of exactly tied scores is unspecified there).
-//
-// The wave max runs on DPP within each 16-lane row (quad swaps, half-row and row mirrors),
-// then across rows with the two lane-swap permutes, leaving the maximum in every lane: no
-// LDS or scalar round trips inside a selection round.
+// (primitives.py:50).  One wave per row (b, h, t); the selection itself is select_topk
+// (bsa_common.h).
 #include "bsa_common.h"
 
 namespace mosaic {
 namespace {
-
-__device__ __forceinline__ uint32_t order16(uint32_t bits) {
-    return (bits & 0x8000u) ? (~bits & 0xffffu) : (bits | 0x8000u);
-}
-
-// Insert x into the descending list (b0 >= b1 >= b2 >= b3); the smallest falls off.
-__device__ __forceinline__ void insert4(uint32_t& b0, uint32_t& b1, uint32_t& b2, uint32_t& b3, uint32_t x) {
-    uint32_t t = max(b0, x); x = min(b0, x); b0 = t;
-    t = max(b1, x); x = min(b1, x); b1 = t;
-    t = max(b2, x); x = min(b2, x); b2 = t;
-    b3 = max(b3, x);
-}
 
 template <int PL>  // keys per lane: nb <= 64 * PL
 __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
@@ -50,48 +31,7 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
         for (; g < p.G; ++g) combine_ocmp<1>(p.cmb, b, p.nb, t, g * p.Hk + h, p.Hk, lane);
     }
 
-    uint32_t key[PL];
-#pragma unroll
-    for (int i = 0; i < PL; ++i) {
-        const int u = lane + 64 * i;
-        key[i] = (u < p.nb) ? ((order16(raw[i]) << 16) | (0xffffu - (uint32_t)u)) : 0u;
-    }
-    // Each lane keeps its four largest remaining keys.  Keys leave the wave in descending
-    // order, so a lane's emitted keys are always its largest ones: after emitting key x the
-    // lane's remaining keys are exactly those below x, and the buffer is refilled from them
-    // only when all four buffered keys have been emitted.
-    uint32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-#pragma unroll
-    for (int i = 0; i < PL; ++i) insert4(b0, b1, b2, b3, key[i]);
-
-    const int64_t out0 = (((int64_t)b * p.nb + t) * p.Hk + h) * p.K;
-
-    int mine = 0;  // lane (kk mod 64) keeps the kk-th index for one coalesced store
-    for (int kk = 0; kk < p.K; ++kk) {
-        const uint32_t mx = wave_max_all_u32(b0);
-        const int u = (int)(0xffffu - (mx & 0xffffu));
-        const bool win = b0 == mx;
-        if (win) {
-            b0 = b1;
-            b1 = b2;
-            b2 = b3;
-            b3 = 0;
-        }
-        if (PL > 4 && __builtin_amdgcn_ballot_w64(win && b0 == 0)) {
-            if (win && b0 == 0) {
-#pragma unroll
-                for (int i = 0; i < PL; ++i) insert4(b0, b1, b2, b3, key[i] < mx ? key[i] : 0u);
-            }
-        }
-        if ((kk & 63) == lane) mine = u;
-        if ((kk & 63) == 63 || kk == p.K - 1) {
-            const int base = kk & ~63;
-            if (lane <= kk - base) {
-                if (p.idx32) p.idx32[out0 + base + lane] = mine;
-                if (p.idx64) p.idx64[out0 + base + lane] = mine;
-            }
-        }
-    }
+    select_topk<PL>(raw, p.nb, p.K, lane, (((int64_t)b * p.nb + t) * p.Hk + h) * p.K, p.idx32, p.idx64);
 }
 
 template <int PL>

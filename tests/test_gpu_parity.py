@@ -214,6 +214,25 @@ def test_compressed_branch_alone(B, N, Hq, Hk):
         close(out[:, :, 0], ref)
 
 
+@pytest.mark.parametrize("B,N,Hq,Hk,K,no_cmp", [(1, 513 * 64, 4, 1, 8, False), (2, 300 * 64, 8, 2, 8, False),
+                                                (1, 513 * 64, 4, 1, 8, True)],
+                         ids=["items513", "b2_items1200", "items513_no_compression"])
+def test_grid_partial_last_round(B, N, Hq, Hk, K, no_cmp):
+    """Grids of 513 and 1200 attention workgroups: a partial last round on 512 slots, and item
+    counts that do not divide by the 8 XCDs (the first XCDs take one item more): every output
+    row against the oracle."""
+    print(f"partial last round B={B} N={N} heads {Hq}/{Hk} K={K} no_compression={no_cmp}", flush=True)
+    q, k, v = rand(B, N, Hq, 64, seed=11), rand(B, N, Hk, 64, seed=12), rand(B, N, Hk, 64, seed=13)
+    w = torch.sigmoid(torch.randn(3, B, N, Hq, generator=torch.Generator().manual_seed(14))).to(torch.bfloat16)
+    w = w.unsqueeze(-1)
+    out, idx = _run_full(q, k, v, w, 64, 64, K, no_compression=no_cmp)
+    ref, parts = O.mosaic_attn_func(q, k, v, w, 64, 64, K, False, no_compression=no_cmp, block_indices=idx,
+                                    return_parts=True)
+    bad, amb, rows = O.selection_band_check(parts["scores"].permute(0, 2, 1, 3), idx, K)
+    assert bad == 0, f"{bad}/{rows} rows violate the band rule"
+    close(out, ref)
+
+
 def test_mosaic_attn_func_variants():
     wl = BOTTLENECK_NSIDE16
     q, k, v, w = make_inputs(wl, seed=1)
