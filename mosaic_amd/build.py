@@ -31,12 +31,13 @@ COMMON_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-# Per-source flags.  cmp.hip: keep MFMA accumulators in VGPRs; by default the compiler puts
-# them in AGPRs there and copies the softmax operands back and forth every tile (48
-# v_accvgpr_read per tile).  The attention kernel keeps its default (the flag costs it
+# Per-source flags.  cmp.hip and bwd.hip: keep MFMA accumulators in VGPRs; by default the
+# compiler puts them in AGPRs there and copies the softmax operands back and forth every tile
+# (48 v_accvgpr_read per tile in cmp; 352 accumulator moves in the grad-k/v kernel).  The attention kernel keeps its default (the flag costs it
 # occupancy in its two-wave instantiations).
 FILE_FLAGS = {
     "cmp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

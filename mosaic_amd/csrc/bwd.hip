@@ -16,9 +16,9 @@
 // holds its block (one pass over the [nb, K] index rows of its kv head) and then walks the
 // marked blocks in ascending order -- the reference's loop order, without the mask tensor.
 //
-// Workgroups are 4 waves.  Each phase of a 64 x 64 tile step gives every wave one 32 x 32
-// quadrant; operands come from LDS rows (16-byte reads), with transposed copies of the
-// operands whose MFMA B side runs along the token dimension.
+// Tiles reach LDS by direct-to-LDS loads (no register staging) in a layout that both 16-byte
+// row reads and ds_read_b64_tr_b16 transposing reads take without bank conflicts, so no
+// transposed copy of any operand is stored.
 
 #include <hip/hip_runtime.h>
 
@@ -32,7 +32,6 @@ namespace mosaic {
 namespace {
 
 constexpr float kLn2 = 0.69314718056f;   // ops.py:197
-constexpr int kLd = 72;                  // LDS row stride in bf16 (144 bytes: 16-byte aligned rows)
 constexpr int kMaxBwdBlocks = 4096;      // query blocks a key tile can mark (LDS flags)
 
 struct BwdParams {
@@ -43,6 +42,8 @@ struct BwdParams {
     const bf16_t* o;        // forward output [B, N, Hq, 64] contiguous
     const float* lse;       // [B, N, Hq] base-2 log-sum-exp of the scaled logits
     float* delta;           // [B, N, Hq] (workspace)
+    bf16_t* qs;             // q' = bf16((q scale) log2 e), [B, N, Hq, 64] contiguous (workspace):
+                            // written by the grad-q kernel, read by the grad-k/v kernel
     const int64_t* idx;     // [B, nb, Hk, K]
     bf16_t* dq; bf16_t* dk; bf16_t* dv;   // contiguous [B, N, H, 64]
     int B, N, Hq, Hk, G, bs, K, nb;
@@ -54,67 +55,6 @@ __device__ __forceinline__ void unpack8(const uint4& u, float f[8]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) { f[2 * i] = bf_lo(w[i]); f[2 * i + 1] = bf_hi(w[i]); }
 }
-__device__ __forceinline__ uint4 pack8(const float f[8]) {
-    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
-                      pack_bf16x2(f[6], f[7]));
-}
-__device__ __forceinline__ bf16x8 lds8(const bf16_t* p) { return as_bf16x8(*reinterpret_cast<const uint4*>(p)); }
-
-// A 64-row x 64-dim tile of a [B, N, H, 64] tensor moves global -> registers -> LDS in two
-// steps, so the loads of the next tile are in flight while the current one is computed.
-// 256 threads, two 16-byte chunks each: chunk c = thread + 256 i is row c / 8, dims 8 (c % 8).
-__device__ __forceinline__ void load_rows(const bf16_t* base, int64_t sn, uint4 reg[2]) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = threadIdx.x + 256 * i;
-        reg[i] = ld16(base + (int64_t)(c >> 3) * sn + (c & 7) * 8);
-    }
-}
-
-// Registers -> LDS rows (row-major, optionally also transposed), scaled to q' when QSCALE.
-template <bool QSCALE, bool TRANSPOSE>
-__device__ __forceinline__ void store_rows(const uint4 reg[2], bf16_t* rows, bf16_t* cols, float scale) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int c = threadIdx.x + 256 * i;
-        const int r = c >> 3, c8 = (c & 7) * 8;
-        uint4 u = reg[i];
-        if (QSCALE || TRANSPOSE) {
-            float f[8];
-            unpack8(u, f);
-            if (QSCALE) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) f[e] = (f[e] * scale) * kLog2e;
-                u = pack8(f);
-                unpack8(u, f);
-            }
-            if (TRANSPOSE) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) cols[(c8 + e) * kLd + r] = (bf16_t)(pack_bf16x2(f[e], 0.f) & 0xffffu);
-            }
-        }
-        *reinterpret_cast<uint4*>(rows + r * kLd + c8) = u;
-    }
-}
-
-template <bool QSCALE, bool TRANSPOSE>
-__device__ __forceinline__ void stage_rows(const bf16_t* base, int64_t sn, bf16_t* rows, bf16_t* cols,
-                                           float scale) {
-    uint4 reg[2];
-    load_rows(base, sn, reg);
-    store_rows<QSCALE, TRANSPOSE>(reg, rows, cols, scale);
-}
-
-// D(32x32) += A(32 x 64) B(64 x 32) with A rows and B columns read as 16-byte LDS runs:
-// a_rows[m][k], b_rows[n][k] (both "row = output index, 64 contiguous k").
-__device__ __forceinline__ f32x16 mma_32x32x64(const bf16_t* a_rows, const bf16_t* b_rows, f32x16 acc, int lane) {
-    const int r = lane & 31, kh = 8 * (lane >> 5);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-        acc = mfma32(lds8(a_rows + r * kLd + 16 * kk + kh), lds8(b_rows + r * kLd + 16 * kk + kh), acc);
-    return acc;
-}
-
 // ------------------------------------------------------------------ delta
 __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
     // one wave per 8 (b, n, h) rows; lane l: row l / 8, dims 8 (l % 8) .. +7
@@ -140,211 +80,451 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
-// MFMA A operand of the transpose of a row-major LDS tile T[token][dim] (row stride kLd): lane
-// l receives dim d0 + l % 32 for tokens t0 + 4 (l / 32) + 0..3 and t0 + 8 + 4 (l / 32) + 0..3,
-// the accumulator row order of P and dS.  ds_read_b64_tr_b16 hands lane 4a + b of each
-// 16-lane group element b of the 8-byte rows addressed by lanes a, a + 4, a + 8, a + 12, so
-// lane s of a group addresses token 4 (l / 32) + s / 4, dims 16 ((l / 16) % 2) + 4 (s % 4).
-__device__ __forceinline__ bf16x8 lds_tr_operand(const bf16_t* T, int t0, int d0, int lane) {
-    const int s = lane & 15;
-    const bf16_t* p = T + (t0 + 4 * (lane >> 5) + (s >> 2)) * kLd + d0 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
-    const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                   (__attribute__((address_space(3))) v4i16*)(p)));
-    const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                   (__attribute__((address_space(3))) v4i16*)(p + 8 * kLd)));
-    return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-}
-
-// The same row order from a row-major tile read along its rows: elements k0 + 4 (l / 32) + 0..3
-// and k0 + 8 + 4 (l / 32) + 0..3 of row r.
-__device__ __forceinline__ bf16x8 lds_row_perm(const bf16_t* T, int r, int k0, int lane) {
-    const bf16_t* p = T + r * kLd + k0 + 4 * (lane >> 5);
-    const uint2 lo = *reinterpret_cast<const uint2*>(p);
-    const uint2 hi = *reinterpret_cast<const uint2*>(p + 8);
-    return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-}
-
 // ------------------------------------------------------------------ grad q
-// grid (N / 64 query tiles, Hq, B)
-__global__ __launch_bounds__(256) void bwd_dq_kernel(BwdParams p) {
-    __shared__ __attribute__((aligned(16))) bf16_t Qs[64 * kLd], Gs[64 * kLd], Ks[64 * kLd], Vs[64 * kLd],
-        Ds[64 * kLd];
-    __shared__ float lse_s[64], dl_s[64];
-    const int qt = blockIdx.x, j = blockIdx.y, b = blockIdx.z;
-    const int c = j / p.G;
-    const int n0 = qt * 64;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    stage_rows<true, false>(p.q + (int64_t)b * p.q_sb + (int64_t)n0 * p.q_sn + (int64_t)j * p.q_sh, p.q_sn, Qs,
-                            nullptr, p.scale);
-    stage_rows<false, false>(p.go + (int64_t)b * p.go_sb + (int64_t)n0 * p.go_sn + (int64_t)j * p.go_sh, p.go_sn,
-                             Gs, nullptr, 0.f);
-    if (threadIdx.x < 64) {
-        const int64_t r = ((int64_t)b * p.N + n0 + threadIdx.x) * p.Hq + j;
-        lse_s[threadIdx.x] = p.lse[r];
-        dl_s[threadIdx.x] = p.delta[r];
+// One workgroup = (batch b, kv head c, 64-query tile, NW query heads of the GQA group); wave w
+// owns query head j = c G + NW h + w and all 64 rows of the tile, as the forward kernel does:
+// the selected blocks' 64-key K and V tiles go from global memory straight into LDS (two
+// buffers, one barrier per tile) and are read by every wave of the group.  Per tile and 32-key
+// half kt, computed transposed so a lane owns one query column (lse and delta are per-lane
+// registers):
+//   S^T  = K Q'^T          A = K rows (b128 reads),  B = q' fragments (registers)
+//   dP^T = V dO^T          A = V rows,               B = do fragments (registers)
+//   dS   = bf16(exp2(S - lse) ln2 (dP - delta)), packed in accumulator order as B operands
+//   dQ^T += K^T dS^T       A = K^T (transposing ds_read_b64_tr_b16 reads of the K tile)
+// Both tiles use the bwd_swz layout.
+constexpr int kTileElems = 64 * 64;
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier for LDS data whose direct-to-LDS loads each wave has already waited for
+// itself: __syncthreads() would also wait for every load still in flight (its release fence
+// covers the loads' LDS writes), which takes the prefetch of the next step out of the overlap.
+// The memory clobber keeps the compiler from moving LDS accesses across it; lgkmcnt(0) retires
+// this wave's LDS reads of the slot that is refilled after the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// LDS layout of the backward's 64-row tiles: 128-byte rows, chunk c of row r at position
+// c ^ bwd_swz(r).  The tiles are read both along rows (ds_read_b128 of one chunk of 16
+// consecutive rows) and transposed (ds_read_b64_tr_b16 of two chunks of 4 consecutive rows,
+// two such groups per cycle); bwd_swz makes both conflict-free: over rows of one parity in 16
+// consecutive rows it is a permutation of 0..7, and rows r and r + 2 of an aligned group of
+// four differ in bit 2, so their four-chunk runs land on disjoint banks.
+__device__ __forceinline__ int bwd_swz(int row) { return (((row >> 1) & 1) << 2) | ((row >> 2) & 3); }
+
+// Per-lane byte offsets of one 64-row tile's direct-to-LDS loads: NW waves, 8/NW runs of
+// 8 rows each; chunk pos of row r holds global chunk pos ^ bwd_swz(r).
+template <int NW>
+__device__ __forceinline__ void tile_dma_init(uint32_t* dk, uint32_t* dv, int wave, int lane, int64_t ksn, int64_t vsn) {
+#pragma unroll
+    for (int i = 0; i < 8 / NW; ++i) {
+        const int row = 8 * (wave * (8 / NW) + i) + (lane >> 3), pos = lane & 7;
+        const int src = 8 * (pos ^ bwd_swz(row));
+        dk[i] = 2u * (uint32_t)(row * ksn + src);
+        dv[i] = 2u * (uint32_t)(row * vsn + src);
     }
-    const int64_t* sel = p.idx + (((int64_t)b * p.nb + n0 / p.bs) * p.Hk + c) * p.K;
-    const int rh = w & 1, kh = w >> 1;   // phase 2: query half, key half
-    const int dh = w >> 1;               // phase 3: dim half (query half rh)
-    f32x16 acc;
+}
+template <int NW>
+__device__ __forceinline__ void tile_dma(const uint32_t* dk, const uint32_t* dv, const bf16_t* kb, const bf16_t* vb,
+                                         int64_t ksn, int64_t vsn, int key0, bf16_t* Kd, bf16_t* Vd, int wave) {
+    const int k0 = __builtin_amdgcn_readfirstlane(key0);
+    const char* kt = reinterpret_cast<const char*>(kb + (int64_t)k0 * ksn);
+    const char* vt = reinterpret_cast<const char*>(vb + (int64_t)k0 * vsn);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[e] = 0.f;
-    // steps: the 64-key tiles of the valid selected blocks, in top-k order
-    const int tiles = p.bs / 64;
-    auto next_valid = [&](int i) {   // first entry >= i holding a block in range (uniform)
-        while (i < p.K && (sel[i] < 0 || sel[i] >= p.nb)) ++i;
-        return i;
-    };
-    int i = next_valid(0), t = 0;
-    uint4 kr[2], vr[2];
-    auto load_kv = [&](int i_, int t_) {
-        const int key0 = (int)sel[i_] * p.bs + 64 * t_;
-        load_rows(p.k + (int64_t)b * p.k_sb + (int64_t)key0 * p.k_sn + (int64_t)c * p.k_sh, p.k_sn, kr);
-        load_rows(p.v + (int64_t)b * p.v_sb + (int64_t)key0 * p.v_sn + (int64_t)c * p.v_sh, p.v_sn, vr);
-    };
-    if (i < p.K) load_kv(i, 0);
-    while (i < p.K) {
-        __syncthreads();   // previous step's readers of Ks / Vs / Ds are done
-        store_rows<false, false>(kr, Ks, nullptr, 0.f);
-        store_rows<false, false>(vr, Vs, nullptr, 0.f);
-        if (++t == tiles) { t = 0; i = next_valid(i + 1); }
-        if (i < p.K) load_kv(i, t);   // next step's tiles, in flight during this step
-        __syncthreads();
-        f32x16 s, dp;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
-        s = mma_32x32x64(Qs + 32 * rh * kLd, Ks + 32 * kh * kLd, s, lane);
-        dp = mma_32x32x64(Gs + 32 * rh * kLd, Vs + 32 * kh * kLd, dp, lane);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int r = 32 * rh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-            const float pr = exp2f(s[e] - lse_s[r]) * kLn2;
-            const float ds = pr * (dp[e] - dl_s[r]);
-            Ds[r * kLd + 32 * kh + (lane & 31)] = (bf16_t)(pack_bf16x2(ds, 0.f) & 0xffffu);
+    for (int i = 0; i < 8 / NW; ++i) {
+        const int row0 = 8 * (wave * (8 / NW) + i);
+        __builtin_amdgcn_global_load_lds(kt + dk[i], (lds_void*)(Kd + row0 * 64), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vt + dv[i], (lds_void*)(Vd + row0 * 64), 16, 0, 0);
+    }
+}
+
+template <int NW>
+__global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(1, 1)))
+void bwd_dq_kernel(BwdParams p, int head_groups, int total_wgs) {
+    __shared__ __attribute__((aligned(1024))) bf16_t Ks0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t Ks1[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t Vs0[kTileElems];
+    __shared__ __attribute__((aligned(1024))) bf16_t Vs1[kTileElems];
+    __shared__ int sel_key0[kMaxSelected];  // first key of each in-range selected block, top-k order
+    __shared__ int sel_count;
+
+    const int lane = threadIdx.x & 63, r = lane & 31, hh = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int qtiles = p.N / 64;
+    const int L = xcd_remap(blockIdx.x, total_wgs);
+    const int qtile = L % qtiles, rest = L / qtiles;
+    const int hg = rest % (p.Hk * head_groups), b = rest / (p.Hk * head_groups);
+    const int c = hg / head_groups;
+    const int j = c * p.G + (hg % head_groups) * NW + wave;
+    const int n0 = qtile * 64;
+    const bf16_t* kb = p.k + (int64_t)b * p.k_sb + (int64_t)c * p.k_sh;
+    const bf16_t* vb = p.v + (int64_t)b * p.v_sb + (int64_t)c * p.v_sh;
+
+    // wave 0 compacts the in-range selected blocks (duplicates kept: each entry counts, as the
+    // reference's loop over the entries does)
+    if (wave == 0) {
+        const int64_t* ip = p.idx + (((int64_t)b * p.nb + n0 / p.bs) * p.Hk + c) * p.K;
+        int count = 0;
+        for (int base = 0; base < p.K; base += 64) {
+            const int i = base + lane;
+            const int64_t blk = i < p.K ? ip[i] : -1;
+            const bool ok = blk >= 0 && blk < p.nb;
+            const uint64_t mask = __builtin_amdgcn_ballot_w64(ok);
+            const int pos = count + (int)__builtin_popcountll(mask & ((1ull << lane) - 1ull));
+            if (ok) sel_key0[pos] = (int)(blk * p.bs);
+            count += (int)__builtin_popcountll(mask);
         }
-        __syncthreads();
-        // dQ += dS k: A = dS rows and B = k^T (transposing reads of the row-major k tile), both
-        // with the keys of each 16-key step in the order 4 (l / 32) + 0..3, 8 + 4 (l / 32) + 0..3
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-            acc = mfma32(lds_row_perm(Ds, 32 * rh + (lane & 31), 16 * kk, lane),
-                         lds_tr_operand(Ks, 16 * kk, 32 * dh, lane), acc);
+        if (lane == 0) sel_count = count;
     }
+    // this wave's rows: q' = bf16((q scale) log2 e) and do as MFMA B fragments, lse and delta
+    bf16x8 qf[2][4], gf[2][4];
+    float lse[2], dlt[2];
+    {
+        const bf16_t* qb = p.q + (int64_t)b * p.q_sb + (int64_t)j * p.q_sh;
+        const bf16_t* gb = p.go + (int64_t)b * p.go_sb + (int64_t)j * p.go_sh;
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const int n = n0 + 32 * qt + r;
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds) {
+                qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)n * p.q_sn + 16 * ds + 8 * hh));
+                gf[qt][ds] = as_bf16x8(ld16(gb + (int64_t)n * p.go_sn + 16 * ds + 8 * hh));
+            }
+            const int64_t row = ((int64_t)b * p.N + n) * p.Hq + j;
+            lse[qt] = p.lse[row];
+            dlt[qt] = p.delta[row];
+        }
+        // q' for the grad-k/v kernel (the rows this lane holds: query 32 qt + r, dims 16 ds + 8 hh)
+        bf16_t* qsb = p.qs + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds) {
+                const uint4 u = __builtin_bit_cast(uint4, qf[qt][ds]);
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+                uint32_t o4[4];
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm)
+                    o4[mm] = pack_bf16x2((bf_lo(w[mm]) * p.scale) * kLog2e, (bf_hi(w[mm]) * p.scale) * kLog2e);
+                const uint4 sc = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+                qf[qt][ds] = as_bf16x8(sc);
+                *reinterpret_cast<uint4*>(qsb + (int64_t)(32 * qt + r) * p.Hq * 64 + 16 * ds + 8 * hh) = sc;
+            }
+    }
+    __syncthreads();
+    const int sub = p.bs / 64;
+    const int total = sel_count * sub;
+    int cur_k = 0, cur_s = 0;
+    const int selv = lane < sel_count ? sel_key0[lane] : 0;
+    auto next_key0 = [&]() -> int {   // tiles are requested in order
+        const int base = sel_count <= 64 ? __builtin_amdgcn_readlane(selv, cur_k) : sel_key0[cur_k];
+        const int key0 = base + cur_s * 64;
+        if (++cur_s == sub) {
+            cur_s = 0;
+            ++cur_k;
+        }
+        return key0;
+    };
+    uint32_t dk[8 / NW], dv[8 / NW];
+    tile_dma_init<NW>(dk, dv, wave, lane, p.k_sn, p.v_sn);
+    if (total > 0) tile_dma<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(), Ks0, Vs0, wave);
+
+    // per-lane LDS element offsets: row reads of key row 32 kt + r, chunk 2 ds + hh; transposing
+    // reads of dims 32 dt + (lane % 32) for keys 16 s2 + 4 hh + 0..3 (+ 8 for sec = 1)
+    int rk[4], tk[2][2];
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) rk[ds] = r * 64 + 8 * ((2 * ds + hh) ^ bwd_swz(r));
+    {
+        const int s = lane & 15, half = (lane >> 4) & 1;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int sec = 0; sec < 2; ++sec) {
+                const int row = 4 * hh + (s >> 2) + 8 * sec;
+                const int chunk = 4 * dt + 2 * half + ((s & 3) >> 1);
+                tk[dt][sec] = row * 64 + 8 * (chunk ^ bwd_swz(row)) + 4 * (s & 1);
+            }
+    }
+    f32x16 acc[2][2];  // dQ^T [dim block dt][query block qt]
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[dt][qt][e] = 0.f;
+
+    auto tile = [&](const bf16_t* Kc, const bf16_t* Vc) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            f32x16 s[2], dp[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) { s[qt][e] = 0.f; dp[qt][e] = 0.f; }
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds) {
+                const bf16x8 ka = as_bf16x8(*reinterpret_cast<const uint4*>(Kc + 32 * kt * 64 + rk[ds]));
+                const bf16x8 va = as_bf16x8(*reinterpret_cast<const uint4*>(Vc + 32 * kt * 64 + rk[ds]));
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    s[qt] = mfma32(ka, qf[qt][ds], s[qt]);
+                    dp[qt] = mfma32(va, gf[qt][ds], dp[qt]);
+                }
+            }
+            // dS in accumulator order, packed as the B operand: keys 16 s2 + 4 hh + 0..3, + 8
+            bf16x8 db[2][2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    uint32_t w4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int e0 = 8 * s2 + 2 * i;
+                        const float p0 = __builtin_amdgcn_exp2f(s[qt][e0] - lse[qt]) * kLn2;
+                        const float p1 = __builtin_amdgcn_exp2f(s[qt][e0 + 1] - lse[qt]) * kLn2;
+                        w4[i] = pack_bf16x2(p0 * (dp[qt][e0] - dlt[qt]), p1 * (dp[qt][e0 + 1] - dlt[qt]));
+                    }
+                    db[qt][s2] = as_bf16x8(make_uint4(w4[0], w4[1], w4[2], w4[3]));
+                }
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+                    const bf16_t* kp = Kc + (32 * kt + 16 * s2) * 64;
+                    const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                                   (__attribute__((address_space(3))) v4i16*)(kp + tk[dt][0])));
+                    const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                                   (__attribute__((address_space(3))) v4i16*)(kp + tk[dt][1])));
+                    const bf16x8 kT = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) acc[dt][qt] = mfma32(kT, db[qt][s2], acc[dt][qt]);
+                }
+        }
+    };
+    // tile t in buffer t & 1: wait for this wave's loads, the barrier publishes every wave's loads
+    // and frees the other buffer, whose next tile is requested right away
+    for (int t = 0; t < total; t += 2) {
+        wait_vmem();
+        __syncthreads();
+        if (t + 1 < total) tile_dma<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(), Ks1, Vs1, wave);
+        tile(Ks0, Vs0);
+        if (t + 1 >= total) break;
+        wait_vmem();
+        __syncthreads();
+        if (t + 2 < total) tile_dma<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(), Ks0, Vs0, wave);
+        tile(Ks1, Vs1);
+    }
+    // dq = bf16((dQ scale) log2 e), rows n0 + 32 qt + r, dims 32 dt + 8 g4 + 4 hh + 0..3
     bf16_t* out = p.dq + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int r = 32 * rh + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        out[(int64_t)r * p.Hq * 64 + 32 * dh + (lane & 31)] =
-            (bf16_t)(pack_bf16x2((acc[e] * p.scale) * kLog2e, 0.f) & 0xffffu);
-    }
+    for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+                const f32x16& a = acc[dt][qt];
+                uint2 w2;
+                w2.x = pack_bf16x2((a[4 * g4 + 0] * p.scale) * kLog2e, (a[4 * g4 + 1] * p.scale) * kLog2e);
+                w2.y = pack_bf16x2((a[4 * g4 + 2] * p.scale) * kLog2e, (a[4 * g4 + 3] * p.scale) * kLog2e);
+                *reinterpret_cast<uint2*>(out + (int64_t)(32 * qt + r) * p.Hq * 64 + 32 * dt + 8 * g4 + 4 * hh) = w2;
+            }
 }
 
 // ------------------------------------------------------------------ grad k, grad v
 // grid (N / 64 key tiles, Hk, B).  Wave w = (key half kh = w / 2, query half qh = w % 2).  Per
-// step a wave forms S = q' k^T and dP = do v^T for its 32 queries x 32 keys; P and dS stay in
-// registers, where the accumulator layout (lane: one key column, 16 query rows) is exactly the
-// MFMA B operand of dV^T += do^T P and dK^T += q'^T dS with k running over those query rows;
-// the A operands (do^T, q'^T) come from transposing LDS reads of the row-major tiles in the
-// same row order, so no transposed copy is staged.
-// The two waves of a key half sum their partial dV^T / dK^T once, at the end.
-__global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
-    __shared__ __attribute__((aligned(16))) bf16_t smem[4 * 64 * kLd];   // also the final 32 KB reduction
-    __shared__ float lse_s[64], dl_s[64];
-    __shared__ uint8_t mark[kMaxBwdBlocks];
-    bf16_t* Ks = smem;
-    bf16_t* Vs = smem + 64 * kLd;
-    bf16_t* Qs = smem + 2 * 64 * kLd;
-    bf16_t* Gs = smem + 3 * 64 * kLd;
+// step -- one (marked query block tile, query head of the group) -- a wave forms S = q' k^T and
+// dP = do v^T for its 32 queries x 32 keys; P and dS stay in registers, where the accumulator
+// layout (lane: one key column, 16 query rows) is exactly the MFMA B operand of
+// dV^T += do^T P and dK^T += q'^T dS with k running over those query rows; the A operands
+// (do^T, q'^T) come from transposing LDS reads of the row-major tiles in the same row order.
+// The step's q' rows (pre-scaled by the grad-q kernel), do rows, lse and delta go from global
+// memory straight into LDS: a ring of three slots, loads requested two steps ahead, one barrier
+// per step.  All tiles use the bwd_swz layout.  The two waves of a key half sum their partial
+// dV^T / dK^T once, at the end.
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256)))
+void bwd_dkv_kernel(BwdParams p) {
+    __shared__ __attribute__((aligned(1024))) bf16_t kvs[2 * kTileElems];   // K tile, V tile
+    bf16_t* Ks = kvs;
+    bf16_t* Vs = kvs + kTileElems;
+    // Three steps in a ring; a slot holds the step's q' tile, do tile, then lse and delta of its
+    // 64 rows (fp32).  Each slot is an array of its own and the loop below is unrolled over
+    // the slots, so the compiler sees that a step's LDS reads and the loads in flight into the
+    // other slots touch different objects and does not wait for those loads before the reads.
+    // The final reduction reuses slots 0 and 1.
+    constexpr int kSlotElems = 2 * kTileElems + 256;
+    __shared__ __attribute__((aligned(1024))) bf16_t ring0[kSlotElems], ring1[kSlotElems], ring2[kSlotElems];
+    __shared__ uint64_t mark[kMaxBwdBlocks / 64];   // bit t: query block t selected this block
     const int kt = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int key0 = kt * 64;
     const int64_t u = key0 / p.bs;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    // query blocks whose selection row (kv head c) holds block u: eight entries per step, all
-    // loads of a step issued before any compare
-    for (int t = threadIdx.x; t < p.nb; t += 256) {
-        const int64_t* row = p.idx + (((int64_t)b * p.nb + t) * p.Hk + c) * p.K;
+    const int lane = threadIdx.x & 63, r = lane & 31, hh = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // K and V of the key tile
+    uint32_t dk[2], dv[2];
+    tile_dma_init<4>(dk, dv, w, lane, p.k_sn, p.v_sn);
+    tile_dma<4>(dk, dv, p.k + (int64_t)b * p.k_sb + (int64_t)c * p.k_sh, p.v + (int64_t)b * p.v_sb + (int64_t)c * p.v_sh,
+                p.k_sn, p.v_sn, key0, Ks, Vs, w);
+    // query blocks whose selection row (kv head c) holds block u, as a bitmap: lane l of a wave
+    // scans row 64 i + l (eight entries per step, all loads of a step issued before any
+    // compare) and the wave's ballot is word i
+    for (int i = w; i < (p.nb + 63) / 64; i += 4) {
+        const int t = 64 * i + lane;
         bool hit = false;
-        for (int i0 = 0; i0 < p.K; i0 += 8) {
-            int64_t e[8];
+        if (t < p.nb) {
+            const int64_t* row = p.idx + (((int64_t)b * p.nb + t) * p.Hk + c) * p.K;
+            for (int i0 = 0; i0 < p.K; i0 += 8) {
+                int64_t e[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) e[i] = i0 + i < p.K ? row[i0 + i] : -1;
+                for (int k8 = 0; k8 < 8; ++k8) e[k8] = i0 + k8 < p.K ? row[i0 + k8] : -1;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) hit |= e[i] == u;
+                for (int k8 = 0; k8 < 8; ++k8) hit |= e[k8] == u;
+            }
         }
-        mark[t] = hit;
+        const uint64_t bits = __builtin_amdgcn_ballot_w64(hit);
+        if (lane == 0) mark[i] = bits;
     }
-    stage_rows<false, false>(p.k + (int64_t)b * p.k_sb + (int64_t)key0 * p.k_sn + (int64_t)c * p.k_sh, p.k_sn, Ks,
-                             nullptr, 0.f);
-    stage_rows<false, false>(p.v + (int64_t)b * p.v_sb + (int64_t)key0 * p.v_sn + (int64_t)c * p.v_sh, p.v_sn, Vs,
-                             nullptr, 0.f);
     __syncthreads();
     const int kh = w >> 1, qh = w & 1;
-    const int hq = 4 * (lane >> 5);         // this lane's row offset inside each group of 8 rows
-    f32x16 dkT[2], dvT[2];                  // [d block]: rows d = 32 db + row(e), column key 32 kh + lane % 32
+    f32x16 dkT[2], dvT[2];  // [d block]: rows d = 32 db + row(e), column key 32 kh + lane % 32
 #pragma unroll
     for (int e = 0; e < 16; ++e) { dkT[0][e] = 0.f; dkT[1][e] = 0.f; dvT[0][e] = 0.f; dvT[1][e] = 0.f; }
     // steps: (marked query block t, its 64-row tile tt, query head g of the group), ascending
     const int tiles = p.bs / 64;
-    auto next_marked = [&](int t) {   // first marked block >= t (uniform LDS reads)
-        while (t < p.nb && !mark[t]) ++t;
-        return t;
+    auto next_marked = [&](int t) {   // first marked block >= t, or nb (uniform LDS reads)
+        const int words = (p.nb + 63) / 64;
+        int i = t >> 6;
+        if (i >= words) return p.nb;
+        uint64_t m = mark[i] & (~0ull << (t & 63));
+        while (m == 0) {
+            if (++i >= words) return p.nb;
+            m = mark[i];
+        }
+        return 64 * i + (int)__builtin_ctzll(m);
     };
     int t = next_marked(0), tt = 0, g = 0;
-    uint4 qr[2], gr[2];
-    float lr = 0.f, dr = 0.f;
-    auto load_q = [&](int t_, int tt_, int g_) {
-        const int n0 = t_ * p.bs + 64 * tt_;
-        const int j = c * p.G + g_;
-        load_rows(p.q + (int64_t)b * p.q_sb + (int64_t)n0 * p.q_sn + (int64_t)j * p.q_sh, p.q_sn, qr);
-        load_rows(p.go + (int64_t)b * p.go_sb + (int64_t)n0 * p.go_sn + (int64_t)j * p.go_sh, p.go_sn, gr);
-        if (threadIdx.x < 64) {
-            const int64_t r = ((int64_t)b * p.N + n0 + threadIdx.x) * p.Hq + j;
-            lr = p.lse[r];
-            dr = p.delta[r];
-        }
-    };
-    if (t < p.nb) load_q(t, 0, 0);
-    while (t < p.nb) {
-        __syncthreads();   // previous step's readers are done with Qs / Gs
-        store_rows<true, false>(qr, Qs, nullptr, p.scale);
-        store_rows<false, false>(gr, Gs, nullptr, 0.f);
-        if (threadIdx.x < 64) {
-            lse_s[threadIdx.x] = lr;
-            dl_s[threadIdx.x] = dr;
-        }
+    auto advance = [&]() {
         if (++g == p.G) {
             g = 0;
             if (++tt == tiles) { tt = 0; t = next_marked(t + 1); }
         }
-        if (t < p.nb) load_q(t, tt, g);   // next step's rows, in flight during this step
-        __syncthreads();
+    };
+    // per-lane byte offsets of the step's q' and do rows (8 rows per 1 KB run, two runs per wave)
+    uint32_t dq_[2], dg_[2];
+    tile_dma_init<4>(dq_, dg_, w, lane, (int64_t)p.Hq * 64, p.go_sn);
+    // one step's loads: every wave issues exactly six direct-to-LDS instructions (two 1 KB runs
+    // each of q' and do, and lse / delta of 16 rows), so a wait for all but the newest step's
+    // loads is one fixed s_waitcnt.  Past the last step it loads query rows 0..63 into the free
+    // slot (never read), so that no branch depends on the step count.
+    auto issue_step = [&](bf16_t* slot) __attribute__((always_inline)) {
+        bf16_t* Qd = slot;
+        bf16_t* Gd = slot + kTileElems;
+        float* ld = reinterpret_cast<float*>(slot + 2 * kTileElems);
+        const int n0 = t < p.nb ? t * p.bs + 64 * tt : 0;
+        const int j = c * p.G + g;
+        tile_dma<4>(dq_, dg_, p.qs + ((int64_t)b * p.N * p.Hq + j) * 64, p.go + (int64_t)b * p.go_sb + (int64_t)j * p.go_sh,
+                    (int64_t)p.Hq * 64, p.go_sn, n0, Qd, Gd, w);
+        const int64_t row = ((int64_t)b * p.N + n0 + 16 * w + (lane & 15)) * p.Hq + j;
+        if (lane < 16) {   // lane l -> 4 bytes at 4 l of this wave's 16 rows
+            __builtin_amdgcn_global_load_lds(p.lse + row, (lds_void*)(ld + 16 * w), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(p.delta + row, (lds_void*)(ld + 64 + 16 * w), 4, 0, 0);
+        }
+    };
+    // per-lane LDS element offsets: row reads (row 32 h + r, chunk 2 kk + hh) and transposing
+    // reads (dims 32 dt + lane % 32, rows 4 hh + 0..3 (+ 8) of a 16-row group)
+    int rd[4], tr[2][2];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) rd[kk] = r * 64 + 8 * ((2 * kk + hh) ^ bwd_swz(r));
+    {
+        const int s4 = lane & 15, half = (lane >> 4) & 1;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int sec = 0; sec < 2; ++sec) {
+                const int row = 4 * hh + (s4 >> 2) + 8 * sec;
+                const int chunk = 4 * dt + 2 * half + ((s4 & 3) >> 1);
+                tr[dt][sec] = row * 64 + 8 * (chunk ^ bwd_swz(row)) + 4 * (s4 & 1);
+            }
+    }
+    auto tr_read = [&](const bf16_t* T, int q0, int dt) __attribute__((always_inline)) -> bf16x8 {
+        const bf16_t* tp = T + q0 * 64;
+        const uint2 lo = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                       (__attribute__((address_space(3))) v4i16*)(tp + tr[dt][0])));
+        const uint2 hi = __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                       (__attribute__((address_space(3))) v4i16*)(tp + tr[dt][1])));
+        return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+    };
+    auto step = [&](const bf16_t* slot) __attribute__((always_inline)) {
+        const bf16_t* Qc = slot;
+        const bf16_t* Gc = slot + kTileElems;
+        const float* lc = reinterpret_cast<const float*>(slot + 2 * kTileElems);
+        const float* dc = lc + 64;
         f32x16 s, dp;
 #pragma unroll
         for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
-        s = mma_32x32x64(Qs + 32 * qh * kLd, Ks + 32 * kh * kLd, s, lane);    // S: queries x keys
-        dp = mma_32x32x64(Gs + 32 * qh * kLd, Vs + 32 * kh * kLd, dp, lane);  // dP
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const bf16x8 qa = as_bf16x8(*reinterpret_cast<const uint4*>(Qc + 32 * qh * 64 + rd[kk]));
+            const bf16x8 kb = as_bf16x8(*reinterpret_cast<const uint4*>(Ks + 32 * kh * 64 + rd[kk]));
+            const bf16x8 ga = as_bf16x8(*reinterpret_cast<const uint4*>(Gc + 32 * qh * 64 + rd[kk]));
+            const bf16x8 vb = as_bf16x8(*reinterpret_cast<const uint4*>(Vs + 32 * kh * 64 + rd[kk]));
+            s = mfma32(qa, kb, s);     // S: queries x keys
+            dp = mfma32(ga, vb, dp);   // dP
+        }
         bf16x8 pb[2], db[2];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int q = 32 * qh + 8 * (e >> 2) + hq + (e & 3);
-            const float pr = exp2f(s[e] - lse_s[q]);
-            const float ds = pr * (dp[e] - dl_s[q]) * kLn2;
-            pb[e >> 3][e & 7] = (__bf16)pr;
-            db[e >> 3][e & 7] = (__bf16)ds;
+        for (int g4 = 0; g4 < 4; ++g4) {   // rows 32 qh + 8 g4 + 4 hh + 0..3: one 16-byte read each
+            const float4 l4 = *reinterpret_cast<const float4*>(lc + 32 * qh + 8 * g4 + 4 * hh);
+            const float4 d4 = *reinterpret_cast<const float4*>(dc + 32 * qh + 8 * g4 + 4 * hh);
+            const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = 4 * g4 + i;
+                const float pr = __builtin_amdgcn_exp2f(s[e] - lv[i]);
+                const float ds = pr * (dp[e] - dv4[i]) * kLn2;
+                pb[e >> 3][e & 7] = (__bf16)pr;
+                db[e >> 3][e & 7] = (__bf16)ds;
+            }
         }
 #pragma unroll
         for (int dblk = 0; dblk < 2; ++dblk) {
 #pragma unroll
             for (int ch = 0; ch < 2; ++ch) {
                 const int q0 = 32 * qh + 16 * ch;
-                dvT[dblk] = mfma32(lds_tr_operand(Gs, q0, 32 * dblk, lane), pb[ch], dvT[dblk]);
-                dkT[dblk] = mfma32(lds_tr_operand(Qs, q0, 32 * dblk, lane), db[ch], dkT[dblk]);
+                dvT[dblk] = mfma32(tr_read(Gc, q0, dblk), pb[ch], dvT[dblk]);
+                dkT[dblk] = mfma32(tr_read(Qc, q0, dblk), db[ch], dkT[dblk]);
             }
         }
+    };
+    // a key tile that no query block selected has no steps (its gradients are zero)
+    int marked = 0;
+    for (int i = 0; i < (p.nb + 63) / 64; ++i) marked += __builtin_popcountll(mark[i]);
+    const int steps = marked * tiles * p.G;
+    issue_step(ring0);
+    advance();
+    issue_step(ring1);
+    advance();
+    // Step i uses ring slot i % 3.  Its loads were requested two steps earlier; wait for them,
+    // leaving the next step's six in flight, and the barrier publishes every wave's loads (the
+    // first time also K and V) and frees slot (i + 2) % 3, whose step is requested right away.
+    auto ring_step = [&](const bf16_t* cur, bf16_t* next) __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        lds_barrier();
+        issue_step(next);
+        advance();
+        step(cur);
+    };
+    for (int i = 0; i < steps; i += 3) {
+        ring_step(ring0, ring2);
+        if (i + 1 >= steps) break;
+        ring_step(ring1, ring0);
+        if (i + 2 >= steps) break;
+        ring_step(ring2, ring1);
     }
-    // sum the two query halves' partials: qh = 1 parks its accumulators in LDS
+    // sum the two query halves' partials: qh = 1 parks its accumulators in LDS (the staging
+    // buffers; with no steps the K / V loads may still be in flight, so wait for them first)
+    wait_vmem();
     __syncthreads();
-    float* red = reinterpret_cast<float*>(smem) + (kh * 64 + lane) * 64;
+    float* red = reinterpret_cast<float*>((kh == 0 ? ring0 : ring1) + hh * kTileElems) + r * 64;
     if (qh == 1) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -353,12 +533,12 @@ __global__ __launch_bounds__(256) void bwd_dkv_kernel(BwdParams p) {
     }
     __syncthreads();
     if (qh == 0) {
-        const int64_t base = (((int64_t)b * p.N + key0 + 32 * kh + (lane & 31)) * p.Hk + c) * 64;
+        const int64_t base = (((int64_t)b * p.N + key0 + 32 * kh + r) * p.Hk + c) * 64;
 #pragma unroll
         for (int dblk = 0; dblk < 2; ++dblk) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int d = 32 * dblk + 8 * (e >> 2) + hq + (e & 3);
+                const int d = 32 * dblk + 8 * (e >> 2) + 4 * hh + (e & 3);
                 p.dk[base + d] = (bf16_t)(pack_bf16x2(dkT[dblk][e] + red[16 * dblk + e], 0.f) & 0xffffu);
                 p.dv[base + d] = (bf16_t)(pack_bf16x2(dvT[dblk][e] + red[32 + 16 * dblk + e], 0.f) & 0xffffu);
             }
@@ -380,9 +560,15 @@ using namespace mosaic;
 
 extern "C" {
 
+// delta (fp32 per row), then q' (bf16 rows of 64), each 256-byte aligned
+static size_t bwd_delta_bytes(int32_t batch, int32_t seq_len, int32_t num_q_heads) {
+    return ((size_t)batch * seq_len * num_q_heads * sizeof(float) + 255) / 256 * 256;
+}
+
 size_t mosaic_sparse_attn_bwd_workspace_size(int32_t batch, int32_t seq_len, int32_t num_q_heads) {
     if (batch <= 0 || seq_len <= 0 || num_q_heads <= 0) return 0;
-    return ((size_t)batch * seq_len * num_q_heads * sizeof(float) + 255) / 256 * 256;
+    const size_t qs = ((size_t)batch * seq_len * num_q_heads * kHeadDim * sizeof(bf16_t) + 255) / 256 * 256;
+    return bwd_delta_bytes(batch, seq_len, num_q_heads) + qs;
 }
 
 int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const void* out, const float* lse,
@@ -413,6 +599,7 @@ int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const vo
     p.o = static_cast<const bf16_t*>(out);
     p.lse = lse;
     p.delta = static_cast<float*>(workspace);
+    p.qs = reinterpret_cast<bf16_t*>(static_cast<char*>(workspace) + bwd_delta_bytes(batch, seq_len, num_q_heads));
     p.idx = block_indices;
     p.dq = static_cast<bf16_t*>(grad_q); p.dk = static_cast<bf16_t*>(grad_k); p.dv = static_cast<bf16_t*>(grad_v);
     p.B = batch; p.N = seq_len; p.Hq = num_q_heads; p.Hk = num_kv_heads; p.G = num_q_heads / num_kv_heads;
@@ -425,9 +612,17 @@ int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const vo
     if (dgrid > 0x7fffffff) return MOSAIC_ERR_SHAPE;
     if (hipLaunchKernel((const void*)&bwd_delta_kernel, dim3((unsigned)dgrid), dim3(256), args, 0, s) != hipSuccess)
         return MOSAIC_ERR_LAUNCH;
-    if (hipLaunchKernel((const void*)&bwd_dq_kernel, dim3(seq_len / 64, num_q_heads, batch), dim3(256), args, 0, s) !=
-        hipSuccess)
-        return MOSAIC_ERR_LAUNCH;
+    // grad q: one workgroup per (batch, kv head, query tile, group of NW query heads)
+    const int G = num_q_heads / num_kv_heads;
+    const int nw = (G == 1 || G == 2 || G == 4) ? G : (G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1));
+    int head_groups = G / nw;
+    const int64_t dq_wgs = (int64_t)batch * num_kv_heads * head_groups * (seq_len / 64);
+    if (dq_wgs > 0x7fffffff) return MOSAIC_ERR_SHAPE;
+    int total_wgs = (int)dq_wgs;
+    void* dq_args[] = {&p, &head_groups, &total_wgs};
+    const void* dq_fn = nw == 4 ? (const void*)&bwd_dq_kernel<4>
+                      : nw == 2 ? (const void*)&bwd_dq_kernel<2> : (const void*)&bwd_dq_kernel<1>;
+    if (hipLaunchKernel(dq_fn, dim3(total_wgs), dim3(64 * nw), dq_args, 0, s) != hipSuccess) return MOSAIC_ERR_LAUNCH;
     if (hipLaunchKernel((const void*)&bwd_dkv_kernel, dim3(seq_len / 64, num_kv_heads, batch), dim3(256), args, 0,
                         s) != hipSuccess)
         return MOSAIC_ERR_LAUNCH;
