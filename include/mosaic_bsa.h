@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 3
+#define MOSAIC_BSA_ABI_VERSION 4
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -140,6 +140,44 @@ MOSAIC_API int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* worksp
 MOSAIC_API int mosaic_bsa_fwd_rope(const mosaic_bsa_args* args, const float* rope_cos, const float* rope_sin,
                                    void* q_rot, void* k_rot, void* workspace, size_t workspace_bytes,
                                    void* stream);
+
+/* Input side of mosaic_bsa_fwd_proj: the attention block's input x and its stacked projection
+   weight.  x: bf16 rows of model dimension dim (contiguous), token n of member b at
+   x + n * x_stride_n + b * x_stride_b (elements; the model's sequence-first [N, B, dim]
+   activations have x_stride_n = B * dim, x_stride_b = dim).  weight: bf16 [weight_rows, dim],
+   the nn.Linear weights to_q (Hq * 64 rows), to_k (Hk * 64), to_v (Hk * 64) and, unless the
+   mode is LOCAL_ONLY, to_strategy_combine_mlp (3 * Hq rows, channel 3 h + branch), each block
+   starting at a multiple of 64 rows: q at 0, k at 64 Hq, v at 64 (Hq + Hk), gates at
+   64 (Hq + 2 Hk); every other row zero; weight_rows = 256 * ceil(groups / 4) with
+   groups = Hq + 2 Hk (+ 1 with gates).  rope_cos / rope_sin: fp32 [seq_len, 32] as for
+   mosaic_bsa_fwd_rope, or both NULL for no rotation.  Outputs (caller-allocated, 16-byte
+   aligned): q, k, v bf16 [B, N, H, 64] contiguous (q and k rotated); weights bf16
+   [B, N, Hq, 3], the softmax of each head's three gate logits (NULL in LOCAL_ONLY mode). */
+typedef struct {
+    const void* x;
+    int64_t x_stride_n, x_stride_b;
+    int32_t dim;
+    int32_t weight_rows;
+    const void* weight;
+    const float* rope_cos;
+    const float* rope_sin;
+    void* q;
+    void* k;
+    void* v;
+    void* weights;
+} mosaic_proj_args;
+
+/* The attention block from its input rows: the q / k / v / gate projection
+   (primitives.py:182-195, one GEMM over the stacked weights), the 2-D RoPE of q and k
+   (:125-135, :193-195), the gate softmax (:171-180) and then the op (primitives.py:54-89) --
+   with the projection, RoPE, gate softmax and the block pooling of q, k and v (:65-66, 76) in
+   one kernel, so q, k and v are written once and the op does not read them back to pool them.
+   args as for mosaic_bsa_fwd, except that q, k, v, weights and their strides are ignored (the
+   projection's outputs take their place).  Requirements beyond mosaic_bsa_fwd's: dim a
+   positive multiple of 128; seq_len a multiple of 256; sparse_block_size 64 or 128 unless
+   LOCAL_ONLY; 3 * Hq <= 64.  Same workspace (mosaic_bsa_workspace_size of the same args). */
+MOSAIC_API int mosaic_bsa_fwd_proj(const mosaic_bsa_args* args, const mosaic_proj_args* proj, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 
 /* k-nearest-neighbour cross-attention between two grids: the gather-attention of
    CrossAttentionInterpolate.forward (primitives.py:265-283), from the kv projection to the

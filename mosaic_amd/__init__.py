@@ -16,12 +16,15 @@ from .primitives import (
     dense_attention,
     mosaic_attn_func,
     mosaic_attn_func_rope,
+    mosaic_attn_proj,
     pool_mean,
+    stack_projection_weight,
 )
 from .healpix import get_healpix_grid, pix2ang_nest
 
 __all__ = [
     "MosaicAttnFunction", "mosaic_attn_bwd", "mosaic_attn_fwd", "mosaic_sparse_attn", "MosaicAttention", "RoPE",
-    "attn_topk", "block_attention", "dense_attention", "mosaic_attn_func", "mosaic_attn_func_rope", "pool_mean",
+    "attn_topk", "block_attention", "dense_attention", "mosaic_attn_func", "mosaic_attn_func_rope", "mosaic_attn_proj",
+    "stack_projection_weight", "pool_mean",
     "get_healpix_grid", "pix2ang_nest",
 ]

@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # mosaic_bsa_mode
 MODE_FULL = 0
@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_bsa_fwd_noalloc",
     "mosaic_bsa_fwd_profiled",
     "mosaic_bsa_fwd_rope",
+    "mosaic_bsa_fwd_proj",
     "mosaic_knn_interp_fwd",
     "mosaic_sparse_attn_bwd_workspace_size",
     "mosaic_sparse_attn_bwd",
@@ -76,6 +77,15 @@ class BsaArgs(ctypes.Structure):
     ]
 
 
+class ProjArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("x_stride_n", ctypes.c_int64), ("x_stride_b", ctypes.c_int64),
+        ("dim", ctypes.c_int32), ("weight_rows", ctypes.c_int32), ("weight", ctypes.c_void_p),
+        ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("weights", ctypes.c_void_p),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -93,6 +103,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_bsa_fwd_profiled.restype = c_int
     lib.mosaic_bsa_fwd_rope.argtypes = [P(BsaArgs), c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]
     lib.mosaic_bsa_fwd_rope.restype = c_int
+    lib.mosaic_bsa_fwd_proj.argtypes = [P(BsaArgs), P(ProjArgs), c_vp, c_size, c_vp]
+    lib.mosaic_bsa_fwd_proj.restype = c_int
     lib.mosaic_knn_interp_fwd.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                           c_f, c_vp, c_vp]
     lib.mosaic_knn_interp_fwd.restype = c_int

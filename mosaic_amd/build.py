@@ -38,6 +38,7 @@ COMMON_FLAGS = [
 FILE_FLAGS = {
     "cmp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "proj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

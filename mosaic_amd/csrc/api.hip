@@ -179,8 +179,10 @@ struct RopeIO {
     void* k_rot;
 };
 
+// proj: the input side's projection kernel runs in place of the pooling pass (its q, k, v,
+// weights and pooled outputs feed the later kernels; a's q / k / v / weights point at them)
 int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* stream, void* const* events,
-                const RopeIO* rope = nullptr) {
+                const RopeIO* rope = nullptr, const ProjParams* proj = nullptr) {
     if (int e = validate(a)) return e;
     // With RoPE, the modes with both local and selected branches rotate q inside the attention
     // kernel, so the rotated q is an optional output there; the other modes read it back.
@@ -248,9 +250,16 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         }
         pp.B = B; pp.nb = L.nb; pp.nb_pad = L.nb_pad; pp.bs = a->sparse_block_size;
         if (sel) pp.kbnd = reinterpret_cast<float*>(w + L.kbnd);
-        if (rope) set_rope(pp);
-        if (int e = launch_status(launch_pool(pp, s))) return e;
-        if (rope) use_rotated();
+        if (proj) {
+            ProjParams jp = *proj;
+            jp.bs = a->sparse_block_size; jp.nb = L.nb; jp.nb_pad = L.nb_pad;
+            jp.qc = pp.out_bnhd[0]; jp.kfrag = pp.kfrag; jp.vfrag = pp.vfrag; jp.kbnd = pp.kbnd;
+            if (int e = launch_status(launch_proj(jp, s))) return e;
+        } else {
+            if (rope) set_rope(pp);
+            if (int e = launch_status(launch_pool(pp, s))) return e;
+            if (rope) use_rotated();
+        }
         if (int e = record(events, 1, s)) return e;
 
         CmpParams cp{};
@@ -287,7 +296,9 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         if (int e = record(events, 3, s)) return e;
         ap.ocmp = cb.ocmp;
     } else {
-        if (rope) {  // local attention only: the pooling pass just rotates q and k
+        if (proj) {  // local attention only: the projection without pooling
+            if (int e = launch_status(launch_proj(*proj, s))) return e;
+        } else if (rope) {  // local attention only: the pooling pass just rotates q and k
             PoolParams pp{};
             pp.x[0] = ap.q; pp.sb[0] = ap.q_sb; pp.sn[0] = ap.q_sn; pp.sh[0] = ap.q_sh; pp.heads[0] = Hq;
             pp.x[1] = ap.k; pp.sb[1] = ap.k_sb; pp.sn[1] = ap.k_sn; pp.sh[1] = ap.k_sh; pp.heads[1] = Hk;
@@ -337,6 +348,47 @@ int mosaic_bsa_fwd_rope(const mosaic_bsa_args* args, const float* rope_cos, cons
                         void* k_rot, void* workspace, size_t workspace_bytes, void* stream) {
     const RopeIO rope{rope_cos, rope_sin, q_rot, k_rot};
     return bsa_forward(args, workspace, workspace_bytes, stream, nullptr, &rope);
+}
+
+int mosaic_bsa_fwd_proj(const mosaic_bsa_args* args, const mosaic_proj_args* proj, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+    if (args == nullptr || proj == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    const mosaic_proj_args& j = *proj;
+    if (!j.x || !j.weight || !j.q || !j.k || !j.v) return MOSAIC_ERR_NULL_POINTER;
+    const bool local = args->mode == MOSAIC_BSA_LOCAL_ONLY;
+    if (!local && !j.weights) return MOSAIC_ERR_NULL_POINTER;
+    if ((j.rope_cos == nullptr) != (j.rope_sin == nullptr)) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(j.x) || !aligned16(j.weight) || !aligned16(j.q) || !aligned16(j.k) || !aligned16(j.v) ||
+        (j.rope_cos && (!aligned16(j.rope_cos) || !aligned16(j.rope_sin))) || j.x_stride_n % 8 || j.x_stride_b % 8)
+        return MOSAIC_ERR_ALIGNMENT;
+    const int32_t B = args->batch, N = args->seq_len, Hq = args->num_q_heads, Hk = args->num_kv_heads;
+    if (B <= 0 || N <= 0 || j.dim <= 0 || j.x_stride_n < 0 || j.x_stride_b < 0) return MOSAIC_ERR_SHAPE;
+    if (int e = check_heads(Hq, Hk)) return e;
+    if (args->head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
+    if (j.dim % 128 || N % 256 || (!local && 3 * Hq > 64)) return MOSAIC_ERR_UNSUPPORTED;
+    if (!local && args->sparse_block_size != 64 && args->sparse_block_size != 128) return MOSAIC_ERR_UNSUPPORTED;
+    const int groups = Hq + 2 * Hk + (local ? 0 : 1);
+    const int n_tiles = (groups + 3) / 4;
+    if (j.weight_rows != 256 * n_tiles) return MOSAIC_ERR_SHAPE;
+    // every row the kernel reads: x rows up to (N - 1, B - 1), weight rows up to weight_rows
+    if ((int64_t)(N - 1) * j.x_stride_n + (int64_t)(B - 1) * j.x_stride_b + j.dim >= ((int64_t)1 << 40))
+        return MOSAIC_ERR_SHAPE;
+    if (j.x_stride_n >= ((int64_t)1 << 27) || j.dim >= (1 << 27))
+        return MOSAIC_ERR_UNSUPPORTED;   // per-lane byte offsets within 8 rows are 32-bit
+    mosaic_bsa_args a = *args;
+    a.q = mosaic_bnhd{j.q, (int64_t)N * Hq * kHeadDim, (int64_t)Hq * kHeadDim, kHeadDim};
+    a.k = mosaic_bnhd{j.k, (int64_t)N * Hk * kHeadDim, (int64_t)Hk * kHeadDim, kHeadDim};
+    a.v = mosaic_bnhd{j.v, (int64_t)N * Hk * kHeadDim, (int64_t)Hk * kHeadDim, kHeadDim};
+    a.weights = local ? nullptr : j.weights;
+    a.w_stride_s = 1; a.w_stride_h = 3; a.w_stride_n = (int64_t)Hq * 3; a.w_stride_b = (int64_t)N * Hq * 3;
+    ProjParams p{};
+    p.x = static_cast<const bf16_t*>(j.x); p.x_sn = j.x_stride_n; p.x_sb = j.x_stride_b;
+    p.w = static_cast<const bf16_t*>(j.weight);
+    p.S = N; p.B = B; p.D = j.dim; p.Hq = Hq; p.Hk = Hk; p.gates = local ? 0 : 1; p.n_tiles = n_tiles;
+    p.rope_cos = j.rope_cos; p.rope_sin = j.rope_sin;
+    p.q = static_cast<bf16_t*>(j.q); p.k = static_cast<bf16_t*>(j.k); p.v = static_cast<bf16_t*>(j.v);
+    p.wts = static_cast<bf16_t*>(j.weights);
+    return bsa_forward(&a, workspace, workspace_bytes, stream, nullptr, nullptr, &p);
 }
 
 int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const int64_t* block_indices,

@@ -294,7 +294,28 @@ struct AttnParams {
     float scale_log2;        // softmax scale * log2(e)
 };
 
+// The attention block's input side (proj.hip): y = x W^T over the stacked q | k | v | gate
+// weights, RoPE of q and k, the gate softmax and the block pooling in one kernel.
+struct ProjParams {
+    const bf16_t* x; int64_t x_sn, x_sb;   // token n of member b at x + n x_sn + b x_sb (D contiguous)
+    const bf16_t* w;                       // [n_tiles * 256, D]: 64-row groups q heads | k | v | gates | zero
+    int S, B, D, Hq, Hk;
+    int gates;                             // a gate group follows the v heads (3 Hq <= 64 logits)
+    int n_tiles;                           // 256-column tiles of w
+    const float* rope_cos;                 // [S, 32] RoPE tables, or null (no rotation)
+    const float* rope_sin;
+    bf16_t* q; bf16_t* k; bf16_t* v;       // [B, S, H, 64] contiguous (q and k rotated)
+    bf16_t* wts;                           // [B, S, Hq, 3] branch weights (gates)
+    int bs;                                // pooled block size (64 or 128), 0: no pooling
+    int nb, nb_pad;
+    bf16_t* qc;                            // [B, nb, Hq, 64] pooled q
+    bf16_t* kfrag;                         // pooled k, operand order (kfrag_index), zero past nb
+    bf16_t* vfrag;                         // pooled v, operand order (vfrag_index), or null
+    float* kbnd;                           // [B, nb, Hk, 8] largest squared chunk norms, or null
+};
+
 // Host-side launchers (defined next to each kernel).
+hipError_t launch_proj(const ProjParams& p, hipStream_t s);
 hipError_t launch_pool(const PoolParams& p, hipStream_t s);
 hipError_t launch_cmp(const CmpParams& p, bool scores, bool attn, hipStream_t s);
 hipError_t launch_topk(const TopkParams& p, hipStream_t s);

@@ -27,7 +27,8 @@ from .ops import _as_bf16_bnhd, _check_gqa, bnhd, forward_only, mosaic_sparse_at
 
 __all__ = [
     "block_attention", "dense_attention", "pool_mean", "attn_topk", "mosaic_attn_func",
-    "mosaic_sparse_attn", "RoPE", "MosaicAttention",
+    "mosaic_attn_func_rope", "mosaic_attn_proj", "stack_projection_weight", "mosaic_sparse_attn", "RoPE",
+    "MosaicAttention",
 ]
 
 
@@ -178,6 +179,135 @@ def mosaic_attn_func_rope(q, k, v, weight_ba_cmp_slc, rope_cos, rope_sin, block_
     return res[0] if len(res) == 1 else res
 
 
+def stack_projection_weight(w_q, w_k, w_v, w_gate, num_q_heads, num_kv_heads):
+    """The stacked bf16 weight of ``mosaic_attn_proj``: the rows of to_q, to_k, to_v and (unless
+    None) to_strategy_combine_mlp at row offsets 0, 64 Hq, 64 (Hq + Hk) and 64 (Hq + 2 Hk), zero
+    rows up to a multiple of 256 (one 64-row group per head, then one for the gate logits)."""
+    groups = num_q_heads + 2 * num_kv_heads + (1 if w_gate is not None else 0)
+    rows = 256 * ((groups + 3) // 4)
+    dim = w_q.shape[1]
+    out = torch.zeros(rows, dim, dtype=torch.bfloat16, device=w_q.device)
+    r = 0
+    for w, n in ((w_q, 64 * num_q_heads), (w_k, 64 * num_kv_heads), (w_v, 64 * num_kv_heads)):
+        if tuple(w.shape) != (n, dim):
+            raise ValueError(f"projection weight shape {tuple(w.shape)} != ({n}, {dim})")
+        out[r:r + n] = w
+        r += n
+    if w_gate is not None:
+        if tuple(w_gate.shape) != (3 * num_q_heads, dim):
+            raise ValueError(f"gate weight shape {tuple(w_gate.shape)} != ({3 * num_q_heads}, {dim})")
+        out[r:r + 3 * num_q_heads] = w_gate
+    return out
+
+
+def _bsa_mode(block_attn_only, no_compression, sparse_block_count):
+    if block_attn_only:
+        return _lib.MODE_LOCAL_ONLY
+    if no_compression:
+        if sparse_block_count <= 0:
+            raise ValueError("no_compression needs sparse_block_count >= 1")
+        return _lib.MODE_NO_COMPRESSION
+    return _lib.MODE_NO_SELECTION if sparse_block_count == 0 else _lib.MODE_FULL
+
+
+def mosaic_attn_proj(x, weight, num_q_heads, num_kv_heads, block_attn_size, sparse_block_size, sparse_block_count,
+                     block_attn_only, no_compression=False, *, rope_cos=None, rope_sin=None,
+                     return_projections=False, return_block_indices=False, out=None):
+    """The attention block from its input rows: the q / k / v / gate projection
+    (primitives.py:182-195), RoPE of q and k (:125-135, :193-195), the gate softmax (:171-180)
+    and mosaic_attn_func (:54-89), with the projection, rotation, gate softmax and the block
+    pooling of q, k and v in one kernel (q, k and v are written once, not read back to pool).
+
+    x: sequence-first rows [S, B, dim] (the model's layout; bf16, or converted as autocast
+    would).  weight: ``stack_projection_weight(...)``.  ``rope_cos`` / ``rope_sin``: the RoPE
+    module's [S, 32] tables, or None.  Returns the op output [B, S, Hq, 64] (``out`` as for
+    ``mosaic_attn_func``), then with ``return_projections`` the rotated q, rotated k, v
+    ([B, S, H, 64]) and the branch weights [B, S, Hq, 3], then with ``return_block_indices``
+    the selected blocks.  Needs S % 256 == 0, dim % 128 == 0, sparse_block_size 64 or 128
+    (unless block_attn_only) and 3 Hq <= 64; ``ValueError`` otherwise.
+    """
+    forward_only("mosaic_attn_proj", x, weight)
+    if x.dim() != 3:
+        raise ValueError(f"x must be [S, B, dim], got shape {tuple(x.shape)}")
+    if x.device.type != "cuda":
+        raise ValueError(f"x must be on a ROCm device, got {x.device}")
+    S, B, dim = x.shape
+    Hq, Hk = num_q_heads, num_kv_heads
+    mode = _bsa_mode(block_attn_only, no_compression, sparse_block_count)
+    local = mode == _lib.MODE_LOCAL_ONLY
+    if S % 256 or dim % 128 or (not local and (sparse_block_size not in (64, 128) or 3 * Hq > 64)):
+        raise ValueError("mosaic_attn_proj needs S % 256 == 0, dim % 128 == 0, sparse_block_size 64 or 128 "
+                         "and 3 * num_q_heads <= 64")
+    dtype = x.dtype
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    if x.stride(2) != 1 or x.data_ptr() % 16 or x.stride(0) % 8 or x.stride(1) % 8:
+        x = x.contiguous()
+    groups = Hq + 2 * Hk + (0 if local else 1)
+    if weight.dtype != torch.bfloat16 or tuple(weight.shape) != (256 * ((groups + 3) // 4), dim):
+        raise ValueError("weight must be stack_projection_weight(...) for these heads (bf16 "
+                         f"[{256 * ((groups + 3) // 4)}, {dim}])")
+    weight = weight.contiguous()
+    dev = x.device
+    q = torch.empty(B, S, Hq, 64, dtype=torch.bfloat16, device=dev)
+    k = torch.empty(B, S, Hk, 64, dtype=torch.bfloat16, device=dev)
+    v = torch.empty_like(k)
+    w = None if local else torch.empty(B, S, Hq, 3, dtype=torch.bfloat16, device=dev)
+    rope = None
+    if (rope_cos is None) != (rope_sin is None):
+        raise ValueError("rope_cos and rope_sin go together")
+    if rope_cos is not None:
+        rope = tuple(t.to(device=dev, dtype=torch.float32).contiguous() for t in (rope_cos, rope_sin))
+        if any(tuple(t.shape) != (S, 32) for t in rope):
+            raise ValueError(f"RoPE tables must be [seq_len, 32] = [{S}, 32]")
+    selects = mode in (_lib.MODE_FULL, _lib.MODE_NO_COMPRESSION)
+    idx = None
+    if return_block_indices and selects:
+        idx = torch.empty(B, S // sparse_block_size, Hk, sparse_block_count, dtype=torch.int64, device=dev)
+    if out is None:
+        out = torch.empty(B, S, Hq, 64, dtype=torch.bfloat16, device=dev)
+    elif (tuple(out.shape) != (B, S, Hq, 64) or out.dtype != torch.bfloat16 or out.device != dev
+          or out.stride(3) != 1 or out.stride(2) != 64 or out.stride(0) % 8 or out.stride(1) % 8
+          or out.data_ptr() % 16):
+        raise ValueError("out must be a bf16 [B, N, Hq, 64] view with contiguous heads and 16-byte rows")
+    a = _lib.BsaArgs()
+    a.batch, a.seq_len, a.num_q_heads, a.num_kv_heads, a.head_dim = B, S, Hq, Hk, 64
+    a.block_attn_size, a.sparse_block_size, a.sparse_block_count = block_attn_size, sparse_block_size, sparse_block_count
+    a.mode, a.softmax_scale = mode, 0.0
+    a.out = out.data_ptr()
+    a.block_indices_out = idx.data_ptr() if idx is not None else None
+    a.out_stride_b, a.out_stride_n = out.stride(0), out.stride(1)
+    j = _lib.ProjArgs()
+    j.x, j.x_stride_n, j.x_stride_b, j.dim = x.data_ptr(), x.stride(0), x.stride(1), dim
+    j.weight_rows, j.weight = weight.shape[0], weight.data_ptr()
+    j.rope_cos = rope[0].data_ptr() if rope else None
+    j.rope_sin = rope[1].data_ptr() if rope else None
+    j.q, j.k, j.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    j.weights = w.data_ptr() if w is not None else None
+    # the op's workspace: the same as mosaic_bsa_fwd's for these shapes (q/k/v/weights stand-ins
+    # only carry shapes and strides for the size query)
+    qa = _lib.BsaArgs.from_buffer_copy(a)
+    qa.q = _lib.Bnhd(q.data_ptr(), q.stride(0), q.stride(1), q.stride(2))
+    qa.k = _lib.Bnhd(k.data_ptr(), k.stride(0), k.stride(1), k.stride(2))
+    qa.v = _lib.Bnhd(v.data_ptr(), v.stride(0), v.stride(1), v.stride(2))
+    if w is not None:
+        qa.weights = w.data_ptr()
+        qa.w_stride_s, qa.w_stride_b, qa.w_stride_n, qa.w_stride_h = 1, S * Hq * 3, Hq * 3, 3
+    L = _lib.lib()
+    nbytes = L.mosaic_bsa_workspace_size(ctypes.byref(qa))
+    if nbytes == 0 and not local:
+        _lib.check(L.mosaic_bsa_fwd_proj(ctypes.byref(a), ctypes.byref(j), None, 0, stream_of(x)), "mosaic_bsa_fwd_proj")
+    ws = _workspace(nbytes, dev) if nbytes else None
+    _lib.check(L.mosaic_bsa_fwd_proj(ctypes.byref(a), ctypes.byref(j), ws.data_ptr() if ws is not None else None,
+                                     ws.numel() if ws is not None else 0, stream_of(x)), "mosaic_bsa_fwd_proj")
+    res = (out.to(dtype),)
+    if return_projections:
+        res += (q, k, v, w)
+    if return_block_indices:
+        res += (idx,)
+    return res[0] if len(res) == 1 else res
+
+
 def _bsa_forward(q, k, v, weight_ba_cmp_slc, block_attn_size, sparse_block_size, sparse_block_count,
                  block_attn_only, no_compression, return_block_indices, rope, return_rotated=False, out=None):
     forward_only("mosaic_attn_func", q, k, v, weight_ba_cmp_slc, *(rope or ()))
@@ -313,25 +443,86 @@ class MosaicAttention(nn.Module):
             self._rope_shared = bool(torch.equal(tabs[0], tabs[2]) and torch.equal(tabs[1], tabs[3]))
         return self._rope_shared
 
-    def _projections(self, x):
-        """q, k, v and the gate logits from ONE GEMM over x: the four weights stacked (zero rows
-        pad the width to a multiple of 64, so every slice starts 16-byte aligned), instead of
-        four GEMMs that each read x (the gate projection alone, 36-60 outputs wide, ran ~10x
-        slower than its bytes allow as a separate skinny GEMM)."""
+    def _proj_modules(self):
         mods = [self.to_q, self.to_k, self.to_v]
         if not self.block_attn_only:
             mods.append(self.to_strategy_combine_mlp)
+        return mods
+
+    def _weights_key(self):
+        return tuple((m.weight.data_ptr(), m.weight._version, m.weight.dtype) for m in self._proj_modules())
+
+    def _projections(self, x):
+        """q, k, v and the gate logits from ONE GEMM over x: the four weights stacked, instead of
+        four GEMMs that each read x (the gate projection alone, 36-60 outputs wide, ran ~10x
+        slower than its bytes allow as a separate skinny GEMM).  Zero rows pad the width to a
+        multiple of 256 (of 64 below 512 outputs): every slice starts 16-byte aligned, and the
+        library GEMM runs its fast tiles (768 -> 1216 outputs took 2.79 ms on 1.18 M rows,
+        768 -> 1280 2.04 ms).  The stacked weight is built once per weight version (the op has
+        no backward, so it carries no graph)."""
+        mods = self._proj_modules()
         sizes = [m.out_features for m in mods]
-        pad = -sum(sizes) % 64
-        ws = [m.weight for m in mods]
-        if pad:
-            ws.append(ws[0].new_zeros(pad, ws[0].shape[1]))
-        y = torch.nn.functional.linear(x, torch.cat(ws, 0))
+        key = self._weights_key()
+        if getattr(self, "_cat_key", None) != key:
+            total = sum(sizes)
+            pad = -total % (256 if total >= 512 else 64)
+            with torch.no_grad():
+                ws = [m.weight for m in mods]
+                if pad:
+                    ws.append(ws[0].new_zeros(pad, ws[0].shape[1]))
+                self._cat_weight = torch.cat(ws, 0)
+            self._cat_key, self._cat_pad = key, pad
+        pad = self._cat_pad
+        y = torch.nn.functional.linear(x, self._cat_weight)
         parts = y.split(sizes + ([pad] if pad else []), dim=-1)
         return parts[0], parts[1], parts[2], (parts[3] if not self.block_attn_only else None)
 
+    def _stacked_weight(self):
+        """The bf16 weight of mosaic_attn_proj, built once per weight version."""
+        key = self._weights_key()
+        if getattr(self, "_stack_key", None) != key:
+            with torch.no_grad():
+                self._stack_weight = stack_projection_weight(
+                    self.to_q.weight, self.to_k.weight, self.to_v.weight,
+                    None if self.block_attn_only else self.to_strategy_combine_mlp.weight, self.q_heads, self.kv_heads)
+            self._stack_key = key
+        return self._stack_weight
+
+    # class-wide switch of the fused input side (mosaic_attn_proj); off, every call takes the
+    # library GEMM + pooling-pass path (for comparisons)
+    fused_input_side = True
+
+    def _fused_input_side(self, x):
+        """Whether mosaic_attn_proj can run this call: bf16 arithmetic (bf16 autocast, or bf16
+        input and weights), q and k rotated by equal tables (or no RoPE), and its shape limits."""
+        if not self.fused_input_side:
+            return False
+        if x.device.type != "cuda" or x.dim() != 3 or self.to_q.out_features != 64 * self.q_heads:
+            return False
+        bf16 = ((torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16)
+                or (x.dtype == torch.bfloat16 and self.to_q.weight.dtype == torch.bfloat16))
+        S_, _, dim = x.shape
+        if not bf16 or S_ % 256 or dim % 128:
+            return False
+        if not self.block_attn_only and (self.sparse_block_size not in (64, 128) or 3 * self.q_heads > 64):
+            return False
+        return self.q_rope is None or self._shared_rope_tables()
+
     def forward(self, x):
         S_, B_ = x.shape[:2]
+        forward_only("MosaicAttention", x, *self.parameters())
+        if self._fused_input_side(x):
+            # projection, RoPE, gate softmax and pooling in one kernel, then the op
+            o = torch.empty(S_, B_, 64 * self.q_heads, dtype=torch.bfloat16, device=x.device)
+            o_view = o.view(S_, B_, self.q_heads, -1).transpose(0, 1)
+            record = self.record_block_indices is not None
+            rope = {} if self.q_rope is None else dict(rope_cos=self.q_rope.cos_freqs, rope_sin=self.q_rope.sin_freqs)
+            res = mosaic_attn_proj(x, self._stacked_weight(), self.q_heads, self.kv_heads, self.block_attn_size,
+                                   self.sparse_block_size, self.sparse_block_count, self.block_attn_only,
+                                   self.no_compression, out=o_view, return_block_indices=record, **rope)
+            if record:
+                self.record_block_indices.append(res[1])
+            return self.to_o(o)
         q, k, v, logits = self._projections(x)
         q = q.unflatten(-1, (self.q_heads, -1)).transpose(0, 1)
         k = k.unflatten(-1, (self.kv_heads, -1)).transpose(0, 1)

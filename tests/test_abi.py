@@ -120,6 +120,44 @@ def test_fused_rope_entry_validates():
     assert L.mosaic_bsa_fwd_rope(ctypes.byref(a), FAKE, FAKE, FAKE, FAKE, None, 0, None) == 6
 
 
+def _proj(**kw):
+    j = _lib.ProjArgs()
+    j.x, j.x_stride_n, j.x_stride_b, j.dim = FAKE, 768, 768, 768
+    # groups 20 + 10 + 1 = 31: eight 256-row tiles
+    j.weight_rows, j.weight = 2048, FAKE
+    j.q, j.k, j.v, j.weights = FAKE, FAKE, FAKE, FAKE
+    for key, val in kw.items():
+        setattr(j, key, val)
+    return j
+
+
+@pytest.mark.parametrize("args_change,proj_change,status", [
+    ({}, dict(x=None), 1),
+    ({}, dict(weights=None), 1),
+    ({}, dict(rope_cos=FAKE), 1),                       # cos without sin
+    ({}, dict(v=FAKE + 2), 7),
+    ({}, dict(x_stride_b=770), 7),
+    ({}, dict(dim=704), 11),                            # not a multiple of 128
+    (dict(seq_len=3072 + 64 * 5), {}, 11),              # not a multiple of 256 (valid for the op)
+    (dict(sparse_block_size=256), {}, 11),
+    ({}, dict(weight_rows=1792), 8),
+    (dict(head_dim=32), {}, 2),
+    (dict(num_q_heads=21), {}, 3),
+    (dict(num_q_heads=25, num_kv_heads=25), dict(weight_rows=256 * 19), 11),   # 3 Hq > 64 gate logits
+])
+def test_fused_projection_entry_validates(args_change, proj_change, status):
+    L = _lib.lib()
+    a = _args(**args_change)
+    assert L.mosaic_bsa_fwd_proj(ctypes.byref(a), ctypes.byref(_proj(**proj_change)), FAKE, 1 << 30, None) == status
+
+
+def test_fused_projection_local_only_needs_no_weights_output():
+    L = _lib.lib()
+    a = _args(mode=_lib.MODE_LOCAL_ONLY, weights=None)
+    # local only: groups 20 + 10 = 30 -> eight tiles; a wrong size is reported, not the missing gates
+    assert L.mosaic_bsa_fwd_proj(ctypes.byref(a), ctypes.byref(_proj(weights=None, weight_rows=256)), None, 0, None) == 8
+
+
 def test_other_entry_points_validate():
     L = _lib.lib()
     t = _lib.Bnhd(FAKE, 0, 64 * 4, 64)
