@@ -276,12 +276,12 @@ def unet_leg(args, dev):
     itself): input [1, 1, 2, 240, 121, 82] fp32 N(0,1) on the 1.5-degree lat-lon grid, 3 static
     fields, ``--unet-members`` noise samples (ensemble members), bf16 autocast, no grad.  Every
     attention layer runs the block-sparse op (local 1024, sparse blocks 128, top-24/12/4) behind
-    the fused input side (q / k / v / gate projection with RoPE, gate softmax and pooling in one
-    kernel; ``--unet-unfused-input-side`` takes the library GEMM + pooling-pass path instead),
-    both grid interpolations the k-NN kernel; the other projections are library GEMMs."""
+    one library GEMM for the q / k / v / gate projection and the op's pooling pass with RoPE
+    (``--unet-fused-input-side`` takes the fused projection kernel instead), both grid
+    interpolations the k-NN kernel; the other projections are library GEMMs."""
     from mosaic_amd.model import Transformer, era5_config, model_flops
     from mosaic_amd.primitives import MosaicAttention
-    MosaicAttention.fused_input_side = not args.unet_unfused_input_side
+    MosaicAttention.fused_input_side = args.unet_fused_input_side
     cfg = era5_config()
     torch.manual_seed(args.seed)
     t0 = time.perf_counter()
@@ -320,7 +320,7 @@ def unet_leg(args, dev):
             "flops": fl, "params": sum(p.numel() for p in model.parameters()),
             "output_shape": list(out.shape), "output_finite": bool(torch.isfinite(out).all().item()),
             "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 1e9, 1), "setup_s": round(setup_s, 1),
-            "input_side": "unfused" if args.unet_unfused_input_side else "fused",
+            "input_side": "fused" if args.unet_fused_input_side else "unfused",
             "data": "synthetic N(0,1) input and static fields, random-init weights (no checkpoint offline)"}
 
 
@@ -423,8 +423,8 @@ def main():
     ap.add_argument("--unet-members", type=int, default=24)
     ap.add_argument("--unet-steps", type=int, default=3)
     ap.add_argument("--unet-warmup", type=int, default=1)
-    ap.add_argument("--unet-unfused-input-side", action="store_true",
-                    help="U-Net attention blocks take the library GEMM + pooling-pass path")
+    ap.add_argument("--unet-fused-input-side", action="store_true",
+                    help="U-Net attention blocks take the fused projection kernel (mosaic_attn_proj)")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")

@@ -196,6 +196,7 @@ def test_mosaic_attention_fused_matches_unfused():
                           gqa_ratio=4, dim=768, qkv_compress_ratio=1, rope=True, rope_theta=10000)
     torch.manual_seed(0)
     m = MosaicAttention(cfg, block_attn_only=False).to(DEV)
+    m.fused_input_side = True
     S, B = 3072, 3
     cos, sin = tables(S, 16)
     m.q_rope.register_buffer("cos_freqs", cos.to(DEV))
@@ -218,6 +219,7 @@ def test_fused_path_refuses_grad():
     cfg = SimpleNamespace(block_attn_size=256, sparse_block_size=64, sparse_block_count=2, num_heads=4,
                           gqa_ratio=4, dim=256, qkv_compress_ratio=1, rope=False, rope_theta=10000)
     m = MosaicAttention(cfg, block_attn_only=False).to(DEV)
+    m.fused_input_side = True
     x = torch.randn(256, 1, 256, device=DEV)
     with torch.autocast(DEV, dtype=torch.bfloat16):
         assert m._fused_input_side(x)
