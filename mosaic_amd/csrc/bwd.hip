@@ -524,23 +524,35 @@ void bwd_dkv_kernel(BwdParams p) {
     // buffers; with no steps the K / V loads may still be in flight, so wait for them first)
     wait_vmem();
     __syncthreads();
-    float* red = reinterpret_cast<float*>((kh == 0 ? ring0 : ring1) + hh * kTileElems) + r * 64;
+    // value v of lane r at v * 32 + r: consecutive lanes on consecutive banks
+    float* red = reinterpret_cast<float*>((kh == 0 ? ring0 : ring1) + hh * kTileElems) + r;
     if (qh == 1) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            red[e] = dkT[0][e]; red[16 + e] = dkT[1][e]; red[32 + e] = dvT[0][e]; red[48 + e] = dvT[1][e];
+            red[32 * e] = dkT[0][e];
+            red[32 * (16 + e)] = dkT[1][e];
+            red[32 * (32 + e)] = dvT[0][e];
+            red[32 * (48 + e)] = dvT[1][e];
         }
     }
     __syncthreads();
     if (qh == 0) {
         const int64_t base = (((int64_t)b * p.N + key0 + 32 * kh + r) * p.Hk + c) * 64;
+        // registers 4 g .. 4 g + 3 hold dims 32 dblk + 8 g + 4 hh + 0..3: one 8-byte store each
 #pragma unroll
         for (int dblk = 0; dblk < 2; ++dblk) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int d = 32 * dblk + 8 * (e >> 2) + 4 * hh + (e & 3);
-                p.dk[base + d] = (bf16_t)(pack_bf16x2(dkT[dblk][e] + red[16 * dblk + e], 0.f) & 0xffffu);
-                p.dv[base + d] = (bf16_t)(pack_bf16x2(dvT[dblk][e] + red[32 + 16 * dblk + e], 0.f) & 0xffffu);
+            for (int g = 0; g < 4; ++g) {
+                float kx[4], vx[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int e = 4 * g + i;
+                    kx[i] = dkT[dblk][e] + red[32 * (16 * dblk + e)];
+                    vx[i] = dvT[dblk][e] + red[32 * (32 + 16 * dblk + e)];
+                }
+                const int d = 32 * dblk + 8 * g + 4 * hh;
+                *reinterpret_cast<uint2*>(p.dk + base + d) = make_uint2(pack_bf16x2(kx[0], kx[1]), pack_bf16x2(kx[2], kx[3]));
+                *reinterpret_cast<uint2*>(p.dv + base + d) = make_uint2(pack_bf16x2(vx[0], vx[1]), pack_bf16x2(vx[2], vx[3]));
             }
         }
     }
