@@ -50,34 +50,6 @@ struct BwdParams {
     float scale;
 };
 
-__device__ __forceinline__ void unpack8(const uint4& u, float f[8]) {
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { f[2 * i] = bf_lo(w[i]); f[2 * i + 1] = bf_hi(w[i]); }
-}
-// ------------------------------------------------------------------ delta
-__global__ __launch_bounds__(256) void bwd_delta_kernel(BwdParams p) {
-    // one wave per 8 (b, n, h) rows; lane l: row l / 8, dims 8 (l % 8) .. +7
-    const int64_t rows = (int64_t)p.B * p.N * p.Hq;
-    const int lane = threadIdx.x & 63;
-    const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
-    if (row >= rows) return;
-    const int h = (int)(row % p.Hq);
-    const int64_t bn = row / p.Hq;
-    const int n = (int)(bn % p.N), b = (int)(bn / p.N);
-    const int c8 = (lane & 7) * 8;
-    float o[8], g[8];
-    unpack8(ld16(p.o + row * 64 + c8), o);
-    unpack8(ld16(p.go + (int64_t)b * p.go_sb + (int64_t)n * p.go_sn + (int64_t)h * p.go_sh + c8), g);
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s += round_bf16(o[e] * g[e]);
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
-    if ((lane & 7) == 0) p.delta[row] = round_bf16(s);
-}
-
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ grad q
@@ -175,23 +147,41 @@ void bwd_dq_kernel(BwdParams p, int head_groups, int total_wgs) {
         }
         if (lane == 0) sel_count = count;
     }
-    // this wave's rows: q' = bf16((q scale) log2 e) and do as MFMA B fragments, lse and delta
+    // this wave's rows: q' = bf16((q scale) log2 e) and do as MFMA B fragments, lse, and
+    // delta = bf16(sum_d bf16(o do)) formed here from o rows loaded in the fragments' layout
+    // (each lane sums its 32 dims in fp32, the two lane halves add once) and written for the
+    // grad-k/v kernel
     bf16x8 qf[2][4], gf[2][4];
     float lse[2], dlt[2];
     {
         const bf16_t* qb = p.q + (int64_t)b * p.q_sb + (int64_t)j * p.q_sh;
         const bf16_t* gb = p.go + (int64_t)b * p.go_sb + (int64_t)j * p.go_sh;
+        const bf16_t* ob = p.o + ((int64_t)b * p.N * p.Hq + j) * 64;
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
             const int n = n0 + 32 * qt + r;
+            uint4 ov[4];
 #pragma unroll
             for (int ds = 0; ds < 4; ++ds) {
                 qf[qt][ds] = as_bf16x8(ld16(qb + (int64_t)n * p.q_sn + 16 * ds + 8 * hh));
                 gf[qt][ds] = as_bf16x8(ld16(gb + (int64_t)n * p.go_sn + 16 * ds + 8 * hh));
+                ov[ds] = ld16(ob + (int64_t)n * p.Hq * 64 + 16 * ds + 8 * hh);
             }
             const int64_t row = ((int64_t)b * p.N + n) * p.Hq + j;
             lse[qt] = p.lse[row];
-            dlt[qt] = p.delta[row];
+            float sum = 0.f;
+#pragma unroll
+            for (int ds = 0; ds < 4; ++ds) {
+                const uint4 gv = __builtin_bit_cast(uint4, gf[qt][ds]);
+                const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, ow[4] = {ov[ds].x, ov[ds].y, ov[ds].z, ov[ds].w};
+#pragma unroll
+                for (int mm = 0; mm < 4; ++mm) {
+                    sum += round_bf16(bf_lo(ow[mm]) * bf_lo(gw[mm]));
+                    sum += round_bf16(bf_hi(ow[mm]) * bf_hi(gw[mm]));
+                }
+            }
+            dlt[qt] = round_bf16(xor32_add(sum));
+            if (hh == 0) p.delta[row] = dlt[qt];
         }
         // q' for the grad-k/v kernel (the rows this lane holds: query 32 qt + r, dims 16 ds + 8 hh)
         bf16_t* qsb = p.qs + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
@@ -619,12 +609,9 @@ int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const vo
     p.scale = softmax_scale > 0.f ? softmax_scale : 0.125f;   // head_dim^-0.5 for head_dim 64
     hipStream_t s = static_cast<hipStream_t>(stream);
     void* args[] = {&p};
-    const int64_t rows = (int64_t)batch * seq_len * num_q_heads;
-    const int64_t dgrid = (rows + 31) / 32;
-    if (dgrid > 0x7fffffff) return MOSAIC_ERR_SHAPE;
-    if (hipLaunchKernel((const void*)&bwd_delta_kernel, dim3((unsigned)dgrid), dim3(256), args, 0, s) != hipSuccess)
-        return MOSAIC_ERR_LAUNCH;
-    // grad q: one workgroup per (batch, kv head, query tile, group of NW query heads)
+    // grad q: one workgroup per (batch, kv head, query tile, group of NW query heads); it also
+    // writes delta and q' for grad k/v
+    if ((int64_t)batch * seq_len * num_q_heads >= ((int64_t)1 << 40)) return MOSAIC_ERR_SHAPE;
     const int G = num_q_heads / num_kv_heads;
     const int nw = (G == 1 || G == 2 || G == 4) ? G : (G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1));
     int head_groups = G / nw;

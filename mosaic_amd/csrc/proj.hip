@@ -90,9 +90,11 @@ __device__ __forceinline__ int group_role(const ProjParams& p, int g, int& head)
 }
 
 // staging layout of a wave's 128 x 64 result (128 rows x 128 bytes): 16-byte chunk c of row r
-// at position c ^ (4 (r & 1)), so the pair writes of rows r and r + 1 fall on disjoint banks
+// at position c ^ (4 ((r / 4) % 2)).  A pair-write instruction covers 64 bytes of each of the
+// rows r, r + 1, r + 4, r + 5; rows of one parity share a 128-byte half of the 64 banks, and
+// r and r + 4 take opposite 64-byte quarters of it
 __device__ __forceinline__ int stage_off(int row, int col) {
-    return row * 64 + 8 * ((col >> 3) ^ (4 * (row & 1))) + (col & 7);
+    return row * 64 + 8 * ((col >> 3) ^ (4 * ((row >> 2) & 1))) + (col & 7);
 }
 
 __global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
@@ -115,8 +117,11 @@ void proj_kernel(ProjParams p) {
 
     // direct-to-LDS loads of a slot (rows of 32 k = 64 bytes): wave w fills rows 32 w .. + 31 of
     // both operands, sixteen rows (1 KB) per instruction; lane l lands at row 16 i + l / 4,
-    // position l % 4, and fetches the row's chunk (l % 4) ^ ((row / 2) % 4)
-    const int r16 = lane >> 2, gch = (lane & 3) ^ ((lane >> 3) & 3);
+    // position l % 4, and fetches the row's chunk (l % 4) ^ ((row / 4) % 4).  A 16-byte LDS
+    // read serves 16 lanes per cycle from 64 banks (256 bytes): the 16 consecutive rows of one
+    // read then cover the four 64-byte quarters of the banks (row % 4) with four distinct
+    // chunk positions each ((row / 4) % 4), so no two lanes share a bank.
+    const int r16 = lane >> 2, gch = (lane & 3) ^ ((lane >> 4) & 3);
     // uniform bases (scalar registers) plus one 32-bit byte offset per lane and operand
     const char* xbase = reinterpret_cast<const char*>(p.x + (int64_t)(s0 + 32 * w) * p.x_sn + (int64_t)b * p.x_sb);
     const char* wbase = reinterpret_cast<const char*>(p.w + (int64_t)(n0 + 32 * w) * p.D);
@@ -135,7 +140,7 @@ void proj_kernel(ProjParams p) {
     // operand reads: row 32 t + lane % 32 of a 32-row block, chunk 2 kk + lane / 32 (kk = 0, 1)
     int rd[2];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) rd[kk] = (lane & 31) * kProjK + 8 * ((2 * kk + (lane >> 5)) ^ ((lane >> 1) & 3));
+    for (int kk = 0; kk < 2; ++kk) rd[kk] = (lane & 31) * kProjK + 8 * ((2 * kk + (lane >> 5)) ^ ((lane >> 2) & 3));
 
     f32x16 acc[4][2];
 #pragma unroll
