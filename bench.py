@@ -302,18 +302,27 @@ def bwd_leg(L, q, k, v, wl, args, dev, stream):
     for _ in range(3):
         mosaic_attn_bwd(q, k, v, o, lse, do, 0.125, idx, bs)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n = max(5, args.steps // 10)
-    e0.record(stream)
-    for _ in range(n):
+    # settle as the forward does, then a HIP event before each of n calls and after the last
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min(args.settle_s, 0.5):
+        for _ in range(10):
+            mosaic_attn_bwd(q, k, v, o, lse, do, 0.125, idx, bs)
+        torch.cuda.synchronize()
+    n = max(20, args.steps // 5)
+    ev = HipEvents(n + 1)
+    sp = stream.cuda_stream
+    for i in range(n):
+        ev.record(i, sp)
         mosaic_attn_bwd(q, k, v, o, lse, do, 0.125, idx, bs)
-    e1.record(stream)
+    ev.record(n, sp)
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / n
+    ms = statistics.median(ev.ms(i, i + 1) for i in range(n))
+    ev.close()
     units = B * Hq * (N // 64) * (K * bs // 64)
     flops = units * 7 * 2 * 64 ** 3
     return {"ms": round(ms, 4), "flops": flops, "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
-            "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "calls": n}
+            "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "calls": n,
+            "timing": "median of per-call HIP event intervals after a settle of up to 0.5 s"}
 
 
 def unet_leg(args, dev):

@@ -218,8 +218,9 @@ MOSAIC_API int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd 
  * writes grad_q (bf16 [B, N, Hq, 64]), grad_k and grad_v (bf16 [B, N, Hk, 64]), all
  * contiguous.  Keys that no query block selected get zero gradients.  block_indices as for
  * mosaic_sparse_attn_fwd (entries outside [0, N/bs) are skipped); N / block_size <= 4096.
- * workspace: mosaic_sparse_attn_bwd_workspace_size() bytes (the per-row delta = o . do and
- * the pre-scaled q' = bf16((q * scale) * log2 e) the two gradient kernels share).
+ * workspace: mosaic_sparse_attn_bwd_workspace_size() bytes (the per-row -lse and
+ * -delta = -(o . do) and the pre-scaled q' = bf16((q * scale) * log2 e) the two gradient
+ * kernels share).
  */
 MOSAIC_API size_t mosaic_sparse_attn_bwd_workspace_size(int32_t batch, int32_t seq_len, int32_t num_q_heads);
 MOSAIC_API int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const void* out,

@@ -41,7 +41,8 @@ struct BwdParams {
     const bf16_t* go; int64_t go_sb, go_sn, go_sh;
     const bf16_t* o;        // forward output [B, N, Hq, 64] contiguous
     const float* lse;       // [B, N, Hq] base-2 log-sum-exp of the scaled logits
-    float* delta;           // [B, N, Hq] (workspace)
+    float* nlse;            // [B, N, Hq] -lse (workspace), written by the grad-q kernel
+    float* ndelta;          // [B, N, Hq] -delta (workspace), written by the grad-q kernel
     bf16_t* qs;             // q' = bf16((q scale) log2 e), [B, N, Hq, 64] contiguous (workspace):
                             // written by the grad-q kernel, read by the grad-k/v kernel
     const int64_t* idx;     // [B, nb, Hk, K]
@@ -108,6 +109,28 @@ __device__ __forceinline__ void tile_dma(const uint32_t* dk, const uint32_t* dv,
         __builtin_amdgcn_global_load_lds(vt + dv[i], (lds_void*)(Vd + row0 * 64), 16, 0, 0);
     }
 }
+
+// Direct-to-LDS loads issued as inline assembly, address = base (uniform) + voff (per lane),
+// LDS destination M0 + 16 l (dwordx4) or M0 + 4 l (dword) for lane l.  The compiler's wait
+// insertion does not see them: across the joins of a ring loop its tracking of which LDS
+// object a direct-to-LDS load writes becomes conservative, and it waited for the loads just
+// requested for a later step before the current step's LDS reads.  The caller waits for these
+// loads (s_waitcnt vmcnt) and synchronises the workgroup itself.  M0 is declared clobbered;
+// the compiler sets M0 again before each of its own uses, so nothing it holds is lost.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
+}
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 template <int NW>
 __global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(1, 1)))
@@ -181,7 +204,10 @@ void bwd_dq_kernel(BwdParams p, int head_groups, int total_wgs) {
                 }
             }
             dlt[qt] = round_bf16(xor32_add(sum));
-            if (hh == 0) p.delta[row] = dlt[qt];
+            if (hh == 0) {   // negated for the grad-k/v kernel's accumulator start values
+                p.nlse[row] = -lse[qt];
+                p.ndelta[row] = -dlt[qt];
+            }
         }
         // q' for the grad-k/v kernel (the rows this lane holds: query 32 qt + r, dims 16 ds + 8 hh)
         bf16_t* qsb = p.qs + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
@@ -327,7 +353,10 @@ void bwd_dq_kernel(BwdParams p, int head_groups, int total_wgs) {
 // layout (lane: one key column, 16 query rows) is exactly the MFMA B operand of
 // dV^T += do^T P and dK^T += q'^T dS with k running over those query rows; the A operands
 // (do^T, q'^T) come from transposing LDS reads of the row-major tiles in the same row order.
-// The step's q' rows (pre-scaled by the grad-q kernel), do rows, lse and delta go from global
+// The wave's K and V rows stay in registers for all steps.  S and dP accumulate onto -lse and
+// -delta of their rows (written by the grad-q kernel), so P = exp2(S) and dS = P dP ln2 take
+// no subtraction (the subtraction happens inside the fp32 accumulation instead of after it).
+// The step's q' rows (pre-scaled by the grad-q kernel), do rows, -lse and -delta go from global
 // memory straight into LDS: a ring of three slots, loads requested two steps ahead, one barrier
 // per step.  All tiles use the bwd_swz layout.  The two waves of a key half sum their partial
 // dV^T / dK^T once, at the end.
@@ -336,11 +365,11 @@ void bwd_dkv_kernel(BwdParams p) {
     __shared__ __attribute__((aligned(1024))) bf16_t kvs[2 * kTileElems];   // K tile, V tile
     bf16_t* Ks = kvs;
     bf16_t* Vs = kvs + kTileElems;
-    // Three steps in a ring; a slot holds the step's q' tile, do tile, then lse and delta of its
-    // 64 rows (fp32).  Each slot is an array of its own and the loop below is unrolled over
-    // the slots, so the compiler sees that a step's LDS reads and the loads in flight into the
-    // other slots touch different objects and does not wait for those loads before the reads.
-    // The final reduction reuses slots 0 and 1.
+    // Three steps in a ring; a slot holds the step's q' tile, do tile, then -lse and -delta of
+    // its 64 rows (fp32).  The loop below is unrolled over the slots (each an array of its own)
+    // and its loads are issued as inline assembly, so no compiler-inserted wait holds a step's
+    // LDS reads until the loads in flight into the other slots land.  The final reduction
+    // reuses slots 0 and 1.
     constexpr int kSlotElems = 2 * kTileElems + 256;
     __shared__ __attribute__((aligned(1024))) bf16_t ring0[kSlotElems], ring1[kSlotElems], ring2[kSlotElems];
     __shared__ uint64_t mark[kMaxBwdBlocks / 64];   // bit t: query block t selected this block
@@ -352,8 +381,16 @@ void bwd_dkv_kernel(BwdParams p) {
     // K and V of the key tile
     uint32_t dk[2], dv[2];
     tile_dma_init<4>(dk, dv, w, lane, p.k_sn, p.v_sn);
-    tile_dma<4>(dk, dv, p.k + (int64_t)b * p.k_sb + (int64_t)c * p.k_sh, p.v + (int64_t)b * p.v_sb + (int64_t)c * p.v_sh,
-                p.k_sn, p.v_sn, key0, Ks, Vs, w);
+    {
+        const bf16_t* kt = p.k + (int64_t)b * p.k_sb + (int64_t)c * p.k_sh + (int64_t)key0 * p.k_sn;
+        const bf16_t* vt = p.v + (int64_t)b * p.v_sb + (int64_t)c * p.v_sh + (int64_t)key0 * p.v_sn;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row0 = 8 * (2 * w + i);
+            dma16(kt, dk[i], lds_addr(Ks + row0 * 64));
+            dma16(vt, dv[i], lds_addr(Vs + row0 * 64));
+        }
+    }
     // query blocks whose selection row (kv head c) holds block u, as a bitmap: lane l of a wave
     // scans row 64 i + l (eight entries per step, all loads of a step issued before any
     // compare) and the wave's ballot is word i
@@ -402,21 +439,29 @@ void bwd_dkv_kernel(BwdParams p) {
     uint32_t dq_[2], dg_[2];
     tile_dma_init<4>(dq_, dg_, w, lane, (int64_t)p.Hq * 64, p.go_sn);
     // one step's loads: every wave issues exactly six direct-to-LDS instructions (two 1 KB runs
-    // each of q' and do, and lse / delta of 16 rows), so a wait for all but the newest step's
-    // loads is one fixed s_waitcnt.  Past the last step it loads query rows 0..63 into the free
-    // slot (never read), so that no branch depends on the step count.
-    auto issue_step = [&](bf16_t* slot) __attribute__((always_inline)) {
+    // each of q' and do, and -lse / -delta of 16 rows), so a wait for all but the newest step's
+    // loads is one fixed s_waitcnt.  Past the last step, and for the virtual steps before the
+    // first, it loads query rows 0..63 into the free slot (never read), so that no branch
+    // depends on the step count.
+    auto issue_step = [&](bf16_t* slot, bool real) __attribute__((always_inline)) {
         bf16_t* Qd = slot;
         bf16_t* Gd = slot + kTileElems;
         float* ld = reinterpret_cast<float*>(slot + 2 * kTileElems);
-        const int n0 = t < p.nb ? t * p.bs + 64 * tt : 0;
+        const int n0 = __builtin_amdgcn_readfirstlane(real && t < p.nb ? t * p.bs + 64 * tt : 0);
         const int j = c * p.G + g;
-        tile_dma<4>(dq_, dg_, p.qs + ((int64_t)b * p.N * p.Hq + j) * 64, p.go + (int64_t)b * p.go_sb + (int64_t)j * p.go_sh,
-                    (int64_t)p.Hq * 64, p.go_sn, n0, Qd, Gd, w);
-        const int64_t row = ((int64_t)b * p.N + n0 + 16 * w + (lane & 15)) * p.Hq + j;
+        const bf16_t* qt = p.qs + ((int64_t)b * p.N * p.Hq + j) * 64 + (int64_t)n0 * p.Hq * 64;
+        const bf16_t* gt = p.go + (int64_t)b * p.go_sb + (int64_t)j * p.go_sh + (int64_t)n0 * p.go_sn;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row0 = 8 * (2 * w + i);
+            dma16(qt, dq_[i], lds_addr(Qd + row0 * 64));
+            dma16(gt, dg_[i], lds_addr(Gd + row0 * 64));
+        }
+        const int64_t row0 = ((int64_t)b * p.N + n0 + 16 * w) * p.Hq + j;
         if (lane < 16) {   // lane l -> 4 bytes at 4 l of this wave's 16 rows
-            __builtin_amdgcn_global_load_lds(p.lse + row, (lds_void*)(ld + 16 * w), 4, 0, 0);
-            __builtin_amdgcn_global_load_lds(p.delta + row, (lds_void*)(ld + 64 + 16 * w), 4, 0, 0);
+            const uint32_t off = 4u * (uint32_t)(lane * p.Hq);
+            dma4(p.nlse + row0, off, lds_addr(ld + 16 * w));
+            dma4(p.ndelta + row0, off, lds_addr(ld + 64 + 16 * w));
         }
     };
     // per-lane LDS element offsets: row reads (row 32 h + r, chunk 2 kk + hh) and transposing
@@ -443,37 +488,36 @@ void bwd_dkv_kernel(BwdParams p) {
                                                        (__attribute__((address_space(3))) v4i16*)(tp + tr[dt][1])));
         return as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
     };
+    bf16x8 kf[4], vf[4];   // this wave's K and V rows (key half kh), constant over the steps
     auto step = [&](const bf16_t* slot) __attribute__((always_inline)) {
         const bf16_t* Qc = slot;
         const bf16_t* Gc = slot + kTileElems;
         const float* lc = reinterpret_cast<const float*>(slot + 2 * kTileElems);
         const float* dc = lc + 64;
+        // S and dP start from -lse and -delta of their rows (accumulator element 4 g4 + i is
+        // row 32 qh + 8 g4 + 4 hh + i): one 16-byte read each, and the products add to them
         f32x16 s, dp;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) { s[e] = 0.f; dp[e] = 0.f; }
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const float4 l4 = *reinterpret_cast<const float4*>(lc + 32 * qh + 8 * g4 + 4 * hh);
+            const float4 d4 = *reinterpret_cast<const float4*>(dc + 32 * qh + 8 * g4 + 4 * hh);
+            s[4 * g4 + 0] = l4.x; s[4 * g4 + 1] = l4.y; s[4 * g4 + 2] = l4.z; s[4 * g4 + 3] = l4.w;
+            dp[4 * g4 + 0] = d4.x; dp[4 * g4 + 1] = d4.y; dp[4 * g4 + 2] = d4.z; dp[4 * g4 + 3] = d4.w;
+        }
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const bf16x8 qa = as_bf16x8(*reinterpret_cast<const uint4*>(Qc + 32 * qh * 64 + rd[kk]));
-            const bf16x8 kb = as_bf16x8(*reinterpret_cast<const uint4*>(Ks + 32 * kh * 64 + rd[kk]));
             const bf16x8 ga = as_bf16x8(*reinterpret_cast<const uint4*>(Gc + 32 * qh * 64 + rd[kk]));
-            const bf16x8 vb = as_bf16x8(*reinterpret_cast<const uint4*>(Vs + 32 * kh * 64 + rd[kk]));
-            s = mfma32(qa, kb, s);     // S: queries x keys
-            dp = mfma32(ga, vb, dp);   // dP
+            s = mfma32(qa, kf[kk], s);     // S: queries x keys
+            dp = mfma32(ga, vf[kk], dp);   // dP
         }
         bf16x8 pb[2], db[2];
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {   // rows 32 qh + 8 g4 + 4 hh + 0..3: one 16-byte read each
-            const float4 l4 = *reinterpret_cast<const float4*>(lc + 32 * qh + 8 * g4 + 4 * hh);
-            const float4 d4 = *reinterpret_cast<const float4*>(dc + 32 * qh + 8 * g4 + 4 * hh);
-            const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = 4 * g4 + i;
-                const float pr = __builtin_amdgcn_exp2f(s[e] - lv[i]);
-                const float ds = pr * (dp[e] - dv4[i]) * kLn2;
-                pb[e >> 3][e & 7] = (__bf16)pr;
-                db[e >> 3][e & 7] = (__bf16)ds;
-            }
+        for (int e = 0; e < 16; ++e) {   // s = q'.k - lse, dp = do.v - delta
+            const float pr = __builtin_amdgcn_exp2f(s[e]);
+            const float ds = pr * dp[e] * kLn2;
+            pb[e >> 3][e & 7] = (__bf16)pr;
+            db[e >> 3][e & 7] = (__bf16)ds;
         }
 #pragma unroll
         for (int dblk = 0; dblk < 2; ++dblk) {
@@ -489,26 +533,37 @@ void bwd_dkv_kernel(BwdParams p) {
     int marked = 0;
     for (int i = 0; i < (p.nb + 63) / 64; ++i) marked += __builtin_popcountll(mark[i]);
     const int steps = marked * tiles * p.G;
-    issue_step(ring0);
-    advance();
-    issue_step(ring1);
-    advance();
-    // Step i uses ring slot i % 3.  Its loads were requested two steps earlier; wait for them,
-    // leaving the next step's six in flight, and the barrier publishes every wave's loads (the
-    // first time also K and V) and frees slot (i + 2) % 3, whose step is requested right away.
-    auto ring_step = [&](const bf16_t* cur, bf16_t* next) __attribute__((always_inline)) {
+    // The loop below runs whole rounds of three steps with one exit.  pad = 0..2 virtual steps
+    // come first (their slots get the rows past the end like the steps after the last one, and
+    // their products are skipped), so real step k uses slot (k + pad) % 3.
+    const int pad = (3 - steps % 3) % 3;
+    issue_step(ring0, pad == 0);
+    if (pad == 0) advance();
+    issue_step(ring1, pad <= 1);
+    if (pad <= 1) advance();
+    // K and V were requested before the two steps' twelve loads; every wave's K / V rows are in
+    // LDS after the barrier, and this wave's half goes to registers
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    lds_barrier();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        kf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(Ks + 32 * kh * 64 + rd[kk]));
+        vf[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(Vs + 32 * kh * 64 + rd[kk]));
+    }
+    // Padded step i uses ring slot i % 3.  Its loads were requested two steps earlier; wait for
+    // them, leaving the next step's six in flight, and the barrier publishes every wave's loads
+    // and frees slot (i + 2) % 3, whose step is requested right away.
+    auto ring_step = [&](const bf16_t* cur, bf16_t* next, bool real) __attribute__((always_inline)) {
         asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
         lds_barrier();
-        issue_step(next);
+        issue_step(next, true);
         advance();
-        step(cur);
+        if (real) step(cur);
     };
-    for (int i = 0; i < steps; i += 3) {
-        ring_step(ring0, ring2);
-        if (i + 1 >= steps) break;
-        ring_step(ring1, ring0);
-        if (i + 2 >= steps) break;
-        ring_step(ring2, ring1);
+    for (int i = 0; i < steps + pad; i += 3) {
+        ring_step(ring0, ring2, i >= pad);
+        ring_step(ring1, ring0, i + 1 >= pad);
+        ring_step(ring2, ring1, true);
     }
     // sum the two query halves' partials: qh = 1 parks its accumulators in LDS (the staging
     // buffers; with no steps the K / V loads may still be in flight, so wait for them first)
@@ -562,15 +617,15 @@ using namespace mosaic;
 
 extern "C" {
 
-// delta (fp32 per row), then q' (bf16 rows of 64), each 256-byte aligned
-static size_t bwd_delta_bytes(int32_t batch, int32_t seq_len, int32_t num_q_heads) {
+// -lse and -delta (fp32 per row), then q' (bf16 rows of 64), each 256-byte aligned
+static size_t bwd_row_bytes(int32_t batch, int32_t seq_len, int32_t num_q_heads) {
     return ((size_t)batch * seq_len * num_q_heads * sizeof(float) + 255) / 256 * 256;
 }
 
 size_t mosaic_sparse_attn_bwd_workspace_size(int32_t batch, int32_t seq_len, int32_t num_q_heads) {
     if (batch <= 0 || seq_len <= 0 || num_q_heads <= 0) return 0;
     const size_t qs = ((size_t)batch * seq_len * num_q_heads * kHeadDim * sizeof(bf16_t) + 255) / 256 * 256;
-    return bwd_delta_bytes(batch, seq_len, num_q_heads) + qs;
+    return 2 * bwd_row_bytes(batch, seq_len, num_q_heads) + qs;
 }
 
 int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const void* out, const float* lse,
@@ -600,8 +655,10 @@ int mosaic_sparse_attn_bwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const vo
     p.go_sb = grad_out.stride_b; p.go_sn = grad_out.stride_n; p.go_sh = grad_out.stride_h;
     p.o = static_cast<const bf16_t*>(out);
     p.lse = lse;
-    p.delta = static_cast<float*>(workspace);
-    p.qs = reinterpret_cast<bf16_t*>(static_cast<char*>(workspace) + bwd_delta_bytes(batch, seq_len, num_q_heads));
+    const size_t row_bytes = bwd_row_bytes(batch, seq_len, num_q_heads);
+    p.nlse = static_cast<float*>(workspace);
+    p.ndelta = reinterpret_cast<float*>(static_cast<char*>(workspace) + row_bytes);
+    p.qs = reinterpret_cast<bf16_t*>(static_cast<char*>(workspace) + 2 * row_bytes);
     p.idx = block_indices;
     p.dq = static_cast<bf16_t*>(grad_q); p.dk = static_cast<bf16_t*>(grad_k); p.dv = static_cast<bf16_t*>(grad_v);
     p.B = batch; p.N = seq_len; p.Hq = num_q_heads; p.Hk = num_kv_heads; p.G = num_q_heads / num_kv_heads;

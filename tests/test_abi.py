@@ -196,7 +196,7 @@ def test_backward_entry_validates():
     L = _lib.lib()
     t = _lib.Bnhd(FAKE, 0, 64 * 4, 64)
     ws = L.mosaic_sparse_attn_bwd_workspace_size(1, 256, 4)
-    assert ws == (256 * 4 * 4 + 255) // 256 * 256 + (256 * 4 * 64 * 2 + 255) // 256 * 256   # delta, then q'
+    assert ws == 2 * ((256 * 4 * 4 + 255) // 256 * 256) + (256 * 4 * 64 * 2 + 255) // 256 * 256   # -lse, -delta, q'
 
     def call(q=t, out=FAKE, lse=FAKE, idx=FAKE, N=256, Hq=4, Hk=1, d=64, bs=64, K=2, gq=FAKE, w=FAKE, wsb=ws):
         return L.mosaic_sparse_attn_bwd(q, t, t, out, lse, t, idx, 1, N, Hq, Hk, d, bs, K, 0.0, gq, FAKE, FAKE,
