@@ -96,19 +96,6 @@ __device__ __forceinline__ void tile_dma_init(uint32_t* dk, uint32_t* dv, int wa
         dv[i] = 2u * (uint32_t)(row * vsn + src);
     }
 }
-template <int NW>
-__device__ __forceinline__ void tile_dma(const uint32_t* dk, const uint32_t* dv, const bf16_t* kb, const bf16_t* vb,
-                                         int64_t ksn, int64_t vsn, int key0, bf16_t* Kd, bf16_t* Vd, int wave) {
-    const int k0 = __builtin_amdgcn_readfirstlane(key0);
-    const char* kt = reinterpret_cast<const char*>(kb + (int64_t)k0 * ksn);
-    const char* vt = reinterpret_cast<const char*>(vb + (int64_t)k0 * vsn);
-#pragma unroll
-    for (int i = 0; i < 8 / NW; ++i) {
-        const int row0 = 8 * (wave * (8 / NW) + i);
-        __builtin_amdgcn_global_load_lds(kt + dk[i], (lds_void*)(Kd + row0 * 64), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(vt + dv[i], (lds_void*)(Vd + row0 * 64), 16, 0, 0);
-    }
-}
 
 // Direct-to-LDS loads issued as inline assembly, address = base (uniform) + voff (per lane),
 // LDS destination M0 + 16 l (dwordx4) or M0 + 4 l (dword) for lane l.  The compiler's wait
@@ -131,9 +118,23 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t l
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
+// One 64-row tile's direct-to-LDS loads (offsets from tile_dma_init), issued as dma16
+template <int NW>
+__device__ __forceinline__ void tile_dma(const uint32_t* dk, const uint32_t* dv, const bf16_t* kb, const bf16_t* vb,
+                                             int64_t ksn, int64_t vsn, int key0, bf16_t* Kd, bf16_t* Vd, int wave) {
+    const int k0 = __builtin_amdgcn_readfirstlane(key0);
+    const bf16_t* kt = kb + (int64_t)k0 * ksn;
+    const bf16_t* vt = vb + (int64_t)k0 * vsn;
+#pragma unroll
+    for (int i = 0; i < 8 / NW; ++i) {
+        const int row0 = 8 * (wave * (8 / NW) + i);
+        dma16(kt, dk[i], lds_addr(Kd + row0 * 64));
+        dma16(vt, dv[i], lds_addr(Vd + row0 * 64));
+    }
+}
 
 template <int NW>
-__global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(1, 1)))
+__global__ __attribute__((amdgpu_flat_work_group_size(NW * 64, NW * 64), amdgpu_waves_per_eu(2, 2)))
 void bwd_dq_kernel(BwdParams p, int head_groups, int total_wgs) {
     __shared__ __attribute__((aligned(1024))) bf16_t Ks0[kTileElems];
     __shared__ __attribute__((aligned(1024))) bf16_t Ks1[kTileElems];
@@ -318,17 +319,19 @@ void bwd_dq_kernel(BwdParams p, int head_groups, int total_wgs) {
         }
     };
     // tile t in buffer t & 1: wait for this wave's loads, the barrier publishes every wave's loads
-    // and frees the other buffer, whose next tile is requested right away
+    // and frees the other buffer, whose next tile is requested right away.  Two tiles per
+    // round and one exit (an odd count skips the last tile's products): with an exit after
+    // each tile the accumulators lived in rotating register sets (316 registers, one wave per
+    // SIMD); now 240, two waves per SIMD.
     for (int t = 0; t < total; t += 2) {
         wait_vmem();
         __syncthreads();
         if (t + 1 < total) tile_dma<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(), Ks1, Vs1, wave);
         tile(Ks0, Vs0);
-        if (t + 1 >= total) break;
         wait_vmem();
         __syncthreads();
         if (t + 2 < total) tile_dma<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(), Ks0, Vs0, wave);
-        tile(Ks1, Vs1);
+        if (t + 1 < total) tile(Ks1, Vs1);
     }
     // dq = bf16((dQ scale) log2 e), rows n0 + 32 qt + r, dims 32 dt + 8 g4 + 4 hh + 0..3
     bf16_t* out = p.dq + (((int64_t)b * p.N + n0) * p.Hq + j) * 64;
