@@ -47,6 +47,7 @@ def check(got, ref, name):
     (2, 1024, 12, 3, 128, 3),
     (1, 3072, 20, 5, 64, 4),      # the bottleneck shape of the CPU reference config
     (1, 2048, 8, 8, 64, 16),
+    (1, 1536, 6, 2, 192, 3),      # GQA group of 3 (one wave per grad-q workgroup), 3 tiles per block
 ])
 def test_sparse_attn_bwd_matches_oracle(B, N, Hq, Hk, bs, K):
     print(f"bwd B={B} N={N} Hq={Hq} Hk={Hk} bs={bs} K={K}", flush=True)
