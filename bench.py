@@ -334,9 +334,10 @@ def unet_leg(args, dev):
     one library GEMM for the q / k / v / gate projection and the op's pooling pass with RoPE
     (``--unet-fused-input-side`` takes the fused projection kernel instead), both grid
     interpolations the k-NN kernel; the other projections are library GEMMs."""
-    from mosaic_amd.model import Transformer, era5_config, model_flops
+    from mosaic_amd.model import Transformer, cSwiGLU, era5_config, model_flops
     from mosaic_amd.primitives import MosaicAttention
     MosaicAttention.fused_input_side = args.unet_fused_input_side
+    cSwiGLU.fused_linear_gate = args.unet_fused_ffn
     cfg = era5_config()
     torch.manual_seed(args.seed)
     t0 = time.perf_counter()
@@ -376,6 +377,7 @@ def unet_leg(args, dev):
             "output_shape": list(out.shape), "output_finite": bool(torch.isfinite(out).all().item()),
             "peak_mem_gb": round(torch.cuda.max_memory_allocated(dev) / 1e9, 1), "setup_s": round(setup_s, 1),
             "input_side": "fused" if args.unet_fused_input_side else "unfused",
+            "ffn_gate": "fused with w13" if args.unet_fused_ffn else "library GEMM, then the gate kernel",
             "data": "synthetic N(0,1) input and static fields, random-init weights (no checkpoint offline)"}
 
 
@@ -480,6 +482,8 @@ def main():
     ap.add_argument("--unet-warmup", type=int, default=1)
     ap.add_argument("--unet-fused-input-side", action="store_true",
                     help="U-Net attention blocks take the fused projection kernel (mosaic_attn_proj)")
+    ap.add_argument("--unet-fused-ffn", action="store_true",
+                    help="U-Net feed-forward blocks run w13 and the SwiGLU gate as one kernel (fused.swiglu_linear)")
     ap.add_argument("--calibration-copy-mb", type=int, default=0,
                     help="after timing, run one device-to-device copy of this many MiB (a known-size "
                          "kernel for scaling FETCH_SIZE / WRITE_SIZE counters)")

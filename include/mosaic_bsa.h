@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 4
+#define MOSAIC_BSA_ABI_VERSION 5
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -285,6 +285,20 @@ MOSAIC_API int mosaic_rms_norm_fwd(const void* x, const void* residual, int32_t 
 MOSAIC_API int mosaic_swiglu_fwd(const void* h, int32_t dtype, int64_t rows, int32_t hidden,
                                  int64_t h_row_stride, const void* noise, int32_t noise_rows, void* out,
                                  void* stream);
+
+/* cSwiGLU's first projection and gate in one kernel (primitives.py:92-105, w13 then the gate
+   of mosaic_swiglu_fwd): out = silu(x1 + noise[row % noise_rows]) * x3 with h = x w13^T
+   rounded to bf16 (fp32 accumulation) and x1, x3 its two halves, so h is never stored.
+   x: bf16 [rows, dim] with row stride x_row_stride; weight: bf16 [2*hidden, dim] contiguous,
+   w13 with its rows permuted in 64-row groups -- group t holds rows 32t..32t+31 of the x1 half
+   (w13 rows 32t..) then of the x3 half (w13 rows hidden+32t..); noise: optional bf16
+   [noise_rows, hidden] contiguous; out: bf16 [rows, hidden] contiguous.  rows a multiple of
+   256, dim of 128, hidden of 128; pointers 16-byte aligned, x_row_stride a multiple of 8.
+   No reference counterpart as one function: it fuses the Linear and the gate the reference
+   runs as separate ops. */
+MOSAIC_API int mosaic_swiglu_linear_fwd(const void* x, int64_t rows, int32_t dim, int64_t x_row_stride,
+                                        const void* weight, int32_t hidden, const void* noise,
+                                        int32_t noise_rows, void* out, void* stream);
 
 /* Name of a status code (static storage). */
 MOSAIC_API const char* mosaic_bsa_strerror(int status);

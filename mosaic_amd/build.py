@@ -39,6 +39,7 @@ FILE_FLAGS = {
     "cmp.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "proj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "ffn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -6,6 +6,8 @@
 * ``RMSNorm``: ``torch.nn.RMSNorm`` (same parameters) running ``rms_norm`` on a ROCm device,
   with ``add_forward`` for the residual-add variant.
 * ``swiglu(h, noise)``: the gate ``silu(x1 + noise) * x3`` of cSwiGLU (primitives.py:102-105).
+* ``swiglu_linear(x, w13_perm, noise)``: cSwiGLU's ``w13`` projection and that gate in one
+  kernel (h is never stored); ``permute_w13`` lays out the weight it takes.
 
 Inputs must be on a ROCm device; there is no CPU path.  ``autocast_dtype`` reports the dtype
 torch's own RMSNorm returns under the current autocast state, so the fused norm's output has
@@ -20,7 +22,7 @@ import torch.nn as nn
 from . import _lib
 from .ops import forward_only, stream_of
 
-__all__ = ["RMSNorm", "rms_norm", "swiglu", "autocast_dtype"]
+__all__ = ["RMSNorm", "rms_norm", "swiglu", "swiglu_linear", "permute_w13", "swiglu_linear_ok", "autocast_dtype"]
 
 _DT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
 _autocast_out: dict = {}
@@ -109,6 +111,58 @@ def swiglu(h: torch.Tensor, noise: torch.Tensor | None = None) -> torch.Tensor:
                                       n.data_ptr() if n is not None else None,
                                       n.shape[0] if n is not None else 0, out.data_ptr(), stream_of(h))
     _lib.check(st, "mosaic_swiglu_fwd")
+    return out
+
+
+def permute_w13(w13: torch.Tensor) -> torch.Tensor:
+    """w13 ``[2*hidden, dim]`` with its rows in the order ``swiglu_linear`` takes: 64-row group
+    t holds rows 32t..32t+31 of the x1 half, then the same rows of the x3 half."""
+    two_h, dim = w13.shape
+    hidden = two_h // 2
+    if two_h % 2 or hidden % 32:
+        raise ValueError(f"w13 rows {two_h} must be 2 * a multiple of 32")
+    a = w13[:hidden].reshape(hidden // 32, 32, dim)
+    b = w13[hidden:].reshape(hidden // 32, 32, dim)
+    return torch.stack([a, b], dim=1).reshape(two_h, dim).contiguous()
+
+
+def swiglu_linear_ok(x: torch.Tensor, hidden: int) -> bool:
+    """Whether ``swiglu_linear`` takes this input: bf16 on a ROCm device, unit stride in the
+    last dimension, rows a multiple of 256, dim and hidden multiples of 128."""
+    if not x.is_cuda or x.dtype != torch.bfloat16 or x.dim() < 2 or x.stride(-1) != 1:
+        return False
+    rows = x.numel() // x.shape[-1]
+    return rows > 0 and rows % 256 == 0 and x.shape[-1] % 128 == 0 and hidden % 128 == 0
+
+
+def swiglu_linear(x: torch.Tensor, w13_perm: torch.Tensor, noise: torch.Tensor | None = None) -> torch.Tensor:
+    """``swiglu(x @ w13^T, noise)`` in one kernel: the projection (bf16 operands, fp32
+    accumulation, rounded to bf16 as a bf16 Linear) and the gate with its rounding points.
+    x: bf16 ``[..., dim]`` (rows sequence-first ``[S, B]`` when noise is given); w13_perm:
+    ``permute_w13(w13)`` in bf16; noise: ``[B, hidden]`` or None.  Returns ``[..., hidden]``."""
+    forward_only("fused.swiglu_linear", x, w13_perm, noise)
+    two_h, dim = w13_perm.shape
+    hidden = two_h // 2
+    if x.shape[-1] != dim:
+        raise ValueError(f"x has {x.shape[-1]} features, the weight {dim}")
+    if not swiglu_linear_ok(x, hidden):
+        raise ValueError("swiglu_linear needs bf16 ROCm input with rows % 256 == 0, dim % 128 == 0, hidden % 128 == 0")
+    if w13_perm.dtype != torch.bfloat16 or not w13_perm.is_contiguous() or w13_perm.device != x.device:
+        raise ValueError("w13_perm must be a contiguous bf16 tensor on x's device")
+    x2 = x.reshape(-1, dim)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    n = None
+    if noise is not None:
+        n = noise.to(torch.bfloat16).reshape(-1, hidden).contiguous()
+        if x.dim() < 2 or x.shape[-2] != n.shape[0]:
+            raise ValueError("noise must hold one row per batch member (x.shape[-2])")
+    out = torch.empty(*x.shape[:-1], hidden, dtype=torch.bfloat16, device=x.device)
+    st = _lib.lib().mosaic_swiglu_linear_fwd(x2.data_ptr(), rows, dim, x2.stride(0), w13_perm.data_ptr(), hidden,
+                                             n.data_ptr() if n is not None else None,
+                                             n.shape[0] if n is not None else 0, out.data_ptr(), stream_of(x))
+    _lib.check(st, "mosaic_swiglu_linear_fwd")
     return out
 
 

@@ -230,6 +230,32 @@ def test_fused_elementwise_entries_validate():
     assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3072, 6144, FAKE, 0, FAKE, None) == 8
     assert L.mosaic_swiglu_fwd(None, BF, 4, 3072, 6144, None, 0, FAKE, None) == 1
     assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3072, 6144, FAKE + 8, 2, FAKE, None) == 7
+    # swiglu_linear(x, rows, dim, x_stride, weight, hidden, noise, noise_rows, out, stream)
+    sl = L.mosaic_swiglu_linear_fwd
+    assert sl(FAKE, 0, 768, 768, FAKE, 3072, None, 0, FAKE, None) == 8
+    assert sl(FAKE, 300, 768, 768, FAKE, 3072, None, 0, FAKE, None) == 11      # rows % 256
+    assert sl(FAKE, 512, 700, 704, FAKE, 3072, None, 0, FAKE, None) == 11      # dim % 128
+    assert sl(FAKE, 512, 768, 768, FAKE, 3000, None, 0, FAKE, None) == 11      # hidden % 128
+    assert sl(FAKE, 512, 768, 760, FAKE, 3072, None, 0, FAKE, None) == 7       # stride < dim
+    assert sl(FAKE, 512, 768, 772, FAKE, 3072, None, 0, FAKE, None) == 7       # stride % 8
+    assert sl(FAKE + 8, 512, 768, 768, FAKE, 3072, None, 0, FAKE, None) == 7
+    assert sl(FAKE, 512, 768, 768, FAKE, 3072, FAKE + 8, 2, FAKE, None) == 7
+    assert sl(FAKE, 512, 768, 768, FAKE, 3072, FAKE, 0, FAKE, None) == 8       # noise rows
+    assert sl(None, 512, 768, 768, FAKE, 3072, None, 0, FAKE, None) == 1
+    assert sl(FAKE, 512, 768, 768, None, 3072, None, 0, FAKE, None) == 1
+    assert sl(FAKE, 512, 768, 1 << 26, FAKE, 3072, None, 0, FAKE, None) == 11  # 32-bit offsets
+
+
+def test_permute_w13_layout():
+    import torch
+    from mosaic_amd import fused
+    w = torch.arange(2 * 96 * 4, dtype=torch.float32).view(2 * 96, 4)
+    p = fused.permute_w13(w)
+    for t in range(3):
+        assert torch.equal(p[64 * t:64 * t + 32], w[32 * t:32 * t + 32])          # x1 rows
+        assert torch.equal(p[64 * t + 32:64 * t + 64], w[96 + 32 * t:96 + 32 * t + 32])   # x3 rows
+    with pytest.raises(ValueError):
+        fused.permute_w13(torch.zeros(2 * 40, 4))
 
 
 def test_bsa_fwd_output_strides_validate():
