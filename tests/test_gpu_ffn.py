@@ -89,8 +89,12 @@ def test_cswiglu_module_fused_equals_unfused():
     check(c, d, "after a weight update")
 
 
-def test_cswiglu_refuses_grad():
-    m = cSwiGLU(256, 256, 0).to(DEV)
+@pytest.mark.parametrize("fused_gate", [True, False])
+def test_cswiglu_refuses_grad(fused_gate):
+    """With grad mode on and weights that require grad, both paths raise rather than return an
+    output cut off from the graph."""
+    m = cSwiGLU(256, 256, 0).to(DEV).to(torch.bfloat16)
+    m.fused_linear_gate = fused_gate
     x = torch.randn(256, 1, 256, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="no backward"):
         m(x)
