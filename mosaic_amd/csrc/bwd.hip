@@ -9,16 +9,18 @@
 //           with P = exp2(q'.k - lse), dP = do.v            (ops.py:265-273)
 //   dv    = sum over the queries that selected the key of bf16(P) do
 //   dk    = sum of bf16(P (dP - delta) ln2) q'              (ops.py:425-431)
-// Products run on v_mfma_f32_32x32x16_bf16 with fp32 accumulation.
+// Products run on v_mfma_f32_32x32x16_bf16 with fp32 accumulation.  One difference in order:
+// grad k/v accumulates S and dP onto -lse and -delta, so those subtractions happen inside the
+// fp32 accumulation rather than after it.
 //
 // The reference's grad-k/v program scans a dense [B, Hk, nb, nb] boolean block mask for every
 // key block.  Here each key-tile workgroup marks, in LDS, the query blocks whose selection row
 // holds its block (one pass over the [nb, K] index rows of its kv head) and then walks the
 // marked blocks in ascending order -- the reference's loop order, without the mask tensor.
 //
-// Tiles reach LDS by direct-to-LDS loads (no register staging) in a layout that both 16-byte
-// row reads and ds_read_b64_tr_b16 transposing reads take without bank conflicts, so no
-// transposed copy of any operand is stored.
+// Tiles reach LDS by direct-to-LDS loads (no register staging, issued as inline assembly) in a
+// layout that both 16-byte row reads and ds_read_b64_tr_b16 transposing reads take without
+// bank conflicts, so no transposed copy of any operand is stored.
 
 #include <hip/hip_runtime.h>
 
