@@ -403,9 +403,13 @@ def branches_leg(L, a, q, k, v, wl, args, stream):
         _lib.check(L.mosaic_block_attn_fwd(bnhd(q), bnhd(k), bnhd(v), B, N, Hq, Hk, d, bl, 0.0, out.data_ptr(), sp),
                    "mosaic_block_attn_fwd")
 
+    sws = torch.empty(max(L.mosaic_sparse_attn_fwd_workspace_size(B, N, Hk, bs), 16), dtype=torch.uint8,
+                      device=q.device)
+
     def selected():
-        _lib.check(L.mosaic_sparse_attn_fwd(bnhd(q), bnhd(k), bnhd(v), idx.data_ptr(), B, N, Hq, Hk, d, bs, K, 0.0,
-                                            out.data_ptr(), lse.data_ptr(), sp), "mosaic_sparse_attn_fwd")
+        _lib.check(L.mosaic_sparse_attn_fwd_ws(bnhd(q), bnhd(k), bnhd(v), idx.data_ptr(), B, N, Hq, Hk, d, bs, K, 0.0,
+                                               out.data_ptr(), lse.data_ptr(), sws.data_ptr(), sws.numel(), sp),
+                   "mosaic_sparse_attn_fwd_ws")
 
     res = {}
     for name, fn, flops in (("local", local, 4 * B * Hq * d * N * bl), ("selected", selected, 4 * B * Hq * d * N * K * bs)):
@@ -421,7 +425,8 @@ def branches_leg(L, a, q, k, v, wl, args, stream):
         ms = e0.elapsed_time(e1) / args.steps
         tf = flops / (ms * 1e-3) / 1e12
         res[name] = {"ms": round(ms, 4), "flops": flops, "tflops": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
-    res["selected"]["kernel"] = "bsa_attn_kernel selected-only (running-reference path, writes the LSE)"
+    res["selected"]["kernel"] = ("key-norm bound pass over k (pool_kernel) + bsa_attn_kernel selected-only "
+                                 "(bounded path where the bound allows, writes the LSE)")
     res["local"]["kernel"] = "bsa_attn_kernel local-only"
     return res
 

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 5
+#define MOSAIC_BSA_ABI_VERSION 6
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -209,6 +209,20 @@ MOSAIC_API int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd 
                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                            int32_t block_size, int32_t block_count, float softmax_scale,
                            void* out, float* lse, void* stream);
+
+/* As mosaic_sparse_attn_fwd, with a workspace of mosaic_sparse_attn_fwd_workspace_size()
+   bytes (16-byte aligned) for the key-norm bounds of k's blocks ([B, N/block_size, Hk, 8]
+   fp32, a pass over k): query tiles whose logits all lie within the bound then take the
+   bounded-logit path of the fused forward (reference 0, row sums on the matrix pipe) instead
+   of the running maximum.  Same outputs, to fp32 rounding. */
+MOSAIC_API size_t mosaic_sparse_attn_fwd_workspace_size(int32_t batch, int32_t seq_len, int32_t num_kv_heads,
+                                                        int32_t block_size);
+MOSAIC_API int mosaic_sparse_attn_fwd_ws(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v,
+                                         const int64_t* block_indices, int32_t batch, int32_t seq_len,
+                                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                         int32_t block_size, int32_t block_count, float softmax_scale,
+                                         void* out, float* lse, void* workspace, size_t workspace_bytes,
+                                         void* stream);
 
 /*
  * Backward of the selected-branch attention.  Replaces MosaicAttnFunction.backward /

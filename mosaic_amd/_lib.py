@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # mosaic_bsa_mode
 MODE_FULL = 0
@@ -42,6 +42,8 @@ EXPORTED_SYMBOLS = (
     "mosaic_swiglu_fwd",
     "mosaic_swiglu_linear_fwd",
     "mosaic_sparse_attn_fwd",
+    "mosaic_sparse_attn_fwd_workspace_size",
+    "mosaic_sparse_attn_fwd_ws",
     "mosaic_block_attn_fwd",
     "mosaic_dense_attn_fwd",
     "mosaic_pool_mean_fwd",
@@ -125,6 +127,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_sparse_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
                                            c_i32, c_i32, c_f, c_vp, c_vp, c_vp]
     lib.mosaic_sparse_attn_fwd.restype = c_int
+    lib.mosaic_sparse_attn_fwd_workspace_size.argtypes = [c_i32, c_i32, c_i32, c_i32]
+    lib.mosaic_sparse_attn_fwd_workspace_size.restype = c_size
+    lib.mosaic_sparse_attn_fwd_ws.argtypes = [Bnhd, Bnhd, Bnhd, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                              c_i32, c_i32, c_f, c_vp, c_vp, c_vp, c_size, c_vp]
+    lib.mosaic_sparse_attn_fwd_ws.restype = c_int
     lib.mosaic_block_attn_fwd.argtypes = [Bnhd, Bnhd, Bnhd, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f,
                                           c_vp, c_vp]
     lib.mosaic_block_attn_fwd.restype = c_int

@@ -391,10 +391,12 @@ int mosaic_bsa_fwd_proj(const mosaic_bsa_args* args, const mosaic_proj_args* pro
     return bsa_forward(&a, workspace, workspace_bytes, stream, nullptr, nullptr, &p);
 }
 
-int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const int64_t* block_indices,
-                           int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
-                           int32_t head_dim, int32_t block_size, int32_t block_count, float softmax_scale,
-                           void* out, float* lse, void* stream) {
+// The selected branch alone; with kbnd (the key-norm bounds of k's blocks, [B, nb, Hk, 8])
+// a workgroup whose logits are all within the bound takes the bounded path.
+static int sparse_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const int64_t* block_indices, int32_t batch,
+                      int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t block_size, int32_t block_count, float softmax_scale, void* out, float* lse,
+                      float* kbnd, void* stream) {
     if (batch <= 0 || seq_len <= 0 || block_count <= 0) return block_count <= 0 ? MOSAIC_ERR_BLOCK_COUNT : MOSAIC_ERR_SHAPE;
     if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
     if (int e = check_heads(num_q_heads, num_kv_heads)) return e;
@@ -416,7 +418,41 @@ int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const in
     ap.bs_l = block_size;
     ap.K = block_count;
     ap.nb = seq_len / block_size;
-    return launch_status(launch_attn(ap, kModeSelectedOnly, true, attn_waves(ap.G), static_cast<hipStream_t>(stream)));
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kbnd != nullptr) {   // k's block bounds: the pooling pass over k alone, bounds only
+        PoolParams pp{};
+        pp.x[1] = ap.k; pp.sb[1] = ap.k_sb; pp.sn[1] = ap.k_sn; pp.sh[1] = ap.k_sh; pp.heads[1] = num_kv_heads;
+        pp.kbnd = kbnd;
+        pp.B = batch; pp.nb = ap.nb; pp.nb_pad = ap.nb; pp.bs = block_size;
+        if (int e = launch_status(launch_pool(pp, s))) return e;
+        ap.kbnd = kbnd;
+    }
+    return launch_status(launch_attn(ap, kModeSelectedOnly, true, attn_waves(ap.G), s));
+}
+
+int mosaic_sparse_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const int64_t* block_indices,
+                           int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                           int32_t head_dim, int32_t block_size, int32_t block_count, float softmax_scale,
+                           void* out, float* lse, void* stream) {
+    return sparse_fwd(q, k, v, block_indices, batch, seq_len, num_q_heads, num_kv_heads, head_dim, block_size,
+                      block_count, softmax_scale, out, lse, nullptr, stream);
+}
+
+size_t mosaic_sparse_attn_fwd_workspace_size(int32_t batch, int32_t seq_len, int32_t num_kv_heads,
+                                             int32_t block_size) {
+    if (batch <= 0 || seq_len <= 0 || num_kv_heads <= 0 || block_size <= 0 || seq_len % block_size) return 0;
+    return (size_t)batch * (seq_len / block_size) * num_kv_heads * 8 * sizeof(float);
+}
+
+int mosaic_sparse_attn_fwd_ws(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, const int64_t* block_indices,
+                              int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t block_size, int32_t block_count, float softmax_scale,
+                              void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+    const size_t need = mosaic_sparse_attn_fwd_workspace_size(batch, seq_len, num_kv_heads, block_size);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+        return MOSAIC_ERR_WORKSPACE;
+    return sparse_fwd(q, k, v, block_indices, batch, seq_len, num_q_heads, num_kv_heads, head_dim, block_size,
+                      block_count, softmax_scale, out, lse, need > 0 ? static_cast<float*>(workspace) : nullptr, stream);
 }
 
 int mosaic_block_attn_fwd(mosaic_bnhd q, mosaic_bnhd k, mosaic_bnhd v, int32_t batch, int32_t seq_len,

@@ -319,7 +319,7 @@ void bsa_attn_kernel(AttnParams p) {
     constexpr bool kWeights = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeNoSelection;
     constexpr bool kPartial = MODE == kModeFull || MODE == kModeNoCompression;
     // selected tiles may take the bounded-logit path (key-norm bounds come with the pooling)
-    constexpr bool kFastSel = MODE == kModeFull || MODE == kModeNoCompression;
+    constexpr bool kFastSel = MODE == kModeFull || MODE == kModeNoCompression || MODE == kModeSelectedOnly;
 
     // two staging buffers as separate objects, so the compiler can tell the loads in flight
     // into one buffer from the reads of the other
@@ -450,7 +450,24 @@ void bsa_attn_kernel(AttnParams p) {
         }
         return key0;
     };
-    if (!kLocal && total_tiles > 0) dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(0), Ks0, Vs0, wave);
+    // With the first selected tile, the key-norm bounds of the selected blocks (32 bytes each)
+    // go to LDS; they arrive with that tile (when the caller supplied them).
+    auto load_kbnd = [&]() {
+        if (wave == 0 && p.kbnd != nullptr && nvalid <= kMaxBounded) {
+            for (int i0 = 0; i0 < nvalid; i0 += 32) {
+                const int i = i0 + (lane >> 1);
+                if (i < nvalid) {
+                    const int64_t blk = sel_key0[i] / p.bs;
+                    const float* src = p.kbnd + ((b * p.nb + blk) * p.Hk + c) * 8 + 4 * (lane & 1);
+                    __builtin_amdgcn_global_load_lds(src, (lds_void*)(sel_kbnd + 8 * i0), 16, 0, 0);
+                }
+            }
+        }
+    };
+    if (!kLocal && total_tiles > 0) {
+        dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(0), Ks0, Vs0, wave);
+        if constexpr (kFastSel) load_kbnd();
+    }
 
     ReadOffsets ro;
     ro.init(lane);
@@ -467,19 +484,8 @@ void bsa_attn_kernel(AttnParams p) {
         const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
         if (t + 1 < total_tiles)
             dma_issue<NW>(dk, dv, kb, vb, p.k_sn, p.v_sn, next_key0(t + 1), BUF ? Ks0 : Ks1, BUF ? Vs0 : Vs1, wave);
-        if constexpr (kFastSel) {
-            // with the first selected tile, the key-norm bounds of the selected blocks (32 bytes
-            // each) go to LDS; they arrive with that tile
-            if (t + 1 == tl_count && wave == 0 && p.kbnd != nullptr && nvalid <= kMaxBounded) {
-                for (int i0 = 0; i0 < nvalid; i0 += 32) {
-                    const int i = i0 + (lane >> 1);
-                    if (i < nvalid) {
-                        const int64_t blk = sel_key0[i] / p.bs;
-                        const float* src = p.kbnd + ((b * p.nb + blk) * p.Hk + c) * 8 + 4 * (lane & 1);
-                        __builtin_amdgcn_global_load_lds(src, (lds_void*)(sel_kbnd + 8 * i0), 16, 0, 0);
-                    }
-                }
-            }
+        if constexpr (kFastSel && kLocal) {
+            if (t + 1 == tl_count) load_kbnd();
         }
     };
     auto begin_tile = [&](auto bufc, int t) {
@@ -723,8 +729,17 @@ void bsa_attn_kernel(AttnParams p) {
             auto fast_body = [&](auto bufc) __attribute__((always_inline)) {
                 const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
                 s_tile_seq(BUF ? Ks1 : Ks0, ro, qf, s);
-                exp_pack_raw(s, pb);
-                row_sums(rsel, pb, lacc);
+                if constexpr (MODE == kModeSelectedOnly) {
+                    // the LSE is an output: row sums of the fp32 P, as the reference forms l
+                    // (ops.py:125), per lane on the VALU
+                    float lt[2];
+                    exp_pack<false, false>(s, m, 1.f, pb, lt);
+                    l[0] += lt[0];
+                    l[1] += lt[1];
+                } else {
+                    exp_pack_raw(s, pb);
+                    row_sums(rsel, pb, lacc);
+                }
                 pv_tile(BUF ? Vs1 : Vs0, ro, pb, o);
             };
             // the first selected tile has begun; enter the two-buffer loop at its parity
@@ -740,10 +755,11 @@ void bsa_attn_kernel(AttnParams p) {
                 if (++t >= total_tiles) break;
                 begin_tile(Buf0{}, t);
             }
-            // every lane holds its row's whole sum; the epilogue adds the two key halves
+            // every lane holds its row's whole sum (matrix-pipe sums) or its partial sum (VALU
+            // sums of the selected-only mode); the epilogue adds the two key halves
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
-                l[qt] = hh == 0 ? lacc[qt][0] : 0.f;
+                if constexpr (MODE != kModeSelectedOnly) l[qt] = hh == 0 ? lacc[qt][0] : 0.f;
                 m[qt] = 0.f;
             }
         } else if (t < total_tiles) {

@@ -91,10 +91,14 @@ def mosaic_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_ind
         raise ValueError(f"block_indices shape {tuple(idx.shape)} != {(B, N // block_size, Hk, '*')}")
     out = torch.empty(B, N, Hq, d, dtype=torch.bfloat16, device=q.device)
     lse = torch.empty(B, N, Hq, dtype=torch.float32, device=q.device)
-    st = _lib.lib().mosaic_sparse_attn_fwd(
+    L = _lib.lib()
+    # workspace for the key-norm bounds of k's blocks (lets query tiles take the bounded path)
+    nbytes = L.mosaic_sparse_attn_fwd_workspace_size(B, N, Hk, int(block_size))
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    st = L.mosaic_sparse_attn_fwd_ws(
         bnhd(q), bnhd(k), bnhd(v), idx.data_ptr(), B, N, Hq, Hk, d, int(block_size), int(idx.shape[-1]),
-        float(softmax_scale), out.data_ptr(), lse.data_ptr(), stream_of(q))
-    _lib.check(st, "mosaic_sparse_attn_fwd")
+        float(softmax_scale), out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(), stream_of(q))
+    _lib.check(st, "mosaic_sparse_attn_fwd_ws")
     return out, lse
 
 

@@ -164,6 +164,14 @@ def test_other_entry_points_validate():
     assert L.mosaic_sparse_attn_fwd(t, t, t, FAKE, 1, 256, 4, 1, 64, 64, 0, 0.0, FAKE, None, None) == 5
     assert L.mosaic_sparse_attn_fwd(t, t, t, FAKE, 1, 256, 4, 3, 64, 64, 1, 0.0, FAKE, None, None) == 3
     assert L.mosaic_sparse_attn_fwd(t, t, t, None, 1, 256, 4, 1, 64, 64, 1, 0.0, FAKE, None, None) == 1
+    # the workspace variant: key-norm bounds [B, N/bs, Hk, 8] fp32
+    assert L.mosaic_sparse_attn_fwd_workspace_size(2, 256, 3, 64) == 2 * 4 * 3 * 8 * 4
+    assert L.mosaic_sparse_attn_fwd_workspace_size(1, 250, 1, 64) == 0
+    ws = L.mosaic_sparse_attn_fwd_workspace_size(1, 256, 1, 64)
+    assert L.mosaic_sparse_attn_fwd_ws(t, t, t, FAKE, 1, 256, 4, 1, 64, 64, 1, 0.0, FAKE, None, None, ws, None) == 6
+    assert L.mosaic_sparse_attn_fwd_ws(t, t, t, FAKE, 1, 256, 4, 1, 64, 64, 1, 0.0, FAKE, None, FAKE, ws - 4,
+                                       None) == 6
+    assert L.mosaic_sparse_attn_fwd_ws(t, t, t, FAKE, 1, 256, 4, 1, 64, 64, 0, 0.0, FAKE, None, FAKE, ws, None) == 5
     assert L.mosaic_block_attn_fwd(t, t, t, 1, 256, 4, 1, 64, 96, 0.0, FAKE, None) == 4
     assert L.mosaic_dense_attn_fwd(t, t, t, 1, 100, 4, 1, 64, 0.0, FAKE, None) == 4
     assert L.mosaic_pool_mean_fwd(t, 1, 256, 4, 48, 64, FAKE, None) == 2
