@@ -339,13 +339,12 @@ hipError_t launch_knn_attn(const InterpParams& p, hipStream_t s);
 constexpr int kMaxSelected = 1024;
 
 // Most compressed-attention splits (partials per row).
-constexpr int kMaxSplits = 2;
+constexpr int kMaxSplits = 4;
 
 // The compressed-branch output at block t of NH heads j0, j0 + jstep, ..., combined over the
 // splits: lane owns dimension d = lane.  exp2 weights are relative to the largest split max.
 // All loads of all heads and splits are issued before any arithmetic (one memory round trip);
-// they are unconditional (past nsplit: the last split again, not used), so no branch sits
-// between them.
+// splits past nsplit (uniform) are neither loaded nor used.
 template <int NH>
 __device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int nb, int t, int j0, int jstep, int lane) {
     const int64_t stride = (int64_t)nb * c.Hq;
@@ -356,9 +355,11 @@ __device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int 
         const int64_t row0 = ((int64_t)b * c.nsplit * nb + t) * c.Hq + j0 + h * jstep;
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; ++sp) {
-            const int64_t row = row0 + min(sp, c.nsplit - 1) * stride;
-            mlv[h][sp] = c.ml[row];
-            ov[h][sp] = c.opart[row * kHeadDim + lane];
+            if (sp < c.nsplit) {
+                const int64_t row = row0 + sp * stride;
+                mlv[h][sp] = c.ml[row];
+                ov[h][sp] = c.opart[row * kHeadDim + lane];
+            }
         }
     }
 #pragma unroll

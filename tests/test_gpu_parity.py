@@ -192,15 +192,16 @@ def test_mosaic_attn_func_many_selected_blocks():
     close(got_rows, ref_rows)
 
 
-@pytest.mark.parametrize("B,N,Hq,Hk", [(1, 3072, 20, 5), (24, 12288, 16, 4)],
-                         ids=["nb48_two_key_splits", "b24_nb192_one_key_split"])
+@pytest.mark.parametrize("B,N,Hq,Hk", [(1, 3072, 20, 5), (1, 49152, 12, 3), (1, 12288, 12, 3), (24, 12288, 16, 4)],
+                         ids=["nb48_two_key_splits", "nb768_three_key_splits", "nb192_four_key_splits",
+                              "b24_nb192_one_key_split"])
 def test_compressed_branch_alone(B, N, Hq, Hk):
     """Gates (0, 1, 0) on block-structured inputs: the output is the compressed branch (pooled
     attention over all blocks, primitives.py:65-66,76-78) broadcast over each block's tokens.
     The pooled logits have std > 2, so a branch that ignored its logits, mis-scaled them or
     read the wrong pooled v block fails the bar (tests/test_oracle.py shows it on the same
-    inputs).  The grids cover the kernel's two key splits (48 blocks) and one split (24
-    members of 192 blocks)."""
+    inputs).  The grids cover the kernel's key splits: two (48 blocks, 5 kv heads), three (768
+    blocks, 3 kv heads), four (192 blocks, 3 kv heads) and one (24 members of 192 blocks)."""
     print(f"compressed branch B={B} N={N} heads {Hq}/{Hk}", flush=True)
     bs = 64
     q, k, v, w = compressed_only_inputs(B, N, Hq, Hk, bs, seed=0)
