@@ -343,11 +343,17 @@ constexpr int kMaxSplits = 4;
 
 // The compressed-branch output at block t of NH heads j0, j0 + jstep, ..., combined over the
 // splits: lane owns dimension d = lane.  exp2 weights are relative to the largest split max.
-// All loads of all heads and splits are issued before any arithmetic (one memory round trip);
-// splits past nsplit (uniform) are neither loaded nor used.
+// All loads of all heads and splits are issued before any arithmetic (one memory round trip).
+// They are unconditional (past nsplit: the last split again, not used): loads under a branch
+// leave the compiler's count of loads in flight unknown at the join, and the first wait after
+// it then waits for all of them.
 template <int NH>
 __device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int nb, int t, int j0, int jstep, int lane) {
     const int64_t stride = (int64_t)nb * c.Hq;
+    // written by an earlier launch and only read here: the constant address space lets the
+    // compiler take the scalar path for the uniform (max, sum) rows
+    typedef const __attribute__((address_space(4))) float cfloat;
+    cfloat* ml = (cfloat*)c.ml;
     float2 mlv[NH][kMaxSplits];
     float ov[NH][kMaxSplits];
 #pragma unroll
@@ -355,11 +361,9 @@ __device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int 
         const int64_t row0 = ((int64_t)b * c.nsplit * nb + t) * c.Hq + j0 + h * jstep;
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; ++sp) {
-            if (sp < c.nsplit) {
-                const int64_t row = row0 + sp * stride;
-                mlv[h][sp] = c.ml[row];
-                ov[h][sp] = c.opart[row * kHeadDim + lane];
-            }
+            const int64_t row = row0 + min(sp, c.nsplit - 1) * stride;
+            mlv[h][sp] = make_float2(ml[2 * row], ml[2 * row + 1]);
+            ov[h][sp] = c.opart[row * kHeadDim + lane];
         }
     }
 #pragma unroll

@@ -10,7 +10,7 @@ namespace {
 
 template <int PL>  // keys per lane: nb <= 64 * PL
 __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));  // one per wave
     if (row >= p.rows) return;  // uniform per wave; no barriers in this kernel
     const int lane = threadIdx.x & 63;
     const bf16_t* src = p.sbar + (int64_t)row * p.nb_pad;
@@ -42,7 +42,7 @@ hipError_t launch_pl(const TopkParams& p, hipStream_t s) {
 
 // Compressed-branch split combine alone (no selection): one wave per (batch, block).
 __global__ __launch_bounds__(256) void combine_kernel(CombineParams c, int rows, int nb) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));  // one per wave
     if (row >= rows) return;
     const int lane = threadIdx.x & 63;
     const int t = row % nb, b = row / nb;
