@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 6
+#define MOSAIC_BSA_ABI_VERSION 7
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -279,7 +279,8 @@ MOSAIC_API int mosaic_attn_topk_fwd(mosaic_bnhd q_cmp, mosaic_bnhd k_cmp, int32_
    calls it (MosaicBlock.norm1 / norm2, primitives.py:220-226; the U-Net's pre/post-processing
    and resampling norms, mosaic.py:163-217, primitives.py:313-359) and, with residual != NULL,
    the add in front of it (x + attention(...), primitives.py:225):
-     y = x + residual      rounded to dtype (written to sum_out, contiguous [rows, cols])
+     y = x + residual      rounded to dtype (written to sum_out, contiguous [rows, cols], when
+                           sum_out != NULL)
      out = y * rsqrt(mean(y^2) + eps) * weight      fp32 statistics, rounded once to out_dtype
    x, residual: dtype rows of cols contiguous elements, rows x_row_stride / residual_row_stride
    elements apart; out: out_dtype [rows, cols] contiguous; weight: optional fp32 [cols].
@@ -288,6 +289,23 @@ MOSAIC_API int mosaic_rms_norm_fwd(const void* x, const void* residual, int32_t 
                                    int32_t cols, int64_t x_row_stride, int64_t residual_row_stride,
                                    const float* weight, float eps, void* sum_out, void* out,
                                    int32_t out_dtype, void* stream);
+
+/* The epilogue of HEALPixUpsample / HEALPixDownsample.forward (primitives.py:313-359): the
+   split of the projection P, the broadcast position term, the skip connection and the RMSNorm
+   in one pass.  Output row R = (n factor + j) members + b of out ([coarse_rows * factor *
+   members, dim] bf16 contiguous, the sequence-first [(n f), B, d] layout) is
+     y = bf16(P[n members + b, j dim + c] + pos[n, j dim + c])        c < dim
+     y = bf16(y + shortcut[R, c])                                     (shortcut != NULL)
+     out = y * rsqrt(mean(y^2) + eps) * weight                        fp32 statistics
+   P: bf16 rows of factor * dim elements, p_row_stride apart; pos: bf16 [coarse_rows, factor *
+   dim] contiguous; shortcut: optional bf16 like out; weight: optional fp32 [dim].  factor = 1
+   without a shortcut is the downsampling epilogue (norm(proj_x(x) + proj_pos(rel_pos))).  dim a
+   multiple of 8, at most 4096; pointers 16-byte aligned.  No counterpart entry point in the
+   reference, which runs these as eager tensor ops. */
+MOSAIC_API int mosaic_resample_norm_fwd(const void* p, int64_t p_row_stride, const void* pos,
+                                        const void* shortcut, const float* weight, float eps,
+                                        int64_t coarse_rows, int32_t members, int32_t factor,
+                                        int32_t dim, void* out, void* stream);
 
 /* The SwiGLU gate of cSwiGLU.forward (primitives.py:102-105): with x1 = h[:, :hidden] and
    x3 = h[:, hidden:2*hidden], out = silu(x1 + noise[row % noise_rows]) * x3, each of the

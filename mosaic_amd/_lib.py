@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # mosaic_bsa_mode
 MODE_FULL = 0
@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_sparse_attn_bwd",
     "mosaic_rms_norm_fwd",
     "mosaic_swiglu_fwd",
+    "mosaic_resample_norm_fwd",
     "mosaic_swiglu_linear_fwd",
     "mosaic_sparse_attn_fwd",
     "mosaic_sparse_attn_fwd_workspace_size",
@@ -117,6 +118,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_rms_norm_fwd.restype = c_int
     lib.mosaic_swiglu_fwd.argtypes = [c_vp, c_i32, c_i64, c_i32, c_i64, c_vp, c_i32, c_vp, c_vp]
     lib.mosaic_swiglu_fwd.restype = c_int
+    lib.mosaic_resample_norm_fwd.argtypes = [c_vp, c_i64, c_vp, c_vp, c_vp, c_f, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp]
+    lib.mosaic_resample_norm_fwd.restype = c_int
     lib.mosaic_swiglu_linear_fwd.argtypes = [c_vp, c_i64, c_i32, c_i64, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp]
     lib.mosaic_swiglu_linear_fwd.restype = c_int
     lib.mosaic_sparse_attn_bwd_workspace_size.argtypes = [c_i32, c_i32, c_i32]

@@ -87,7 +87,7 @@ __global__ __launch_bounds__(kNormWaves * 64) void rms_norm_kernel(NormParams p)
                 load8(r + 8 * c, rv);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[i][e] = as_stored(v[i][e] + rv[e], x);
-                store8(static_cast<T*>(p.sum_out) + row * p.cols + 8 * c, v[i]);
+                if (p.sum_out) store8(static_cast<T*>(p.sum_out) + row * p.cols + 8 * c, v[i]);
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
@@ -133,6 +133,91 @@ hipError_t launch_norm_t(const NormParams& p, hipStream_t s) {
 template <typename T, typename TO>
 hipError_t launch_norm_res(const NormParams& p, hipStream_t s) {
     return p.res ? launch_norm_t<T, TO, true>(p, s) : launch_norm_t<T, TO, false>(p, s);
+}
+
+// HEALPix resampling epilogue (primitives.py:313-359): the resampled rows of the projection P
+// plus the broadcast position term, plus the skip connection, normalised:
+//   output row R = (n f + j) B + b  (sequence-first [(n f), B, d]) takes
+//   y = bf16(P[n B + b, j d .. j d + d) + pos[n, j d .. j d + d))     (the '(f d)' split)
+//   y = bf16(y + shortcut[R])                                        (upsampling only)
+//   out = y * rsqrt(mean(y^2) + eps) * weight
+// f = 1 with no shortcut is the downsampling epilogue.  One wave per output row; the eager
+// form is an add, a transposed copy, an add and the norm, each a pass over the activations.
+struct ResampleParams {
+    const bf16_t* p; const bf16_t* pos; const bf16_t* shortcut; const float* weight;
+    bf16_t* out;
+    int64_t rows, p_stride;
+    int members, factor, dim;
+    float eps;
+};
+
+template <int NCH, bool SC>
+__global__ __launch_bounds__(kNormWaves * 64) void resample_norm_kernel(ResampleParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kNormWaves + (threadIdx.x >> 6);
+    if (row >= p.rows) return;
+    const int64_t fb = (int64_t)p.factor * p.members;
+    const int64_t n = row / fb;
+    const int rem = (int)(row - n * fb);
+    const int j = rem / p.members, b = rem - j * p.members;
+    const bf16_t* prow = p.p + (n * p.members + b) * p.p_stride + (int64_t)j * p.dim;
+    const bf16_t* qrow = p.pos + n * ((int64_t)p.factor * p.dim) + (int64_t)j * p.dim;
+    const int nchunk = p.dim >> 3;
+    float v[NCH][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nchunk) {
+            float a[8];
+            load8(prow + 8 * c, v[i]);
+            load8(qrow + 8 * c, a);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[i][e] = round_bf16(v[i][e] + a[e]);
+            if (SC) {
+                load8(p.shortcut + row * p.dim + 8 * c, a);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[i][e] = round_bf16(v[i][e] + a[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+        }
+    }
+    const float inv = rsqrtf(wave_sum(ss) / (float)p.dim + p.eps);
+    bf16_t* out = p.out + row * p.dim;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nchunk) {
+            float o[8];
+            if (p.weight) {
+                const float* w = p.weight + 8 * c;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = v[i][e] * inv * w[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = v[i][e] * inv;
+            }
+            store8(out + 8 * c, o);
+        }
+    }
+}
+
+template <bool SC>
+hipError_t launch_resample_t(const ResampleParams& p, hipStream_t s) {
+    const unsigned grid = (unsigned)((p.rows + kNormWaves - 1) / kNormWaves);
+    void* args[] = {const_cast<ResampleParams*>(&p)};
+    const void* k = nullptr;
+    switch ((p.dim / 8 + 63) / 64) {
+        case 1: k = (const void*)&resample_norm_kernel<1, SC>; break;
+        case 2: k = (const void*)&resample_norm_kernel<2, SC>; break;
+        case 3: k = (const void*)&resample_norm_kernel<3, SC>; break;
+        case 4: k = (const void*)&resample_norm_kernel<4, SC>; break;
+        case 5: case 6: k = (const void*)&resample_norm_kernel<6, SC>; break;
+        case 7: case 8: k = (const void*)&resample_norm_kernel<8, SC>; break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipLaunchKernel(k, dim3(grid), dim3(kNormWaves * 64), args, 0, s);
 }
 
 struct GluParams {
@@ -197,7 +282,7 @@ int mosaic_rms_norm_fwd(const void* x, const void* residual, int32_t dtype, int6
     if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return MOSAIC_ERR_UNSUPPORTED;
     if (cols % 8 || cols > kMaxNormChunks * 64 * 8) return MOSAIC_ERR_UNSUPPORTED;
     if (rows > (int64_t)0x7fffffff * kNormWaves) return MOSAIC_ERR_SHAPE;
-    if (!x || !out || (residual && !sum_out)) return MOSAIC_ERR_NULL_POINTER;
+    if (!x || !out) return MOSAIC_ERR_NULL_POINTER;
     if (!aligned16(x) || !aligned16(out) || !chunk_stride(x_row_stride, dtype)) return MOSAIC_ERR_ALIGNMENT;
     if (residual && (!aligned16(residual) || !aligned16(sum_out) || !chunk_stride(residual_row_stride, dtype)))
         return MOSAIC_ERR_ALIGNMENT;
@@ -209,6 +294,24 @@ int mosaic_rms_norm_fwd(const void* x, const void* residual, int32_t dtype, int6
                                                      : launch_norm_res<bf16_t, float>(p, s));
     return status(out_dtype == MOSAIC_DTYPE_BF16 ? launch_norm_res<float, bf16_t>(p, s)
                                                  : launch_norm_res<float, float>(p, s));
+}
+
+int mosaic_resample_norm_fwd(const void* p, int64_t p_row_stride, const void* pos, const void* shortcut,
+                             const float* weight, float eps, int64_t coarse_rows, int32_t members,
+                             int32_t factor, int32_t dim, void* out, void* stream) {
+    if (coarse_rows <= 0 || members <= 0 || factor <= 0 || dim <= 0) return MOSAIC_ERR_SHAPE;
+    if (dim % 8 || dim > kMaxNormChunks * 64 * 8) return MOSAIC_ERR_UNSUPPORTED;
+    if (p_row_stride < (int64_t)factor * dim) return MOSAIC_ERR_SHAPE;
+    const int64_t rows = coarse_rows * factor * members;
+    if (rows / factor / members != coarse_rows || rows > (int64_t)0x7fffffff * kNormWaves) return MOSAIC_ERR_SHAPE;
+    if (!p || !pos || !out) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(p) || !aligned16(pos) || !aligned16(out) || p_row_stride % 8) return MOSAIC_ERR_ALIGNMENT;
+    if ((shortcut && !aligned16(shortcut)) || (weight && !aligned16(weight))) return MOSAIC_ERR_ALIGNMENT;
+    ResampleParams rp{static_cast<const bf16_t*>(p), static_cast<const bf16_t*>(pos),
+                      static_cast<const bf16_t*>(shortcut), weight, static_cast<bf16_t*>(out),
+                      rows, p_row_stride, members, factor, dim, eps};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    return status(shortcut ? launch_resample_t<true>(rp, s) : launch_resample_t<false>(rp, s));
 }
 
 int mosaic_swiglu_fwd(const void* h, int32_t dtype, int64_t rows, int32_t hidden, int64_t h_row_stride,

@@ -6,6 +6,9 @@
 * ``RMSNorm``: ``torch.nn.RMSNorm`` (same parameters) running ``rms_norm`` on a ROCm device,
   with ``add_forward`` for the residual-add variant.
 * ``swiglu(h, noise)``: the gate ``silu(x1 + noise) * x3`` of cSwiGLU (primitives.py:102-105).
+* ``resample_norm(p, pos, weight, eps, factor, shortcut)``: the epilogue of the HEALPix
+  up/downsampling layers (primitives.py:313-359): split, position term, skip connection and
+  RMSNorm in one pass.
 * ``swiglu_linear(x, w13_perm, noise)``: cSwiGLU's ``w13`` projection and that gate in one
   kernel (h is never stored); ``permute_w13`` lays out the weight it takes.
 
@@ -22,7 +25,8 @@ import torch.nn as nn
 from . import _lib
 from .ops import forward_only, stream_of
 
-__all__ = ["RMSNorm", "rms_norm", "swiglu", "swiglu_linear", "permute_w13", "swiglu_linear_ok", "autocast_dtype"]
+__all__ = ["RMSNorm", "rms_norm", "swiglu", "swiglu_linear", "permute_w13", "swiglu_linear_ok", "autocast_dtype",
+           "resample_norm"]
 
 _DT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
 _autocast_out: dict = {}
@@ -55,18 +59,21 @@ def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
-             out_dtype: torch.dtype | None = None, residual: torch.Tensor | None = None):
+             out_dtype: torch.dtype | None = None, residual: torch.Tensor | None = None,
+             return_sum: bool = True):
     """RMSNorm of ``x`` (or of ``x + residual``) over its last dimension.
 
     Returns ``out`` (dtype ``out_dtype``, default x's), or ``(x + residual, out)`` when a
-    residual is given; the sum has x's dtype, rounded as torch's add rounds.
+    residual is given; the sum has x's dtype, rounded as torch's add rounds.  With a residual
+    and ``return_sum=False`` only ``out`` is returned and the sum is never stored.
     """
     forward_only("fused.rms_norm", x, weight, residual)
     if not x.is_cuda:
         raise ValueError("fused.rms_norm needs a ROCm device tensor")
     if residual is not None and residual.dtype != x.dtype:
         x = x + residual                      # mixed dtypes: torch's promotion, then the plain norm
-        return x, rms_norm(x, weight, eps, out_dtype)
+        out = rms_norm(x, weight, eps, out_dtype)
+        return (x, out) if return_sum else out
     if x.dtype not in _DT:
         x = x.float()
     out_dtype = out_dtype or x.dtype
@@ -81,13 +88,14 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
     r2, rs, s_out = None, 0, None
     if residual is not None:
         r2, rs = _rows(residual.expand(shape))
-        s_out = torch.empty(shape, dtype=x.dtype, device=x.device)
+        if return_sum:
+            s_out = torch.empty(shape, dtype=x.dtype, device=x.device)
     st = _lib.lib().mosaic_rms_norm_fwd(
         x2.data_ptr(), r2.data_ptr() if r2 is not None else None, _DT[x.dtype], rows, C, xs, rs,
         w.data_ptr() if w is not None else None, float(DEFAULT_EPS if eps is None else eps),
         s_out.data_ptr() if s_out is not None else None, out.data_ptr(), _DT[out_dtype], stream_of(x))
     _lib.check(st, "mosaic_rms_norm_fwd")
-    return out if residual is None else (s_out, out)
+    return (s_out, out) if residual is not None and return_sum else out
 
 
 def swiglu(h: torch.Tensor, noise: torch.Tensor | None = None) -> torch.Tensor:
@@ -186,3 +194,49 @@ class RMSNorm(nn.RMSNorm):
             return y, out
         y = x + residual
         return y, self(y)
+
+    def add_norm(self, x: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """``self(x + residual)`` without storing the sum; on a ROCm device one kernel."""
+        if x.is_cuda and x.dtype == residual.dtype:
+            return rms_norm(x, self.weight, self.eps, out_dtype=autocast_dtype(x), residual=residual,
+                            return_sum=False)
+        return self(x + residual)
+
+
+def resample_norm(p: torch.Tensor, pos: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
+                  factor: int, shortcut: torch.Tensor | None = None) -> torch.Tensor:
+    """The epilogue of HEALPixUpsample / HEALPixDownsample (primitives.py:313-359) in one kernel:
+    ``rms_norm(split(p + pos[:, None]) (+ shortcut))`` where ``split`` is the
+    ``'n b (f d) -> (n f) b d'`` rearrangement.  p: bf16 ``[n, B, factor * d]`` (unit last
+    stride), pos: bf16 ``[n, factor * d]``, shortcut: bf16 ``[n * factor, B, d]`` or None.  The
+    adds round to bf16 as torch's bf16 adds do; the norm is ``rms_norm``'s.  Returns bf16
+    ``[n * factor, B, d]``."""
+    forward_only("fused.resample_norm", p, pos, shortcut, weight)
+    if p.dim() != 3 or p.dtype != torch.bfloat16 or not p.is_cuda:
+        raise ValueError("resample_norm needs a bf16 ROCm tensor p of shape [n, B, factor * d]")
+    n, B, fd = p.shape
+    if fd % factor:
+        raise ValueError(f"p's last dimension {fd} is not a multiple of factor {factor}")
+    d = fd // factor
+    if pos.shape != (n, fd) or pos.dtype != torch.bfloat16:
+        raise ValueError(f"pos must be bf16 [{n}, {fd}], got {tuple(pos.shape)} {pos.dtype}")
+    p2 = p.reshape(n * B, fd)
+    if p2.stride(-1) != 1 or p2.stride(0) % 8 or p2.data_ptr() % 16:
+        p2 = p2.contiguous()
+    pos = pos.contiguous()
+    sc = None
+    if shortcut is not None:
+        if shortcut.shape != (n * factor, B, d) or shortcut.dtype != torch.bfloat16:
+            raise ValueError(f"shortcut must be bf16 [{n * factor}, {B}, {d}], got {tuple(shortcut.shape)}")
+        sc = shortcut.contiguous()
+    w = None
+    if weight is not None:
+        w = weight.to(device=p.device, dtype=torch.float32).contiguous()
+    out = torch.empty(n * factor, B, d, dtype=torch.bfloat16, device=p.device)
+    st = _lib.lib().mosaic_resample_norm_fwd(p2.data_ptr(), p2.stride(0), pos.data_ptr(),
+                                             sc.data_ptr() if sc is not None else None,
+                                             w.data_ptr() if w is not None else None,
+                                             float(DEFAULT_EPS if eps is None else eps), n, B, factor, d,
+                                             out.data_ptr(), stream_of(p))
+    _lib.check(st, "mosaic_resample_norm_fwd")
+    return out

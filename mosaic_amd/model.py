@@ -233,6 +233,13 @@ def _child_offsets(nside_fine: int, nside_coarse: int) -> torch.Tensor:
     return ((rel - rel.mean(dim=0, keepdim=True)) / (rel.std(dim=0, keepdim=True) + 1e-6)).contiguous()
 
 
+def _bf16_epilogue(*ts: torch.Tensor) -> bool:
+    """Whether a resampling epilogue runs as fused.resample_norm: bf16 ROCm tensors whose
+    RMSNorm output would be bf16 too (the model under bf16 autocast)."""
+    return (all(t.is_cuda and t.dtype == torch.bfloat16 for t in ts)
+            and fused.autocast_dtype(ts[0]) == torch.bfloat16)
+
+
 class HEALPixDownsample(nn.Module):
     """Merge each coarse pixel's f children: ``norm(proj_x(concat children) + proj_pos(rel_pos))``
     (primitives.py:305-329).  The concat is a view of the NESTED sequence-first activations."""
@@ -251,8 +258,10 @@ class HEALPixDownsample(nn.Module):
         S, B, C = x.shape
         # '(n f) b c -> n b (f c)': pixel n*f + j, member b lands at [n, b, j*C:(j+1)*C]
         x = x.view(S // self.factor, self.factor, B, C).transpose(1, 2).reshape(S // self.factor, B, self.factor * C)
-        x = self.proj_x(x) + self.proj_pos(self.rel_pos).unsqueeze(1)
-        return self.norm(x)
+        p, pos = self.proj_x(x), self.proj_pos(self.rel_pos)
+        if _bf16_epilogue(p, pos):  # the add and the norm in one pass
+            return fused.resample_norm(p, pos, self.norm.weight, self.norm.eps, 1)
+        return self.norm(p + pos.unsqueeze(1))
 
 
 class HEALPixUpsample(nn.Module):
@@ -271,7 +280,10 @@ class HEALPixUpsample(nn.Module):
 
     def forward(self, x: torch.Tensor, shortcut: torch.Tensor) -> torch.Tensor:
         n, B, _ = x.shape
-        x = self.proj_x(x) + self.proj_pos(self.rel_pos).unsqueeze(1)
+        p, pos = self.proj_x(x), self.proj_pos(self.rel_pos)
+        if _bf16_epilogue(p, pos, shortcut):  # add, split, skip add and norm in one pass
+            return fused.resample_norm(p, pos, self.norm.weight, self.norm.eps, self.factor, shortcut)
+        x = p + pos.unsqueeze(1)
         # 'n b (f d) -> (n f) b d'
         x = x.view(n, B, self.factor, -1).transpose(1, 2).reshape(n * self.factor, B, -1)
         return self.norm(x + shortcut)
@@ -292,10 +304,16 @@ class UNetStage(nn.Module):
             for i in range(depth)])
 
     def forward(self, x: torch.Tensor, z: torch.Tensor | None = None) -> torch.Tensor:
+        x, pending = self.forward_pending(x, z)
+        return x if pending is None else x + pending
+
+    def forward_pending(self, x: torch.Tensor, z: torch.Tensor | None = None):
+        """The stage with its last residual add left undone: ``(x, pending)``, the output being
+        ``x + pending`` (pending None for a stage without blocks)."""
         pending = None
         for block in self.blocks:
             x, pending = block.forward_deferred(x, pending, z)
-        return x if pending is None else x + pending
+        return x, pending
 
 
 class Transformer(nn.Module):
@@ -435,10 +453,14 @@ class Transformer(nn.Module):
             skips.append(h)
             h = down(h)
         h = self.bottleneck(h, z)
-        for stage, up, skip in zip(self.decoder_stages, self.upsample_layers, reversed(skips)):
+        pending = None
+        for i, (stage, up, skip) in enumerate(zip(self.decoder_stages, self.upsample_layers, reversed(skips))):
             h = up(h, skip)
-            h = stage(h, z)
-        h = self.norm_before_interp_ll(h)
+            if i + 1 < len(self.decoder_stages):
+                h = stage(h, z)
+            else:  # the last stage's residual add goes into the norm after it
+                h, pending = stage.forward_pending(h, z)
+        h = self.norm_before_interp_ll(h) if pending is None else self.norm_before_interp_ll.add_norm(h, pending)
         h = self.interp_to_ll(h)
         h = self.postprocess(h)
         # '(lon lat) (b n s) c -> b (n s) lon lat c'

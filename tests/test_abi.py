@@ -227,10 +227,22 @@ def test_fused_elementwise_entries_validate():
     assert L.mosaic_rms_norm_fwd(FAKE, None, 5, 4, 768, 768, 0, None, 0.0, None, FAKE, BF, None) == 11
     assert L.mosaic_rms_norm_fwd(FAKE, None, BF, 4, 770, 770, 0, None, 0.0, None, FAKE, BF, None) == 11
     assert L.mosaic_rms_norm_fwd(FAKE, None, BF, 4, 8192, 8192, 0, None, 0.0, None, FAKE, BF, None) == 11
-    assert L.mosaic_rms_norm_fwd(FAKE, FAKE, BF, 4, 768, 768, 768, None, 0.0, None, FAKE, BF, None) == 1
+    # a residual without sum_out is valid (the sum is not stored): a misaligned residual still fails
+    assert L.mosaic_rms_norm_fwd(FAKE, FAKE + 2, BF, 4, 768, 768, 768, None, 0.0, None, FAKE, BF, None) == 7
     assert L.mosaic_rms_norm_fwd(None, None, BF, 4, 768, 768, 0, None, 0.0, None, FAKE, BF, None) == 1
     assert L.mosaic_rms_norm_fwd(FAKE + 2, None, BF, 4, 768, 768, 0, None, 0.0, None, FAKE, BF, None) == 7
     assert L.mosaic_rms_norm_fwd(FAKE, None, BF, 4, 768, 772, 0, None, 0.0, None, FAKE, F32, None) == 7
+    # resample_norm(p, p_stride, pos, shortcut, weight, eps, coarse_rows, members, factor, dim, out, stream)
+    rn = L.mosaic_resample_norm_fwd
+    assert rn(FAKE, 3072, FAKE, FAKE, None, 0.0, 0, 24, 4, 768, FAKE, None) == 8
+    assert rn(FAKE, 3072, FAKE, FAKE, None, 0.0, 16, 24, 4, 770, FAKE, None) == 11      # dim % 8
+    assert rn(FAKE, 32768, FAKE, None, None, 0.0, 16, 24, 1, 8192, FAKE, None) == 11    # dim > 4096
+    assert rn(FAKE, 3000, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, FAKE, None) == 8       # stride < factor * dim
+    assert rn(None, 3072, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, FAKE, None) == 1
+    assert rn(FAKE, 3072, None, FAKE, None, 0.0, 16, 24, 4, 768, FAKE, None) == 1
+    assert rn(FAKE, 3072, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, None, None) == 1
+    assert rn(FAKE, 3076, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, FAKE, None) == 7       # stride % 8
+    assert rn(FAKE, 3072, FAKE, FAKE + 4, None, 0.0, 16, 24, 4, 768, FAKE, None) == 7
     # swiglu(h, dtype, rows, hidden, h_stride, noise, noise_rows, out, stream)
     assert L.mosaic_swiglu_fwd(FAKE, BF, 0, 3072, 6144, None, 0, FAKE, None) == 8
     assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3070, 6140, None, 0, FAKE, None) == 11
