@@ -307,6 +307,16 @@ MOSAIC_API int mosaic_resample_norm_fwd(const void* p, int64_t p_row_stride, con
                                         int64_t coarse_rows, int32_t members, int32_t factor,
                                         int32_t dim, void* out, void* stream);
 
+/* MosaicAttention.generate_strategy_weights (primitives.py:173-180) on a bf16 logits slice:
+   w[s, b, n, h] = bf16(softmax_s(fp32 logits[n, b, 3 h + s])) for s < 3, the softmax computed
+   as torch.softmax(..., dim=0) computes it (max, exp of the differences, divided by their sum).
+   logits: bf16 rows (n, b) of 3 * heads elements, row n * members + b at logits_row_stride
+   elements (the sequence-first [seq, members, .] gate slice of a wider projection); w: bf16
+   [3, members, seq, heads] contiguous, the layout mosaic_bsa_args.weights takes with strides
+   (members seq heads, seq heads, heads, 1).  No counterpart entry point in the reference. */
+MOSAIC_API int mosaic_gate_softmax_fwd(const void* logits, int64_t logits_row_stride, int64_t seq,
+                                       int32_t members, int32_t heads, void* w, void* stream);
+
 /* The SwiGLU gate of cSwiGLU.forward (primitives.py:102-105): with x1 = h[:, :hidden] and
    x3 = h[:, hidden:2*hidden], out = silu(x1 + noise[row % noise_rows]) * x3, each of the
    add, the silu and the product rounded to dtype as the reference's eager ops round.

@@ -220,6 +220,35 @@ hipError_t launch_resample_t(const ResampleParams& p, hipStream_t s) {
     return hipLaunchKernel(k, dim3(grid), dim3(kNormWaves * 64), args, 0, s);
 }
 
+// generate_strategy_weights (primitives.py:173-180) on the gate slice of the stacked projection:
+//   w[s, b, n, h] = bf16(softmax over s of fp32(logits[n, b, 3 h + s]))
+// as torch.softmax(logits.float(), dim=0).type_as(x) computes it: m = max, e_s = exp(l_s - m),
+// w_s = e_s / (e_0 + e_1 + e_2).  One thread per (n, b, h); the eager form is a strided fp32
+// copy, a softmax launch over a dimension of 3 and a cast, each a separate pass.
+struct GateParams {
+    const bf16_t* logits; bf16_t* w;
+    int64_t rows, row_stride;  // rows = S * B, logits row (n, b) at (n B + b) row_stride
+    int members, heads;
+};
+
+__global__ __launch_bounds__(256) void gate_softmax_kernel(GateParams p) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= p.rows * p.heads) return;
+    const int64_t row = i / p.heads;
+    const int h = (int)(i - row * p.heads);
+    const bf16_t* l = p.logits + row * p.row_stride + 3 * h;
+    const float l0 = bf2f(l[0]), l1 = bf2f(l[1]), l2 = bf2f(l[2]);
+    const float m = fmaxf(fmaxf(l0, l1), l2);
+    const float e0 = expf(l0 - m), e1 = expf(l1 - m), e2 = expf(l2 - m);
+    const float sum = e0 + e1 + e2;
+    const int64_t n = row / p.members, b = row - n * p.members;
+    const int64_t plane = p.rows * p.heads;  // one [B, S, H] plane per branch s
+    bf16_t* w = p.w + (b * (p.rows / p.members) + n) * p.heads + h;
+    w[0] = (bf16_t)(pack_bf16x2(e0 / sum, 0.f) & 0xffffu);
+    w[plane] = (bf16_t)(pack_bf16x2(e1 / sum, 0.f) & 0xffffu);
+    w[2 * plane] = (bf16_t)(pack_bf16x2(e2 / sum, 0.f) & 0xffffu);
+}
+
 struct GluParams {
     const void* h; const void* noise; void* out;
     int64_t rows, h_stride;
@@ -312,6 +341,20 @@ int mosaic_resample_norm_fwd(const void* p, int64_t p_row_stride, const void* po
                       rows, p_row_stride, members, factor, dim, eps};
     hipStream_t s = static_cast<hipStream_t>(stream);
     return status(shortcut ? launch_resample_t<true>(rp, s) : launch_resample_t<false>(rp, s));
+}
+
+int mosaic_gate_softmax_fwd(const void* logits, int64_t logits_row_stride, int64_t seq, int32_t members,
+                            int32_t heads, void* w, void* stream) {
+    if (seq <= 0 || members <= 0 || heads <= 0) return MOSAIC_ERR_SHAPE;
+    if (logits_row_stride < 3 * (int64_t)heads) return MOSAIC_ERR_SHAPE;
+    const int64_t rows = seq * members, total = rows * heads;
+    if (rows / members != seq || total / heads != rows || (total + 255) / 256 > 0x7fffffff) return MOSAIC_ERR_SHAPE;
+    if (!logits || !w) return MOSAIC_ERR_NULL_POINTER;
+    if ((reinterpret_cast<uintptr_t>(logits) & 1u) || (reinterpret_cast<uintptr_t>(w) & 1u)) return MOSAIC_ERR_ALIGNMENT;
+    GateParams gp{static_cast<const bf16_t*>(logits), static_cast<bf16_t*>(w), rows, logits_row_stride, members, heads};
+    void* args[] = {&gp};
+    return status(hipLaunchKernel((const void*)gate_softmax_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                                  args, 0, static_cast<hipStream_t>(stream)));
 }
 
 int mosaic_swiglu_fwd(const void* h, int32_t dtype, int64_t rows, int32_t hidden, int64_t h_row_stride,

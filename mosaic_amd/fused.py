@@ -6,6 +6,8 @@
 * ``RMSNorm``: ``torch.nn.RMSNorm`` (same parameters) running ``rms_norm`` on a ROCm device,
   with ``add_forward`` for the residual-add variant.
 * ``swiglu(h, noise)``: the gate ``silu(x1 + noise) * x3`` of cSwiGLU (primitives.py:102-105).
+* ``gate_softmax(logits, heads)``: MosaicAttention's branch weights, the softmax over the three
+  logits of each head (primitives.py:173-180), from the projection's gate slice.
 * ``resample_norm(p, pos, weight, eps, factor, shortcut)``: the epilogue of the HEALPix
   up/downsampling layers (primitives.py:313-359): split, position term, skip connection and
   RMSNorm in one pass.
@@ -26,7 +28,7 @@ from . import _lib
 from .ops import forward_only, stream_of
 
 __all__ = ["RMSNorm", "rms_norm", "swiglu", "swiglu_linear", "permute_w13", "swiglu_linear_ok", "autocast_dtype",
-           "resample_norm"]
+           "resample_norm", "gate_softmax"]
 
 _DT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
 _autocast_out: dict = {}
@@ -240,3 +242,20 @@ def resample_norm(p: torch.Tensor, pos: torch.Tensor, weight: torch.Tensor | Non
                                              out.data_ptr(), stream_of(p))
     _lib.check(st, "mosaic_resample_norm_fwd")
     return out
+
+
+def gate_softmax(logits: torch.Tensor, heads: int) -> torch.Tensor:
+    """``torch.softmax(logits.unflatten(-1, (heads, 3)).permute(3, 1, 0, 2).float(), dim=0)``
+    rounded to bf16, in one kernel: logits bf16 ``[S, B, 3 * heads]`` sequence-first (a slice
+    of a wider projection is fine); returns bf16 ``[3, B, S, heads]``."""
+    forward_only("fused.gate_softmax", logits)
+    if logits.dim() != 3 or logits.dtype != torch.bfloat16 or not logits.is_cuda or logits.shape[-1] != 3 * heads:
+        raise ValueError(f"gate_softmax needs bf16 ROCm logits [S, B, {3 * heads}], got {tuple(logits.shape)}")
+    S, B, _ = logits.shape
+    if logits.stride(-1) != 1 or logits.stride(0) != B * logits.stride(1):
+        logits = logits.contiguous()
+    w = torch.empty(3, B, S, heads, dtype=torch.bfloat16, device=logits.device)
+    st = _lib.lib().mosaic_gate_softmax_fwd(logits.data_ptr(), logits.stride(1), S, B, heads, w.data_ptr(),
+                                            stream_of(logits))
+    _lib.check(st, "mosaic_gate_softmax_fwd")
+    return w

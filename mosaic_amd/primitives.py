@@ -21,7 +21,7 @@ import ctypes
 import torch
 import torch.nn as nn
 
-from . import _lib
+from . import _lib, fused
 from .healpix import rope_tables
 from .ops import _as_bf16_bnhd, _check_gqa, bnhd, forward_only, mosaic_sparse_attn, stream_of
 
@@ -531,8 +531,11 @@ class MosaicAttention(nn.Module):
         v = v.unflatten(-1, (self.kv_heads, -1)).transpose(0, 1)
         w = None
         if logits is not None:      # generate_strategy_weights on the fused GEMM's slice
-            logits = logits.unflatten(-1, (self.q_heads, 3)).permute(3, 1, 0, 2)
-            w = torch.softmax(logits.float(), dim=0).type_as(x).unsqueeze(-1)
+            if logits.is_cuda and logits.dtype == torch.bfloat16 and x.dtype == torch.bfloat16:
+                w = fused.gate_softmax(logits, self.q_heads).unsqueeze(-1)   # one pass, same values
+            else:
+                logits = logits.unflatten(-1, (self.q_heads, 3)).permute(3, 1, 0, 2)
+                w = torch.softmax(logits.float(), dim=0).type_as(x).unsqueeze(-1)
         args = dict(block_attn_size=self.block_attn_size, sparse_block_size=self.sparse_block_size,
                     sparse_block_count=self.sparse_block_count, block_attn_only=self.block_attn_only,
                     no_compression=self.no_compression)

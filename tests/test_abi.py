@@ -243,6 +243,13 @@ def test_fused_elementwise_entries_validate():
     assert rn(FAKE, 3072, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, None, None) == 1
     assert rn(FAKE, 3076, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, FAKE, None) == 7       # stride % 8
     assert rn(FAKE, 3072, FAKE, FAKE + 4, None, 0.0, 16, 24, 4, 768, FAKE, None) == 7
+    # gate_softmax(logits, row_stride, seq, members, heads, w, stream)
+    gs = L.mosaic_gate_softmax_fwd
+    assert gs(FAKE, 1280, 0, 24, 12, FAKE, None) == 8
+    assert gs(FAKE, 30, 100, 24, 12, FAKE, None) == 8          # row stride < 3 * heads
+    assert gs(None, 1280, 100, 24, 12, FAKE, None) == 1
+    assert gs(FAKE, 1280, 100, 24, 12, None, None) == 1
+    assert gs(FAKE + 1, 1280, 100, 24, 12, FAKE, None) == 7
     # swiglu(h, dtype, rows, hidden, h_stride, noise, noise_rows, out, stream)
     assert L.mosaic_swiglu_fwd(FAKE, BF, 0, 3072, 6144, None, 0, FAKE, None) == 8
     assert L.mosaic_swiglu_fwd(FAKE, BF, 4, 3070, 6140, None, 0, FAKE, None) == 11
