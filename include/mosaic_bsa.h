@@ -307,6 +307,16 @@ MOSAIC_API int mosaic_resample_norm_fwd(const void* p, int64_t p_row_stride, con
                                         int64_t coarse_rows, int32_t members, int32_t factor,
                                         int32_t dim, void* out, void* stream);
 
+/* The end of an encoder stage and the input of HEALPixDownsample (mosaic.py:318-321,
+   primitives.py:322-326): sum_out = bf16(x + residual) (bf16 [coarse_rows * factor * members,
+   dim] contiguous, the sequence-first [(n f), B, d] rows; the skip connection) and merged_out
+   = the same sums as [coarse_rows, members, factor * dim] ('(n f) b c -> n b (f c)'), the
+   downsampling projection's input.  x, residual: bf16 like sum_out.  dim a multiple of 8;
+   pointers 16-byte aligned.  No counterpart entry point in the reference. */
+MOSAIC_API int mosaic_add_merge_fwd(const void* x, const void* residual, int64_t coarse_rows,
+                                    int32_t members, int32_t factor, int32_t dim, void* sum_out,
+                                    void* merged_out, void* stream);
+
 /* MosaicAttention.generate_strategy_weights (primitives.py:173-180) on a bf16 logits slice:
    w[s, b, n, h] = bf16(softmax_s(fp32 logits[n, b, 3 h + s])) for s < 3, the softmax computed
    as torch.softmax(..., dim=0) computes it (max, exp of the differences, divided by their sum).

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_swiglu_fwd",
     "mosaic_resample_norm_fwd",
     "mosaic_gate_softmax_fwd",
+    "mosaic_add_merge_fwd",
     "mosaic_swiglu_linear_fwd",
     "mosaic_sparse_attn_fwd",
     "mosaic_sparse_attn_fwd_workspace_size",
@@ -123,6 +124,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_resample_norm_fwd.restype = c_int
     lib.mosaic_gate_softmax_fwd.argtypes = [c_vp, c_i64, c_i64, c_i32, c_i32, c_vp, c_vp]
     lib.mosaic_gate_softmax_fwd.restype = c_int
+    lib.mosaic_add_merge_fwd.argtypes = [c_vp, c_vp, c_i64, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp]
+    lib.mosaic_add_merge_fwd.restype = c_int
     lib.mosaic_swiglu_linear_fwd.argtypes = [c_vp, c_i64, c_i32, c_i64, c_vp, c_i32, c_vp, c_i32, c_vp, c_vp]
     lib.mosaic_swiglu_linear_fwd.restype = c_int
     lib.mosaic_sparse_attn_bwd_workspace_size.argtypes = [c_i32, c_i32, c_i32]

@@ -220,6 +220,35 @@ hipError_t launch_resample_t(const ResampleParams& p, hipStream_t s) {
     return hipLaunchKernel(k, dim3(grid), dim3(kNormWaves * 64), args, 0, s);
 }
 
+// The end of an encoder stage and the input of its downsampling (mosaic.py:318-321,
+// primitives.py:322-326): s = bf16(x + pending) (the stage's last residual add, kept as the skip
+// connection) and the same sums merged per coarse pixel, '(n f) b c -> n b (f c)', for the
+// downsampling projection.  One thread per 8-element chunk of s; both stores are 16 bytes.
+struct MergeParams {
+    const bf16_t* x; const bf16_t* r; bf16_t* s; bf16_t* merged;
+    int64_t rows;  // (n f) B rows of s
+    int members, factor, dim;
+};
+
+__global__ __launch_bounds__(256) void add_merge_kernel(MergeParams p) {
+    const int chunks = p.dim >> 3;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= p.rows * chunks) return;
+    const int64_t row = i / chunks;
+    const int c = (int)(i - row * chunks) * 8;
+    float a[8], b[8];
+    load8(p.x + row * p.dim + c, a);
+    load8(p.r + row * p.dim + c, b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = round_bf16(a[e] + b[e]);
+    store8(p.s + row * p.dim + c, a);
+    const int64_t fb = (int64_t)p.factor * p.members;
+    const int64_t n = row / fb;
+    const int rem = (int)(row - n * fb);
+    const int j = rem / p.members, m = rem - j * p.members;
+    store8(p.merged + ((n * p.members + m) * p.factor + j) * p.dim + c, a);
+}
+
 // generate_strategy_weights (primitives.py:173-180) on the gate slice of the stacked projection:
 //   w[s, b, n, h] = bf16(softmax over s of fp32(logits[n, b, 3 h + s]))
 // as torch.softmax(logits.float(), dim=0).type_as(x) computes it: m = max, e_s = exp(l_s - m),
@@ -343,6 +372,22 @@ int mosaic_resample_norm_fwd(const void* p, int64_t p_row_stride, const void* po
                       rows, p_row_stride, members, factor, dim, eps};
     hipStream_t s = static_cast<hipStream_t>(stream);
     return status(shortcut ? launch_resample_t<true>(rp, s) : launch_resample_t<false>(rp, s));
+}
+
+int mosaic_add_merge_fwd(const void* x, const void* residual, int64_t coarse_rows, int32_t members,
+                         int32_t factor, int32_t dim, void* sum_out, void* merged_out, void* stream) {
+    if (coarse_rows <= 0 || members <= 0 || factor <= 0 || dim <= 0) return MOSAIC_ERR_SHAPE;
+    if (dim % 8) return MOSAIC_ERR_UNSUPPORTED;
+    const int64_t rows = coarse_rows * factor * members, total = rows * (dim / 8);
+    if (rows / factor / members != coarse_rows || (total + 255) / 256 > 0x7fffffff) return MOSAIC_ERR_SHAPE;
+    if (!x || !residual || !sum_out || !merged_out) return MOSAIC_ERR_NULL_POINTER;
+    if (!aligned16(x) || !aligned16(residual) || !aligned16(sum_out) || !aligned16(merged_out))
+        return MOSAIC_ERR_ALIGNMENT;
+    MergeParams mp{static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(residual), static_cast<bf16_t*>(sum_out),
+                   static_cast<bf16_t*>(merged_out), rows, members, factor, dim};
+    void* args[] = {&mp};
+    return status(hipLaunchKernel((const void*)add_merge_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                                  args, 0, static_cast<hipStream_t>(stream)));
 }
 
 int mosaic_gate_softmax_fwd(const void* logits, int64_t logits_row_stride, int64_t seq, int32_t members,

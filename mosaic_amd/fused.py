@@ -6,6 +6,8 @@
 * ``RMSNorm``: ``torch.nn.RMSNorm`` (same parameters) running ``rms_norm`` on a ROCm device,
   with ``add_forward`` for the residual-add variant.
 * ``swiglu(h, noise)``: the gate ``silu(x1 + noise) * x3`` of cSwiGLU (primitives.py:102-105).
+* ``add_merge(x, residual, factor)``: an encoder stage's last residual add and the merge of each
+  coarse pixel's children for the downsampling projection (mosaic.py:318-321), one pass.
 * ``gate_softmax(logits, heads)``: MosaicAttention's branch weights, the softmax over the three
   logits of each head (primitives.py:173-180), from the projection's gate slice.
 * ``resample_norm(p, pos, weight, eps, factor, shortcut)``: the epilogue of the HEALPix
@@ -28,7 +30,7 @@ from . import _lib
 from .ops import forward_only, stream_of
 
 __all__ = ["RMSNorm", "rms_norm", "swiglu", "swiglu_linear", "permute_w13", "swiglu_linear_ok", "autocast_dtype",
-           "resample_norm", "gate_softmax"]
+           "resample_norm", "gate_softmax", "add_merge"]
 
 _DT = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
 _autocast_out: dict = {}
@@ -259,3 +261,24 @@ def gate_softmax(logits: torch.Tensor, heads: int) -> torch.Tensor:
                                             stream_of(logits))
     _lib.check(st, "mosaic_gate_softmax_fwd")
     return w
+
+
+def add_merge(x: torch.Tensor, residual: torch.Tensor, factor: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``s = x + residual`` (bf16, rounded as torch's add) and ``s`` merged per coarse pixel,
+    ``s.view(n, f, B, C).transpose(1, 2).reshape(n, B, f * C)``, in one kernel.  x, residual:
+    bf16 ``[n * factor, B, C]``; returns ``(s, merged)``."""
+    forward_only("fused.add_merge", x, residual)
+    if x.dim() != 3 or x.dtype != torch.bfloat16 or residual.dtype != torch.bfloat16 or not x.is_cuda:
+        raise ValueError("add_merge needs bf16 ROCm tensors [n * factor, B, C]")
+    if residual.shape != x.shape:
+        raise ValueError(f"residual {tuple(residual.shape)} does not match x {tuple(x.shape)}")
+    S, B, C = x.shape
+    if S % factor:
+        raise ValueError(f"{S} rows are not a multiple of factor {factor}")
+    x, residual = x.contiguous(), residual.contiguous()
+    s = torch.empty_like(x)
+    merged = torch.empty(S // factor, B, factor * C, dtype=torch.bfloat16, device=x.device)
+    st = _lib.lib().mosaic_add_merge_fwd(x.data_ptr(), residual.data_ptr(), S // factor, B, factor, C,
+                                         s.data_ptr(), merged.data_ptr(), stream_of(x))
+    _lib.check(st, "mosaic_add_merge_fwd")
+    return s, merged

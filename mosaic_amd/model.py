@@ -258,6 +258,10 @@ class HEALPixDownsample(nn.Module):
         S, B, C = x.shape
         # '(n f) b c -> n b (f c)': pixel n*f + j, member b lands at [n, b, j*C:(j+1)*C]
         x = x.view(S // self.factor, self.factor, B, C).transpose(1, 2).reshape(S // self.factor, B, self.factor * C)
+        return self.forward_merged(x)
+
+    def forward_merged(self, x: torch.Tensor) -> torch.Tensor:
+        """forward on the children already merged per coarse pixel, ``[n, B, f * C]``."""
         p, pos = self.proj_x(x), self.proj_pos(self.rel_pos)
         if _bf16_epilogue(p, pos):  # the add and the norm in one pass
             return fused.resample_norm(p, pos, self.norm.weight, self.norm.eps, 1)
@@ -449,9 +453,16 @@ class Transformer(nn.Module):
         h = self.interp_to_hp(h)
         skips = []
         for stage, down in zip(self.encoder_stages, self.downsample_layers):
-            h = stage(h, z)
-            skips.append(h)
-            h = down(h)
+            h, pending = stage.forward_pending(h, z)
+            if pending is not None and _bf16_epilogue(h, pending):
+                # the stage's last add and the merge of the children in one pass
+                h, merged = fused.add_merge(h, pending, down.factor)
+                skips.append(h)
+                h = down.forward_merged(merged)
+            else:
+                h = h if pending is None else h + pending
+                skips.append(h)
+                h = down(h)
         h = self.bottleneck(h, z)
         pending = None
         for i, (stage, up, skip) in enumerate(zip(self.decoder_stages, self.upsample_layers, reversed(skips))):

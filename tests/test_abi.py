@@ -243,6 +243,13 @@ def test_fused_elementwise_entries_validate():
     assert rn(FAKE, 3072, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, None, None) == 1
     assert rn(FAKE, 3076, FAKE, FAKE, None, 0.0, 16, 24, 4, 768, FAKE, None) == 7       # stride % 8
     assert rn(FAKE, 3072, FAKE, FAKE + 4, None, 0.0, 16, 24, 4, 768, FAKE, None) == 7
+    # add_merge(x, residual, coarse_rows, members, factor, dim, sum_out, merged_out, stream)
+    am = L.mosaic_add_merge_fwd
+    assert am(FAKE, FAKE, 0, 24, 4, 768, FAKE, FAKE, None) == 8
+    assert am(FAKE, FAKE, 16, 24, 4, 770, FAKE, FAKE, None) == 11
+    assert am(FAKE, None, 16, 24, 4, 768, FAKE, FAKE, None) == 1
+    assert am(FAKE, FAKE, 16, 24, 4, 768, FAKE, None, None) == 1
+    assert am(FAKE, FAKE, 16, 24, 4, 768, FAKE + 8, FAKE, None) == 7
     # gate_softmax(logits, row_stride, seq, members, heads, w, stream)
     gs = L.mosaic_gate_softmax_fwd
     assert gs(FAKE, 1280, 0, 24, 12, FAKE, None) == 8

@@ -102,3 +102,18 @@ def test_resample_norm_refuses_grad():
     w.requires_grad_(True)
     with pytest.raises(RuntimeError, match="no backward"):
         fused.resample_norm(p, pos, w, None, 4, sc)
+
+
+@pytest.mark.parametrize("n,B,f,C", [(192, 24, 4, 768), (48, 3, 4, 1024), (7, 5, 1, 96)])
+def test_add_merge_matches_eager(n, B, f, C):
+    """An encoder stage's last residual add and the merge of the children
+    ('(n f) b c -> n b (f c)') for the downsampling projection."""
+    print(f"add_merge n={n} B={B} f={f} C={C}", flush=True)
+    g = torch.Generator().manual_seed(n + C)
+    x = torch.randn(n * f, B, C, generator=g).to(torch.bfloat16).to(DEV)
+    r = torch.randn(n * f, B, C, generator=g).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        s, merged = fused.add_merge(x, r, f)
+        ref = x + r
+        ref_m = ref.view(n, f, B, C).transpose(1, 2).reshape(n, B, f * C)
+    assert torch.equal(s, ref) and torch.equal(merged, ref_m)
