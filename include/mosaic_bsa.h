@@ -118,7 +118,10 @@ MOSAIC_API int mosaic_bsa_fwd(const mosaic_bsa_args* args, void* workspace, size
    launch (128 MiB covers e.g. N = 196608 with 12/3 heads and 64-token blocks, or 24 members of
    N = 12288 with 16/4 heads).  Every call on one GPU shares that GPU's array, which keeps the
    last call's contents: calls that overlap on one GPU (unordered streams, or threads) race
-   and corrupt each other's results. */
+   and corrupt each other's results.  HIP loads the library's code object on a device (and
+   places the static array there) at the first launch of any library kernel on it: make one
+   call on each device before capturing a HIP graph, so that the load and the address lookup
+   do not happen under capture. */
 MOSAIC_API int mosaic_bsa_fwd_noalloc(const mosaic_bsa_args* args, void* stream);
 
 /* As mosaic_bsa_fwd, recording events[0..4] (hipEvent_t) on the stream before the pooling

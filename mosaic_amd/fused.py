@@ -53,6 +53,10 @@ def autocast_dtype(x: torch.Tensor) -> torch.dtype:
     return dt
 
 
+def _on_device(t: torch.Tensor) -> bool:
+    return t.is_cuda
+
+
 def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     """t as [rows, cols] with a unit last stride and one row stride (copying if needed)."""
     t2 = t.reshape(-1, t.shape[-1])
@@ -72,15 +76,19 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float | None,
     and ``return_sum=False`` only ``out`` is returned and the sum is never stored.
     """
     forward_only("fused.rms_norm", x, weight, residual)
-    if not x.is_cuda:
+    if not _on_device(x):
         raise ValueError("fused.rms_norm needs a ROCm device tensor")
-    if residual is not None and residual.dtype != x.dtype:
-        x = x + residual                      # mixed dtypes: torch's promotion, then the plain norm
+    if residual is not None and (residual.dtype != x.dtype or x.dtype not in _DT):
+        # mixed dtypes, or a pair the kernel does not read (fp16, fp64): torch's add with its
+        # promotion and rounding, then the plain norm of the sum
+        x = x + residual
         out = rms_norm(x, weight, eps, out_dtype)
         return (x, out) if return_sum else out
-    if x.dtype not in _DT:
-        x = x.float()
     out_dtype = out_dtype or x.dtype
+    if x.dtype not in _DT:
+        x = x.float()                         # statistics in fp32 either way
+    if out_dtype not in _DT:                  # the kernel writes fp32, then torch's cast
+        return rms_norm(x, weight, eps, torch.float32).to(out_dtype)
     shape = x.shape
     C = shape[-1]
     x2, xs = _rows(x)

@@ -10,8 +10,10 @@ projections are library GEMMs; the RMSNorms and the SwiGLU gate run as the fused
 ``mosaic_amd.fused`` when their inputs are on a ROCm device.
 
 Activations are sequence-first ``[S, B, C]`` (S pixels, B = members x noise samples), as in
-the reference.  The model is meant to run under ``torch.autocast('cuda', torch.bfloat16)``,
-as the reference's inference does (inference.py:379).
+the reference.  The model runs under ``torch.autocast('cuda', torch.bfloat16)``.  The
+reference's inference autocasts to ``DTYPE = torch.float16`` (inference.py:59, 379); the
+attention op and the interpolation kernel here compute in bf16 only and refuse fp16 inputs
+with a ``TypeError``, so a caller keeps bf16 autocast.
 """
 
 from __future__ import annotations

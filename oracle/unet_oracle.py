@@ -66,7 +66,8 @@ def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor
     return torch.stack([even * c - odd * s, odd * c + even * s], dim=-1).flatten(-2).to(x.dtype)
 
 
-def mosaic_attention(P: dict, pre: str, x: torch.Tensor, cfg, norm_dtype: dict, indices=None) -> torch.Tensor:
+def mosaic_attention(P: dict, pre: str, x: torch.Tensor, cfg, norm_dtype: dict, indices=None,
+                     band_stats=None) -> torch.Tensor:
     Hq = cfg.num_heads
     Hk = Hq // cfg.gqa_ratio
     q = rearrange(linear(x, P[pre + "to_q.weight"]), "s b (h d) -> b s h d", h=Hq)
@@ -78,13 +79,26 @@ def mosaic_attention(P: dict, pre: str, x: torch.Tensor, cfg, norm_dtype: dict, 
         q = _rope(q, P[pre + "q_rope.cos_freqs"], P[pre + "q_rope.sin_freqs"])
         k = _rope(k, P[pre + "k_rope.cos_freqs"], P[pre + "k_rope.sin_freqs"])
     idx = next(indices).cpu() if indices is not None else None
+    if idx is not None and band_stats is not None:
+        # the given selection against this oracle's own scores (primitives.py:35-51): blocks
+        # may differ only where the scores tie within the band
+        bs = cfg.sparse_block_size
+        scores = bsa_oracle.topk_scores(bsa_oracle.pool_mean(q, bs), bsa_oracle.pool_mean(k, bs)).permute(0, 2, 1, 3)
+        band = band_stats["rel_band"] * scores.float().abs().max().item()
+        bad, amb, rows = bsa_oracle.selection_band_check(scores, idx, cfg.sparse_block_count, band)
+        rec = {"bad": bad, "ambiguous": amb, "rows": rows, "band": band}
+        if band_stats.get("planted") is not None:  # a deliberately wrong selection must fail
+            rec["bad_planted"] = bsa_oracle.selection_band_check(scores, band_stats["planted"](idx),
+                                                                 cfg.sparse_block_count, band)[0]
+        band_stats["calls"].append(rec)
     o = bsa_oracle.mosaic_attn_func(q, k, v.to(BF16), w.to(BF16), cfg.block_attn_size, cfg.sparse_block_size,
                                     cfg.sparse_block_count, False, block_indices=idx)
     return linear(rearrange(o, "b s h d -> s b (h d)"), P[pre + "to_o.weight"])
 
 
-def mosaic_block(P: dict, pre: str, x: torch.Tensor, z, cfg, norm_dtype: dict, indices=None) -> torch.Tensor:
-    x = x + mosaic_attention(P, pre + "attention.", rms_norm(x, norm_dtype), cfg, norm_dtype, indices)
+def mosaic_block(P: dict, pre: str, x: torch.Tensor, z, cfg, norm_dtype: dict, indices=None,
+                 band_stats=None) -> torch.Tensor:
+    x = x + mosaic_attention(P, pre + "attention.", rms_norm(x, norm_dtype), cfg, norm_dtype, indices, band_stats)
     return x + cswiglu(P, pre + "ffn.", rms_norm(x, norm_dtype), z)
 
 
@@ -119,12 +133,20 @@ def _stage_cfg(config, stage_cfg):
 
 
 def forward(P: dict, config, x: torch.Tensor, day_year_time: torch.Tensor, num_noise_samples: int,
-            noise: torch.Tensor | None, norm_dtype: dict, block_indices=None) -> torch.Tensor:
+            noise: torch.Tensor | None, norm_dtype: dict, block_indices=None, band_stats=None) -> torch.Tensor:
     """The Transformer forward (mosaic.py:304-337) on CPU tensors; P = the model's state dict.
 
     ``block_indices``: optional list of the selected block indices of every attention call, in
     call order (encoder blocks, bottleneck, decoder blocks); each replaces the oracle's own
-    top-k there, so the forward can be evaluated on a device's selection where scores tie."""
+    top-k there, so the forward can be evaluated on a device's selection where scores tie.
+
+    ``band_stats``: with ``block_indices``, a dict ``{"rel_band": r, "calls": []}``; every
+    attention call then checks the given indices against this oracle's own selection scores
+    with ``selection_band_check`` at band ``r * max|S-bar|`` of that call and appends
+    ``{"bad", "ambiguous", "rows", "band"}`` to ``calls``; with a callable ``"planted"`` in the
+    dict, the indices it returns for the given ones are checked as well (``"bad_planted"``).  The band is relative because the
+    given indices come from a device whose projections may round q and k differently in
+    the last place."""
     it = iter(block_indices) if block_indices is not None else None
     P = {k: v.detach().cpu() for k, v in P.items()}
     b, n, t, lon, lat, c = x.shape
@@ -149,17 +171,17 @@ def forward(P: dict, config, x: torch.Tensor, day_year_time: torch.Tensor, num_n
     skips = []
     for i, st in enumerate(config.cg_stage_cfgs):
         for j in range(st.encoder_depth):
-            h = mosaic_block(P, f"encoder_stages.{i}.blocks.{j}.", h, z, _stage_cfg(config, st), norm_dtype, it)
+            h = mosaic_block(P, f"encoder_stages.{i}.blocks.{j}.", h, z, _stage_cfg(config, st), norm_dtype, it, band_stats)
         skips.append(h)
         h = downsample(P, f"downsample_layers.{i}.", h, (st.nside // stages[i + 1].nside) ** 2, norm_dtype)
     bc = config.bottleneck_cfg
     for j in range(bc.depth):
-        h = mosaic_block(P, f"bottleneck.blocks.{j}.", h, z, _stage_cfg(config, bc), norm_dtype, it)
+        h = mosaic_block(P, f"bottleneck.blocks.{j}.", h, z, _stage_cfg(config, bc), norm_dtype, it, band_stats)
     for u, i in enumerate(reversed(range(len(config.cg_stage_cfgs)))):
         st = stages[i]
         h = upsample(P, f"upsample_layers.{u}.", h, skips[i], (st.nside // stages[i + 1].nside) ** 2, norm_dtype)
         for j in range(st.decoder_depth):
-            h = mosaic_block(P, f"decoder_stages.{u}.blocks.{j}.", h, z, _stage_cfg(config, st), norm_dtype, it)
+            h = mosaic_block(P, f"decoder_stages.{u}.blocks.{j}.", h, z, _stage_cfg(config, st), norm_dtype, it, band_stats)
     h = rms_norm(h, norm_dtype)
     h = interpolate(P, "interp_to_ll.", h, config.num_heads, norm_dtype)
     h = rms_norm(h, norm_dtype)

@@ -178,7 +178,21 @@ def test_unet_forward_matches_oracle(selective):
     gen = torch.Generator(device=DEV)
     gen.manual_seed(11)
     noise = torch.randn((S, cfg.noise_dim), generator=gen, device=DEV, dtype=torch.float32).cpu()
-    ref = unet_oracle.forward(model.state_dict(), cfg, x, dyt, S, noise, probe, block_indices=recorded)
+    # the recorded selections are checked against the oracle's own scores at every call; the
+    # band is relative (2% of the call's largest score) because the oracle's q / k come from
+    # its own projections, a few bf16 spacings away from the device's after several layers
+    stats = {"rel_band": 2e-2, "calls": [],
+             "planted": lambda idx: (idx + 1) % idx.shape[1]}   # every selected block shifted by one
+    ref = unet_oracle.forward(model.state_dict(), cfg, x, dyt, S, noise, probe, block_indices=recorded,
+                              band_stats=stats)
+    for c in stats["calls"]:
+        print(f"selection vs oracle scores: {c}", flush=True)
+    assert len(stats["calls"]) == 5
+    assert all(c["bad"] == 0 for c in stats["calls"]), stats["calls"]
+    if selective:
+        decided = sum(c["rows"] - c["ambiguous"] for c in stats["calls"])
+        assert decided >= 0.5 * sum(c["rows"] for c in stats["calls"]), "band too wide to decide most rows"
+        assert all(c["bad_planted"] > 0 for c in stats["calls"][:2]), "shifted selections passed the band rule"
     got = out.float().cpu()
     r = ref.float()
     assert got.shape == r.shape == (1, S, 24, 13, 5), (got.shape, r.shape)

@@ -107,3 +107,33 @@ def test_backward_validates_shapes(change, monkeypatch):
         bs = 96
     with pytest.raises(ValueError):
         ops.mosaic_attn_bwd(q, k, v, o, lse, go, 0.125, idx, bs)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float64])
+@pytest.mark.parametrize("return_sum", [True, False])
+def test_rms_norm_residual_pairs_the_kernel_does_not_read_never_reach_it(dtype, return_sum, monkeypatch):
+    # x and residual share a dtype the kernel does not take: the kernel must only ever see
+    # buffers whose dtype matches the dtype code it is given (an fp16 residual passed as fp32
+    # would be read past its end).  The launch is recorded instead of run.
+    calls = []
+
+    class FakeLib:
+        def mosaic_rms_norm_fwd(self, x, r, dt, rows, C, xs, rs, w, eps, s_out, out, out_dt, stream):
+            calls.append(dict(x=x, r=r, dt=dt, out_dt=out_dt, rows=rows, C=C, xs=xs, rs=rs))
+            return 0
+
+    monkeypatch.setattr(fused, "_on_device", lambda x: True)
+    monkeypatch.setattr(fused, "stream_of", lambda x: 0)
+    monkeypatch.setattr(fused._lib, "lib", lambda: FakeLib())
+    x = torch.randn(4, 64).to(dtype)
+    res = torch.randn(4, 64).to(dtype)
+    out = fused.rms_norm(x, None, None, residual=res, return_sum=return_sum)
+    assert len(calls) == 1
+    call = calls[0]
+    assert call["r"] is None                   # the sum was formed by torch, not by the kernel
+    assert call["dt"] == fused._lib.DTYPE_F32  # the kernel read an fp32 copy of the sum
+    assert call["xs"] == 64 and call["rows"] == 4 and call["C"] == 64
+    if return_sum:
+        s, out = out
+        assert s.dtype == dtype and torch.equal(s, x + res)
+    assert out.dtype == dtype                  # torch.nn.RMSNorm's output dtype for this input
