@@ -498,10 +498,9 @@ void bsa_attn_kernel(AttnParams p) {
 
     // ------------------------------------------------------------------ local branch
     if constexpr (kLocal) {
-        auto local_step = [&](auto bufc, int t) {
-            const int BUF = bufc;  // compile-time (Buf0 / Buf1) or runtime (t & 1)
-            const bf16_t* Kc = BUF ? Ks1 : Ks0;
-            const bf16_t* Vc = BUF ? Vs1 : Vs0;
+        // Start of local tile t: tile 0 of the modes with a partial buffer first takes the Q rows
+        // staged in the prologue (and rotates them).
+        auto local_begin = [&](auto bufc, int t) {
             if (kPartial && t == 0) {
                 wait_vmem();
                 __syncthreads();
@@ -534,6 +533,13 @@ void bsa_attn_kernel(AttnParams p) {
             } else {
                 begin_tile(bufc, t);
             }
+        };
+        // The tile's compute.  The buffer is a compile-time choice (Buf0 / Buf1): with a runtime
+        // choice the compiler cannot tell the buffer read here from the one the next tile's
+        // loads are landing in, and it waits for those loads before the first V read.
+        auto local_run = [&](auto bufc, int t) {
+            const bf16_t* Kc = decltype(bufc)::value ? Ks1 : Ks0;
+            const bf16_t* Vc = decltype(bufc)::value ? Vs1 : Vs0;
             s_tile(Kc, ro, qf, s);
             float mt[2];
             bool need = false;
@@ -562,18 +568,15 @@ void bsa_attn_kernel(AttnParams p) {
             l[1] += lt[1];
             pv_tile(Vc, ro, pb, o);
         };
-        if constexpr (MODE == kModeLocalOnly) {  // the local tiles are the hot loop
-            int t = 0;
-            for (; t + 1 < tl_count; t += 2) {
-                local_step(Buf0{}, t);
-                local_step(Buf1{}, t + 1);
-            }
-            if (t < tl_count) local_step(Buf0{}, t);
-        } else {
-            // one copy of the local step (runtime buffer): the selected loop is the hot one,
-            // and the kernel's code stays small in the instruction cache
-#pragma clang loop unroll(disable)
-            for (int t = 0; t < tl_count; ++t) local_step(t & 1, t);
+        // tile 0 (with the Q rows), then the rest in pairs over the two buffers
+        local_begin(Buf0{}, 0);
+        local_run(Buf0{}, 0);
+        for (int t = 1; t < tl_count; t += 2) {
+            begin_tile(Buf1{}, t);
+            local_run(Buf1{}, t);
+            if (t + 1 >= tl_count) break;
+            begin_tile(Buf0{}, t + 1);
+            local_run(Buf0{}, t + 1);
         }
         float inv[2];
 #pragma unroll
