@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 7
+#define MOSAIC_BSA_ABI_VERSION 8
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -130,6 +130,24 @@ MOSAIC_API int mosaic_bsa_fwd_noalloc(const mosaic_bsa_args* args, void* stream)
    the measurement hook of the benchmark. */
 MOSAIC_API int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* workspace,
                             size_t workspace_bytes, void* stream, void* const* events);
+
+/* Stages of the full forward, in launch order (mosaic_bsa_fwd_stage). */
+typedef enum {
+    MOSAIC_BSA_STAGE_POOL = 0,   /* pooling (with RoPE where the entry fuses it) */
+    MOSAIC_BSA_STAGE_CMP = 1,    /* compressed attention partials + selection scores */
+    MOSAIC_BSA_STAGE_TOPK = 2,   /* top-k selection + split combine (combine alone without selection) */
+    MOSAIC_BSA_STAGE_ATTN = 3    /* fused local + selected attention with the merge */
+} mosaic_bsa_stage;
+
+/* One stage of mosaic_bsa_fwd alone: the same validation, then only that stage's launch,
+   reading what the earlier stages left in the workspace.  The workspace must hold the
+   results of a complete mosaic_bsa_fwd with the same args (and the same inputs, for the
+   outputs to be the op's); each stage rewrites exactly what it wrote in that call, so
+   repeating a stage is idempotent.  A stage the mode does not run returns MOSAIC_OK and
+   launches nothing.  No reference counterpart: it lets a caller time each kernel on its own
+   with plain launches (no events between the kernels of a call). */
+MOSAIC_API int mosaic_bsa_fwd_stage(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes,
+                                    void* stream, int stage);
 
 /* Full forward with the input side's 2-D RoPE fused into the pooling pass: q and k are
    rotated as the caller's RoPE modules rotate them (primitives.py:125-135, applied at

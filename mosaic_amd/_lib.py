@@ -12,13 +12,19 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # mosaic_bsa_mode
 MODE_FULL = 0
 MODE_LOCAL_ONLY = 1
 MODE_NO_COMPRESSION = 2
 MODE_NO_SELECTION = 3
+
+# mosaic_bsa_stage (mosaic_bsa_fwd_stage)
+STAGE_POOL = 0
+STAGE_CMP = 1
+STAGE_TOPK = 2
+STAGE_ATTN = 3
 
 # mosaic_status values the Python side names
 ERR_SCRATCH_LIMIT = 12
@@ -33,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_bsa_fwd",
     "mosaic_bsa_fwd_noalloc",
     "mosaic_bsa_fwd_profiled",
+    "mosaic_bsa_fwd_stage",
     "mosaic_bsa_fwd_rope",
     "mosaic_bsa_fwd_proj",
     "mosaic_knn_interp_fwd",
@@ -107,6 +114,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_bsa_fwd_noalloc.restype = c_int
     lib.mosaic_bsa_fwd_profiled.argtypes = [P(BsaArgs), c_vp, c_size, c_vp, P(c_vp)]
     lib.mosaic_bsa_fwd_profiled.restype = c_int
+    lib.mosaic_bsa_fwd_stage.argtypes = [P(BsaArgs), c_vp, c_size, c_vp, c_int]
+    lib.mosaic_bsa_fwd_stage.restype = c_int
     lib.mosaic_bsa_fwd_rope.argtypes = [P(BsaArgs), c_vp, c_vp, c_vp, c_vp, c_vp, c_size, c_vp]
     lib.mosaic_bsa_fwd_rope.restype = c_int
     lib.mosaic_bsa_fwd_proj.argtypes = [P(BsaArgs), P(ProjArgs), c_vp, c_size, c_vp]

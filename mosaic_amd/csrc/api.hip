@@ -188,9 +188,12 @@ struct RopeIO {
 
 // proj: the input side's projection kernel runs in place of the pooling pass (its q, k, v,
 // weights and pooled outputs feed the later kernels; a's q / k / v / weights point at them)
+// stages: bit k launches stage k (mosaic_bsa_stage); all four for a whole forward.
+constexpr unsigned kAllStages = 0xfu;
 int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* stream, void* const* events,
-                const RopeIO* rope = nullptr, const ProjParams* proj = nullptr) {
+                const RopeIO* rope = nullptr, const ProjParams* proj = nullptr, unsigned stages = kAllStages) {
     if (int e = validate(a)) return e;
+    auto run = [stages](int stage) { return (stages >> stage) & 1u; };
     // With RoPE, the modes with both local and selected branches rotate q inside the attention
     // kernel, so the rotated q is an optional output there; the other modes read it back.
     const bool q_in_kernel = a->mode == MOSAIC_BSA_FULL || a->mode == MOSAIC_BSA_NO_COMPRESSION;
@@ -261,10 +264,12 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
             ProjParams jp = *proj;
             jp.bs = a->sparse_block_size; jp.nb = L.nb; jp.nb_pad = L.nb_pad;
             jp.qc = pp.out_bnhd[0]; jp.kfrag = pp.kfrag; jp.vfrag = pp.vfrag; jp.kbnd = pp.kbnd;
-            if (int e = launch_status(launch_proj(jp, s))) return e;
+            if (run(MOSAIC_BSA_STAGE_POOL))
+                if (int e = launch_status(launch_proj(jp, s))) return e;
         } else {
             if (rope) set_rope(pp);
-            if (int e = launch_status(launch_pool(pp, s))) return e;
+            if (run(MOSAIC_BSA_STAGE_POOL))
+                if (int e = launch_status(launch_pool(pp, s))) return e;
             if (rope) use_rotated();
         }
         if (int e = record(events, 1, s)) return e;
@@ -279,7 +284,8 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         cp.B = B; cp.nb = L.nb; cp.nb_pad = L.nb_pad; cp.Hq = Hq; cp.Hk = Hk; cp.G = Hq / Hk;
         cp.nsplit = L.nsplit; cp.ut_total = L.nb_pad / 32;
         cp.scale_log2 = scale * kLog2e;
-        if (int e = launch_status(launch_cmp(cp, sel, cmp, s))) return e;
+        if (run(MOSAIC_BSA_STAGE_CMP))
+            if (int e = launch_status(launch_cmp(cp, sel, cmp, s))) return e;
         if (int e = record(events, 2, s)) return e;
 
         CombineParams cb{};
@@ -294,24 +300,28 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
             tp.idx64 = a->block_indices_out;
             tp.B = B; tp.nb = L.nb; tp.nb_pad = L.nb_pad; tp.Hk = Hk; tp.K = a->sparse_block_count;
             tp.rows = B * Hk * L.nb;
-            if (int e = launch_status(launch_topk(tp, s))) return e;
+            if (run(MOSAIC_BSA_STAGE_TOPK))
+                if (int e = launch_status(launch_topk(tp, s))) return e;
             ap.idx = tp.idx32;
             ap.kbnd = pp.kbnd;
         } else if (cmp) {
-            if (int e = launch_status(launch_combine(cb, B, L.nb, s))) return e;
+            if (run(MOSAIC_BSA_STAGE_TOPK))
+                if (int e = launch_status(launch_combine(cb, B, L.nb, s))) return e;
         }
         if (int e = record(events, 3, s)) return e;
         ap.ocmp = cb.ocmp;
     } else {
         if (proj) {  // local attention only: the projection without pooling
-            if (int e = launch_status(launch_proj(*proj, s))) return e;
+            if (run(MOSAIC_BSA_STAGE_POOL))
+                if (int e = launch_status(launch_proj(*proj, s))) return e;
         } else if (rope) {  // local attention only: the pooling pass just rotates q and k
             PoolParams pp{};
             pp.x[0] = ap.q; pp.sb[0] = ap.q_sb; pp.sn[0] = ap.q_sn; pp.sh[0] = ap.q_sh; pp.heads[0] = Hq;
             pp.x[1] = ap.k; pp.sb[1] = ap.k_sb; pp.sn[1] = ap.k_sn; pp.sh[1] = ap.k_sh; pp.heads[1] = Hk;
             pp.B = B; pp.nb = N / kTile; pp.nb_pad = pp.nb; pp.bs = kTile;
             set_rope(pp);
-            if (int e = launch_status(launch_pool(pp, s))) return e;
+            if (run(MOSAIC_BSA_STAGE_POOL))
+                if (int e = launch_status(launch_pool(pp, s))) return e;
             use_rotated();
         }
         if (int e = record(events, 1, s)) return e;
@@ -319,7 +329,8 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         if (int e = record(events, 3, s)) return e;
     }
     static const int mode_map[4] = {kModeFull, kModeLocalOnly, kModeNoCompression, kModeNoSelection};
-    if (int e = launch_status(launch_attn(ap, mode_map[a->mode], false, waves, s))) return e;
+    if (run(MOSAIC_BSA_STAGE_ATTN))
+        if (int e = launch_status(launch_attn(ap, mode_map[a->mode], false, waves, s))) return e;
     return record(events, 4, s);
 }
 
@@ -349,6 +360,12 @@ int mosaic_bsa_fwd_noalloc(const mosaic_bsa_args* args, void* stream) {
 int mosaic_bsa_fwd_profiled(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes, void* stream,
                             void* const* events) {
     return bsa_forward(args, workspace, workspace_bytes, stream, events);
+}
+
+int mosaic_bsa_fwd_stage(const mosaic_bsa_args* args, void* workspace, size_t workspace_bytes, void* stream,
+                         int stage) {
+    if (stage < MOSAIC_BSA_STAGE_POOL || stage > MOSAIC_BSA_STAGE_ATTN) return MOSAIC_ERR_UNSUPPORTED;
+    return bsa_forward(args, workspace, workspace_bytes, stream, nullptr, nullptr, nullptr, 1u << stage);
 }
 
 int mosaic_bsa_fwd_rope(const mosaic_bsa_args* args, const float* rope_cos, const float* rope_sin, void* q_rot,

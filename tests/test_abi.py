@@ -105,6 +105,18 @@ def test_noalloc_entry_validates_before_touching_the_device():
     assert "static scratch" in _lib.strerror(_lib.ERR_SCRATCH_LIMIT)
 
 
+def test_stage_entry_validates_before_any_launch():
+    L = _lib.lib()
+    a = _args()
+    n = L.mosaic_bsa_workspace_size(ctypes.byref(a))
+    for stage in (_lib.STAGE_POOL, _lib.STAGE_CMP, _lib.STAGE_TOPK, _lib.STAGE_ATTN):
+        # the forward's own validation runs first, whatever the stage
+        assert L.mosaic_bsa_fwd_stage(ctypes.byref(_args(head_dim=32)), FAKE, n, None, stage) == 2
+        assert L.mosaic_bsa_fwd_stage(ctypes.byref(a), None, 0, None, stage) == 6
+    assert L.mosaic_bsa_fwd_stage(ctypes.byref(a), FAKE, n, None, -1) == 11
+    assert L.mosaic_bsa_fwd_stage(ctypes.byref(a), FAKE, n, None, 4) == 11
+
+
 def test_fused_rope_entry_validates():
     L = _lib.lib()
     a = _args()
