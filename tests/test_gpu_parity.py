@@ -10,8 +10,8 @@ import pytest
 import torch
 
 import mosaic_amd as M
-from mosaic_amd.inputs import (BOTTLENECK_NSIDE16, STAGE1_NSIDE64, STAGE2_NSIDE32_B24, Workload, make_inputs,
-                               scaling_workload)
+from mosaic_amd.inputs import (BOTTLENECK_NSIDE16, STAGE1_NSIDE64, STAGE1_NSIDE64_MODEL, STAGE2_NSIDE32_B24, Workload,
+                               make_inputs, scaling_workload)
 from mosaic_amd.healpix import apply_rope, get_healpix_grid, rope_tables
 from oracle import bsa_oracle as O
 from structured_inputs import compressed_only_inputs, pooled_logit_std
@@ -61,16 +61,17 @@ def test_block_attention(N, Hq, Hk, bs_l):
     close(got, O.block_attention(q, k, v, bs_l))
 
 
-@pytest.mark.parametrize("nside", [32, 64])
-def test_dense_attention_sweep_sizes(nside):
-    """The dense baseline of the scaling sweep (flash_attn_func over the whole sequence) at
-    N = 12288 and 49152, 12/3 heads: a sample of query rows against the oracle."""
+@pytest.mark.parametrize("nside,nrows", [(32, 192), (64, 192), (128, 64)])
+def test_dense_attention_sweep_sizes(nside, nrows):
+    """The dense baseline of the scaling sweep (flash_attn_func over the whole sequence,
+    primitives.py:31) at N = 12288, 49152 and 196608, 12/3 heads: a sample of query rows
+    against the oracle."""
     print(f"dense attention nside {nside}", flush=True)
     wl = scaling_workload(nside)
     q, k, v, _ = make_inputs(wl, seed=2)
     out = M.dense_attention(*dev(q, k, v)).cpu()
     assert torch.isfinite(out.float()).all()
-    rows = torch.randperm(wl.seq_len, generator=torch.Generator().manual_seed(3))[:192].sort().values
+    rows = torch.randperm(wl.seq_len, generator=torch.Generator().manual_seed(3))[:nrows].sort().values
     close(out[:, rows], O.dense_attention(q[:, rows], k, v))
 
 
@@ -336,12 +337,21 @@ def test_deterministic():
     assert torch.equal(a, b)
 
 
+# Stage 2 of the shipped model at 24 members: Nside 32, 16/4 heads, local blocks of 1024 tokens,
+# selection blocks of 128, top-12 (inference.py:71-88)
+STAGE2_NSIDE32_B24_MODEL = Workload("bsa_nside32_b24_h16kv4_bl1024_bs128_top12", 32, 24, 16, 4, 64, 1024, 128, 12,
+                                    True)
+
+
 @pytest.mark.parametrize("wl,nsample", [(STAGE1_NSIDE64, 24), (STAGE2_NSIDE32_B24, 6), (scaling_workload(32), 16),
-                                         (scaling_workload(128), 16)],
-                         ids=["nside64", "nside32_b24", "sweep_nside32", "sweep_nside128"])
+                                         (scaling_workload(128), 16), (STAGE1_NSIDE64_MODEL, 12),
+                                         (STAGE2_NSIDE32_B24_MODEL, 6)],
+                         ids=["nside64", "nside32_b24", "sweep_nside32", "sweep_nside128", "nside64_model_blocks",
+                              "nside32_b24_model_blocks"])
 def test_full_size_workloads(wl, nsample):
-    """Full-size workloads: indices of every row by the band rule; output rows of a sample of
-    query blocks against the oracle; finite everywhere."""
+    """Full-size workloads, including the shipped model's op settings (local blocks of 1024,
+    selection blocks of 128, top-24 / top-12): indices of every row by the band rule; output
+    rows of a sample of query blocks against the oracle; finite everywhere."""
     print(f"full-size workload {wl.name}", flush=True)
     q, k, v, w = make_inputs(wl, seed=0)
     out, idx = _run_full(q, k, v, w, wl.block_attn_size, wl.sparse_block_size, wl.sparse_block_count)
