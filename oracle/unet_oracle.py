@@ -73,12 +73,18 @@ def mosaic_attention(P: dict, pre: str, x: torch.Tensor, cfg, norm_dtype: dict, 
     q = rearrange(linear(x, P[pre + "to_q.weight"]), "s b (h d) -> b s h d", h=Hq)
     k = rearrange(linear(x, P[pre + "to_k.weight"]), "s b (h d) -> b s h d", h=Hk)
     v = rearrange(linear(x, P[pre + "to_v.weight"]), "s b (h d) -> b s h d", h=Hk)
-    logits = rearrange(linear(x, P[pre + "to_strategy_combine_mlp.weight"]), "t b (h s) -> s b t h", h=Hq)
-    w = torch.softmax(logits.float(), dim=0).type_as(x).unsqueeze(-1)
+    # a layer without the branch-weight projection is a local-only layer (block_attn_only,
+    # mosaic.py:125, primitives.py:168-175)
+    local_only = pre + "to_strategy_combine_mlp.weight" not in P
+    w = None
+    if not local_only:
+        logits = rearrange(linear(x, P[pre + "to_strategy_combine_mlp.weight"]), "t b (h s) -> s b t h", h=Hq)
+        w = torch.softmax(logits.float(), dim=0).type_as(x).unsqueeze(-1).to(BF16)
     if pre + "q_rope.cos_freqs" in P:
         q = _rope(q, P[pre + "q_rope.cos_freqs"], P[pre + "q_rope.sin_freqs"])
         k = _rope(k, P[pre + "k_rope.cos_freqs"], P[pre + "k_rope.sin_freqs"])
-    idx = next(indices).cpu() if indices is not None else None
+    rec = next(indices) if indices is not None else None
+    idx = rec.cpu() if rec is not None else None
     if idx is not None and band_stats is not None:
         # the given selection against this oracle's own scores (primitives.py:35-51): blocks
         # may differ only where the scores tie within the band
@@ -91,8 +97,8 @@ def mosaic_attention(P: dict, pre: str, x: torch.Tensor, cfg, norm_dtype: dict, 
             rec["bad_planted"] = bsa_oracle.selection_band_check(scores, band_stats["planted"](idx),
                                                                  cfg.sparse_block_count, band)[0]
         band_stats["calls"].append(rec)
-    o = bsa_oracle.mosaic_attn_func(q, k, v.to(BF16), w.to(BF16), cfg.block_attn_size, cfg.sparse_block_size,
-                                    cfg.sparse_block_count, False, block_indices=idx)
+    o = bsa_oracle.mosaic_attn_func(q, k, v.to(BF16), w, cfg.block_attn_size, cfg.sparse_block_size,
+                                    cfg.sparse_block_count, local_only, block_indices=idx)
     return linear(rearrange(o, "b s h d -> s b (h d)"), P[pre + "to_o.weight"])
 
 

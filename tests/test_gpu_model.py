@@ -118,30 +118,31 @@ def test_op_writes_sequence_first_rows(mode):
     assert torch.equal(buf.view(N, B, Hq, 64).transpose(0, 1), ref)
 
 
-def tiny_config(selective: bool = False) -> ModelConfig:
+def tiny_config(selective: bool = False, sparse_every: int = 1, depth0: int = 1) -> ModelConfig:
     """Three resolutions (nside 16 / 8 / 4: 3072 / 768 / 192 pixels), head_dim 64, GQA 4.  By
     default the selection count equals the block count at every stage (selection keeps every
     block); ``selective`` keeps 6 of 48, 4 of 12 and 2 of 3 blocks with local blocks of 4, 4 and
-    3 selection blocks, as the shipped model's bs_l = 8 bs and K < N / bs do."""
+    3 selection blocks, as the shipped model's bs_l = 8 bs and K < N / bs do.  ``sparse_every``
+    and the first stage's encoder depth ``depth0`` give local-only layers (mosaic.py:125)."""
     K = (6, 4, 2) if selective else (48, 12, 3)
     bl_last = 192 if selective else 64
     stages = [
         StageConfig(nside=16, dim=256, num_heads=4, block_attn_size=256, sparse_block_size=64,
-                    sparse_block_count=K[0], encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
+                    sparse_block_count=K[0], encoder_depth=depth0, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
         StageConfig(nside=8, dim=512, num_heads=8, block_attn_size=256, sparse_block_size=64,
                     sparse_block_count=K[1], encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
     ]
     bottleneck = BottleneckConfig(nside=4, dim=512, num_heads=8, block_attn_size=bl_last, sparse_block_size=64,
                                   sparse_block_count=K[2], depth=1, mlp_ratio=2.0, gqa_ratio=4)
     return ModelConfig(dim=256, num_heads=4, k_neighbors=8, qk_norm=False, rope=True, rope_theta=10000,
-                       sparse_every=1, variables=[f"v{i}" for i in range(5)], static_variables=["a", "b", "c"],
+                       sparse_every=sparse_every, variables=[f"v{i}" for i in range(5)], static_variables=["a", "b", "c"],
                        qkv_compress_ratio=1, cg_stage_cfgs=stages, bottleneck_cfg=bottleneck,
                        num_history_steps=2, noise_dim=32, rmsnorm_elementwise_affine=False)
 
 
-def build_tiny(seed=0, selective=False):
+def build_tiny(seed=0, selective=False, **kw):
     torch.manual_seed(seed)
-    cfg = tiny_config(selective)
+    cfg = tiny_config(selective, **kw)
     model = Transformer(cfg, seed=11)
     g = torch.Generator().manual_seed(seed + 1)
     for name, p in model.named_parameters():          # residual outputs at full scale
@@ -201,6 +202,45 @@ def test_unet_forward_matches_oracle(selective):
     rel = ((got - r).norm() / r.norm()).item()
     err = (got - r).abs().max().item()
     print(f"unet tiny: rel_l2 {rel:.3e} max_abs {err:.3e} |ref| max {r.abs().max().item():.3f}", flush=True)
+    assert rel <= 2e-2 and err <= 6e-2, f"rel_l2 {rel:.3e} max_abs {err:.3e}"
+
+
+@pytest.mark.parametrize("sparse_every,depth0,n_sparse", [(2, 2, 5), (0, 1, 0)],
+                         ids=["every_second_layer_local_only", "all_layers_local_only"])
+def test_unet_forward_with_local_only_layers_matches_oracle(sparse_every, depth0, n_sparse):
+    """Local-only attention layers (block_attn_only, mosaic.py:125, primitives.py:62-63) in the
+    model against the oracle: with sparse_every = 2 the second encoder block of the first stage
+    runs the local branch alone; with sparse_every = 0 every layer does."""
+    print(f"unet tiny forward, sparse_every {sparse_every}", flush=True)
+    cfg, model = build_tiny(selective=True, sparse_every=sparse_every, depth0=depth0)
+    local_only = [m for m in model.modules() if isinstance(m, MosaicAttention) and m.block_attn_only]
+    assert len(local_only) == (1 if sparse_every == 2 else 6 if depth0 == 2 else 5)
+    assert all(m.to_strategy_combine_mlp is None for m in local_only)
+    recorded = []
+    for m in model.modules():
+        if isinstance(m, MosaicAttention):
+            m.record_block_indices = recorded
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(1, 1, 2, 24, 13, 5, generator=g)
+    dyt = torch.rand(1, 1, 2, generator=g)
+    S = 2
+    with torch.no_grad(), torch.autocast(DEV, dtype=torch.bfloat16):
+        out = model(x.to(DEV), dyt.to(DEV), S)
+        probe = {dt: torch.nn.functional.rms_norm(torch.zeros(1, 8, dtype=dt, device=DEV), (8,)).dtype
+                 for dt in (torch.bfloat16, torch.float32)}
+    assert sum(i is not None for i in recorded) == n_sparse
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(11)
+    noise = torch.randn((S, cfg.noise_dim), generator=gen, device=DEV, dtype=torch.float32).cpu()
+    stats = {"rel_band": 2e-2, "calls": []}
+    ref = unet_oracle.forward(model.state_dict(), cfg, x, dyt, S, noise, probe, block_indices=recorded,
+                              band_stats=stats)
+    assert len(stats["calls"]) == n_sparse and all(c["bad"] == 0 for c in stats["calls"]), stats["calls"]
+    got, r = out.float().cpu(), ref.float()
+    assert torch.isfinite(got).all()
+    rel = ((got - r).norm() / r.norm()).item()
+    err = (got - r).abs().max().item()
+    print(f"unet tiny (sparse_every {sparse_every}): rel_l2 {rel:.3e} max_abs {err:.3e}", flush=True)
     assert rel <= 2e-2 and err <= 6e-2, f"rel_l2 {rel:.3e} max_abs {err:.3e}"
 
 
