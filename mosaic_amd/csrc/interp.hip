@@ -11,11 +11,13 @@
 // to_q, and the k / v rows are read straight from [S_from, B, H, 64] (neighbouring targets
 // share most of their neighbours, so rows are reused from L2).
 //
-// The work is VALU-bound: every (target, member, head) takes 2 K 64 bf16-rounded products
-// (a multiply, half a v_cvt_pk_bf16_f32 and half a v_dot2_f32_bf16 each, plus the bf16 ->
-// fp32 unpack of the k / v element).  Staging each tile of targets' neighbour union in LDS
-// (cutting the L2 requests 4-7x) measured slower than this direct form: it halves the
-// occupancy, and occupancy is what hides the latency of the reduction chains.
+// The work is VALU-bound: every (target, member, head) takes 2 K 64 bf16-rounded products.
+// Each product is one v_dot2_f32_bf16 of the packed k / v pair against (x, 0) or (0, x)
+// (exact: a bf16 x bf16 product fits fp32), then half a v_cvt_pk_bf16_f32 and half a
+// v_dot2_f32_bf16 that adds the rounded pair; no k / v element is unpacked to fp32.
+// Staging each tile of targets' neighbour union in LDS (cutting the L2 requests 4-7x)
+// measured slower than this direct form: it halves the occupancy, and occupancy is what
+// hides the latency of the reduction chains.
 //
 // One wave per (target s, head h) pair, looping over the batch members b with the next
 // member's rows in flight.  Lane l = 8 jg + dc holds the 8-dim chunk dc of neighbours
@@ -26,6 +28,8 @@
 // reduce-scattered over the groups by the same three exchanges, leaving one dimension per
 // lane.  Workgroups are remapped so that each XCD takes one contiguous range of targets.
 #include "bsa_common.h"
+
+#include <type_traits>
 
 namespace mosaic {
 namespace {
@@ -74,12 +78,36 @@ __device__ __forceinline__ float group_max(float x) {
     return xor32_max(fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1])));
 }
 
-// c + bf16(a0 * b0) + bf16(a1 * b1): both products rounded to bf16 (one v_cvt_pk_bf16_f32),
-// then added in fp32 by a dot product with (1, 1)
-__device__ __forceinline__ float add_rounded_pair(float a0, float b0, float a1, float b1, float c) {
-    const uint32_t pr = pack_bf16x2(a0 * b0, a1 * b1);
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr),
-                                           __builtin_bit_cast(bf16x2_t, 0x3f803f80u), c, false);
+// Eight exact bf16 products, rounded to bf16 in pairs:
+//   c[j] = (bf16(t[2j]), bf16(t[2j + 1])) packed,  t[i] = a[i] . b[i]  (v_dot2_f32_bf16)
+// where a[i] is (x, 0) or (0, x), x bf16 in the low or high half, so t[i] is x times the
+// matching half of the packed pair b[i] (a bf16 x bf16 product is exact in fp32) -- no
+// element is unpacked to fp32.  A dot product's result needs three wait states before another
+// VALU instruction reads it, and the compiler does not track that through inline assembly:
+// the eight products go first and every rounding reads products at least three instructions
+// old.  c may share registers with a and b (read only by the products); t may not.
+__device__ __forceinline__ void prod8_round4(const uint32_t (&a)[8], const uint32_t (&b)[8], uint32_t (&c)[4]) {
+    float t0, t1, t2, t3, t4, t5, t6, t7;
+    asm("v_dot2_f32_bf16 %4, %12, %20, 0\n\t"
+        "v_dot2_f32_bf16 %5, %13, %21, 0\n\t"
+        "v_dot2_f32_bf16 %6, %14, %22, 0\n\t"
+        "v_dot2_f32_bf16 %7, %15, %23, 0\n\t"
+        "v_dot2_f32_bf16 %8, %16, %24, 0\n\t"
+        "v_dot2_f32_bf16 %9, %17, %25, 0\n\t"
+        "v_dot2_f32_bf16 %10, %18, %26, 0\n\t"
+        "v_dot2_f32_bf16 %11, %19, %27, 0\n\t"
+        "v_cvt_pk_bf16_f32 %0, %4, %5\n\t"
+        "v_cvt_pk_bf16_f32 %1, %6, %7\n\t"
+        "v_cvt_pk_bf16_f32 %2, %8, %9\n\t"
+        "v_cvt_pk_bf16_f32 %3, %10, %11"
+        : "=v"(c[0]), "=v"(c[1]), "=v"(c[2]), "=v"(c[3]),
+          "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+          "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(b[4]), "v"(b[5]), "v"(b[6]), "v"(b[7]));
+}
+// c + the two bf16 halves of the packed pair pr, by a dot product with (1, 1)
+__device__ __forceinline__ float add_pair(uint32_t pr, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr), __builtin_bit_cast(bf16x2_t, 0x3f803f80u), c, false);
 }
 
 __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
@@ -88,7 +116,7 @@ __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
     for (int e = 0; e < 4; ++e) { f[2 * e] = bf_lo(a[e]); f[2 * e + 1] = bf_hi(a[e]); }
 }
 
-template <int NSLOT>
+template <int NSLOT, bool OFF32>
 __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -112,20 +140,25 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
     // per slot: the neighbour's row offsets and this lane's 8 query values,
     // q[j][d] = bf16(rel[j] . W[h*64 + d]) (fp32 sum of the three bf16 products: the
     // Linear's bf16 inputs)
-    int64_t koff[NSLOT], voff[NSLOT];
-    float q[NSLOT][8];
+    // byte offsets of this lane's k / v chunks within a member (32 bits when they fit: the
+    // loads then add them to a wave-uniform member base in the address unit)
+    using Off = typename std::conditional<OFF32, uint32_t, int64_t>::type;
+    Off koff[NSLOT], voff[NSLOT];
+    uint32_t qp[NSLOT][8];  // q[j][d] as a bf16 in the half of a word that k's dim d occupies
 #pragma unroll
     for (int i = 0; i < NSLOT; ++i) {
         const int64_t sj = (int64_t)s * K + min(jg + 8 * i, K - 1);
         // indices outside [0, S_from) are clamped (memory safety; the reference would raise)
         const int64_t n = min(max(p.neighbors[sj], 0), p.S_from - 1);
-        koff[i] = n * p.k_sn + (int64_t)h * p.k_sh + 8 * dc;
-        voff[i] = n * p.v_sn + (int64_t)h * p.v_sh + 8 * dc;
+        koff[i] = (Off)(2 * (n * p.k_sn + (int64_t)h * p.k_sh + 8 * dc));
+        voff[i] = (Off)(2 * (n * p.v_sn + (int64_t)h * p.v_sh + 8 * dc));
         const float r0 = round_bf16(p.rel_pos[3 * sj]), r1 = round_bf16(p.rel_pos[3 * sj + 1]),
                     r2 = round_bf16(p.rel_pos[3 * sj + 2]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            q[i][e] = round_bf16(fmaf(r2, wq[3 * e + 2], fmaf(r1, wq[3 * e + 1], r0 * wq[3 * e])));
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t bits = __float_as_uint(round_bf16(fmaf(r2, wq[3 * e + 2], fmaf(r1, wq[3 * e + 1], r0 * wq[3 * e]))));
+            qp[i][e] = (e & 1) ? bits : bits >> 16;
+        }
     }
     // the output dimension this lane ends up holding after the reduce-scatter
     const int dout = 8 * dc + 4 * (lane >> 5) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
@@ -133,24 +166,34 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
 
     uint4 kw[NSLOT], vw[NSLOT], kn[NSLOT], vn[NSLOT];
 #pragma unroll
-    for (int i = 0; i < NSLOT; ++i) { kw[i] = ld16(p.k + koff[i]); vw[i] = ld16(p.v + voff[i]); }
+    for (int i = 0; i < NSLOT; ++i) {
+        kw[i] = ld16(reinterpret_cast<const char*>(p.k) + koff[i]);
+        vw[i] = ld16(reinterpret_cast<const char*>(p.v) + voff[i]);
+    }
     for (int b = 0; b < p.B; ++b) {
         if (b + 1 < p.B) {
+            const char* kb = reinterpret_cast<const char*>(p.k + (int64_t)(b + 1) * p.k_sb);
+            const char* vb = reinterpret_cast<const char*>(p.v + (int64_t)(b + 1) * p.v_sb);
 #pragma unroll
             for (int i = 0; i < NSLOT; ++i) {
-                kn[i] = ld16(p.k + koff[i] + (int64_t)(b + 1) * p.k_sb);
-                vn[i] = ld16(p.v + voff[i] + (int64_t)(b + 1) * p.v_sb);
+                Off ko = koff[i], vo = voff[i];
+                // keeps the 32-bit offsets in the loop, where the load takes them with the
+                // uniform base (hoisted, they become 64-bit pairs and a 64-bit add per load)
+                if constexpr (OFF32) asm volatile("" : "+v"(ko), "+v"(vo));
+                kn[i] = ld16(kb + ko);
+                vn[i] = ld16(vb + vo);
             }
         }
         // scores of this lane's slots (every lane of a neighbour group holds its score)
         float sc[NSLOT], m = -INFINITY;
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
-            float kf[8];
-            unpack8(kw[i], kf);
+            const uint32_t kd[8] = {kw[i].x, kw[i].x, kw[i].y, kw[i].y, kw[i].z, kw[i].z, kw[i].w, kw[i].w};
+            uint32_t pr[4];
+            prod8_round4(qp[i], kd, pr);
             float part = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) part = add_rounded_pair(q[i][2 * e], kf[2 * e], q[i][2 * e + 1], kf[2 * e + 1], part);
+            for (int e = 0; e < 4; ++e) part = add_pair(pr[e], part);
             part = chunk_sum(part);
             sc[i] = jg + 8 * i < K ? round_bf16(round_bf16(part) * p.scale) : -INFINITY;
             m = fmaxf(m, sc[i]);
@@ -164,35 +207,37 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
         }
         const float inv = __builtin_amdgcn_rcpf(group_sum(l));
         // out[d] = sum over slots of bf16(w * v[d]); two slots at a time share one rounding
-        // instruction and one dot-product add.  An absent neighbour (j >= K) has weight 0 and
-        // its row (a duplicate of a present one) is replaced by zeros.
+        // instruction and one dot-product add.  An absent neighbour (j >= K) has weight 0; its
+        // row (a duplicate of a present one) then adds bf16(0 * v) = 0.  The weights are bf16, so
+        // each product is one dot product of (w, 0) or (0, w) with a packed pair of v.
         float acc[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] = 0.f;
 #pragma unroll
         for (int i = 0; i < NSLOT; i += 2) {
-            float va[8], vb[8];
-            unpack8(vw[i], va);
-            if (jg + 8 * i >= K) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) va[e] = 0.f;
-            }
-            const float wa = round_bf16(ex[i] * inv);
+            const uint32_t va[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+            const uint32_t wa_hi = __float_as_uint(round_bf16(ex[i] * inv)), wa_lo = wa_hi >> 16;
             if (i + 1 < NSLOT) {
-                unpack8(vw[i + 1], vb);
-                if (jg + 8 * (i + 1) >= K) {
+                const uint32_t vb[4] = {vw[i + 1].x, vw[i + 1].y, vw[i + 1].z, vw[i + 1].w};
+                const uint32_t wb_hi = __float_as_uint(round_bf16(ex[i + 1] * inv)), wb_lo = wb_hi >> 16;
+                const uint32_t w8[8] = {wa_lo, wb_lo, wa_hi, wb_hi, wa_lo, wb_lo, wa_hi, wb_hi};
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) vb[e] = 0.f;
+                for (int m = 0; m < 4; m += 2) {
+                    const uint32_t v8[8] = {va[m], vb[m], va[m], vb[m], va[m + 1], vb[m + 1], va[m + 1], vb[m + 1]};
+                    uint32_t pr[4];
+                    prod8_round4(w8, v8, pr);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[2 * m + e] = add_pair(pr[e], acc[2 * m + e]);
                 }
-                const float wb = round_bf16(ex[i + 1] * inv);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[e] = add_rounded_pair(wa, va[e], wb, vb[e], acc[e]);
             } else {
+                const uint32_t w8[8] = {wa_lo, wa_hi, wa_lo, wa_hi, wa_lo, wa_hi, wa_lo, wa_hi};
+                const uint32_t v8[8] = {va[0], va[0], va[1], va[1], va[2], va[2], va[3], va[3]};
+                uint32_t pr[4];
+                prod8_round4(w8, v8, pr);
 #pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const uint32_t pr = pack_bf16x2(wa * va[e], wa * va[e + 1]);
-                    acc[e] += bf_lo(pr);
-                    acc[e + 1] += bf_hi(pr);
+                for (int m = 0; m < 4; ++m) {
+                    acc[2 * m] += bf_lo(pr[m]);
+                    acc[2 * m + 1] += bf_hi(pr[m]);
                 }
             }
         }
@@ -215,7 +260,13 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
 template <int NSLOT>
 hipError_t launch_slots(const InterpParams& p, unsigned wgs, hipStream_t s) {
     void* args[] = {const_cast<InterpParams*>(&p)};
-    return hipLaunchKernel((const void*)&knn_attn_kernel<NSLOT>, dim3(wgs), dim3(kInterpWaves * 64), args, 0, s);
+    // 32-bit chunk offsets when every chunk of a member lies within 4 GiB of its start
+    const int64_t kmax = (int64_t)(p.S_from - 1) * p.k_sn + (int64_t)(p.H - 1) * p.k_sh + 64;
+    const int64_t vmax = (int64_t)(p.S_from - 1) * p.v_sn + (int64_t)(p.H - 1) * p.v_sh + 64;
+    const bool off32 = p.k_sn >= 0 && p.k_sh >= 0 && p.v_sn >= 0 && p.v_sh >= 0 &&
+                       2 * kmax <= 0xffffffffLL && 2 * vmax <= 0xffffffffLL;
+    const void* fn = off32 ? (const void*)&knn_attn_kernel<NSLOT, true> : (const void*)&knn_attn_kernel<NSLOT, false>;
+    return hipLaunchKernel(fn, dim3(wgs), dim3(kInterpWaves * 64), args, 0, s);
 }
 
 }  // namespace
