@@ -533,6 +533,8 @@ int mosaic_knn_interp_fwd(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors
     p.out = static_cast<bf16_t*>(out);
     p.S_from = num_from; p.S_to = num_to; p.B = batch; p.H = num_heads; p.K = num_neighbors;
     p.scale = resolve_scale(scale, head_dim);
+    int exp2 = 0;
+    p.scale_pow2 = std::isfinite(p.scale) && p.scale >= 0x1p-126f && std::frexp(p.scale, &exp2) == 0.5f;
     return launch_status(launch_knn_attn(p, static_cast<hipStream_t>(stream)));
 }
 

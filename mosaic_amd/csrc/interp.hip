@@ -116,7 +116,21 @@ __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
     for (int e = 0; e < 4; ++e) { f[2 * e] = bf_lo(a[e]); f[2 * e + 1] = bf_hi(a[e]); }
 }
 
-template <int NSLOT, bool OFF32>
+// The 16-byte chunk at byte offset off from a member's base (wave-uniform).  With 32-bit
+// offsets the load is a raw buffer load: base in the resource (scalar registers), the offset
+// as its per-lane offset, so the member loop spends no vector instruction on addresses.
+template <bool OFF32, typename Off>
+__device__ __forceinline__ uint4 ld_member(const bf16_t* base, Off off) {
+    if constexpr (OFF32) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, -1, 0x00020000);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        return make_uint4(v[0], v[1], v[2], v[3]);
+    } else {
+        return ld16(reinterpret_cast<const char*>(base) + off);
+    }
+}
+
+template <int NSLOT, bool OFF32, bool POW2>
 __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -140,8 +154,7 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
     // per slot: the neighbour's row offsets and this lane's 8 query values,
     // q[j][d] = bf16(rel[j] . W[h*64 + d]) (fp32 sum of the three bf16 products: the
     // Linear's bf16 inputs)
-    // byte offsets of this lane's k / v chunks within a member (32 bits when they fit: the
-    // loads then add them to a wave-uniform member base in the address unit)
+    // byte offsets of this lane's k / v chunks within a member (32 bits when they fit)
     using Off = typename std::conditional<OFF32, uint32_t, int64_t>::type;
     Off koff[NSLOT], voff[NSLOT];
     uint32_t qp[NSLOT][8];  // q[j][d] as a bf16 in the half of a word that k's dim d occupies
@@ -164,26 +177,13 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
     const int dout = 8 * dc + 4 * (lane >> 5) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
     bf16_t* out = p.out + ((int64_t)s * p.B * p.H + h) * 64 + dout;
 
-    uint4 kw[NSLOT], vw[NSLOT], kn[NSLOT], vn[NSLOT];
+    // k / v chunks of the current member; the next member's k is loaded as soon as the scores
+    // are done with k, its v once the output is done with v
+    uint4 kw[NSLOT], vw[NSLOT];
 #pragma unroll
-    for (int i = 0; i < NSLOT; ++i) {
-        kw[i] = ld16(reinterpret_cast<const char*>(p.k) + koff[i]);
-        vw[i] = ld16(reinterpret_cast<const char*>(p.v) + voff[i]);
-    }
+    for (int i = 0; i < NSLOT; ++i) { kw[i] = ld_member<OFF32>(p.k, koff[i]); vw[i] = ld_member<OFF32>(p.v, voff[i]); }
     for (int b = 0; b < p.B; ++b) {
-        if (b + 1 < p.B) {
-            const char* kb = reinterpret_cast<const char*>(p.k + (int64_t)(b + 1) * p.k_sb);
-            const char* vb = reinterpret_cast<const char*>(p.v + (int64_t)(b + 1) * p.v_sb);
-#pragma unroll
-            for (int i = 0; i < NSLOT; ++i) {
-                Off ko = koff[i], vo = voff[i];
-                // keeps the 32-bit offsets in the loop, where the load takes them with the
-                // uniform base (hoisted, they become 64-bit pairs and a 64-bit add per load)
-                if constexpr (OFF32) asm volatile("" : "+v"(ko), "+v"(vo));
-                kn[i] = ld16(kb + ko);
-                vn[i] = ld16(vb + vo);
-            }
-        }
+        const bool more = b + 1 < p.B;
         // scores of this lane's slots (every lane of a neighbour group holds its score)
         float sc[NSLOT], m = -INFINITY;
 #pragma unroll
@@ -195,8 +195,16 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
 #pragma unroll
             for (int e = 0; e < 4; ++e) part = add_pair(pr[e], part);
             part = chunk_sum(part);
-            sc[i] = jg + 8 * i < K ? round_bf16(round_bf16(part) * p.scale) : -INFINITY;
+            // a power-of-two scale leaves bf16(part) * scale a bf16 value (a product too small
+            // to be normal is below 2^-126 in magnitude, and so is the difference its rounding
+            // would make: the softmax weights come out the same)
+            const float t = POW2 ? round_bf16(part) * p.scale : round_bf16(round_bf16(part) * p.scale);
+            sc[i] = jg + 8 * i < K ? t : -INFINITY;
             m = fmaxf(m, sc[i]);
+        }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < NSLOT; ++i) kw[i] = ld_member<OFF32>(p.k + (int64_t)(b + 1) * p.k_sb, koff[i]);
         }
         m = group_max(m);
         float ex[NSLOT], l = 0.f;
@@ -241,6 +249,10 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
                 }
             }
         }
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < NSLOT; ++i) vw[i] = ld_member<OFF32>(p.v + (int64_t)(b + 1) * p.v_sb, voff[i]);
+        }
         // reduce-scatter over the 8 neighbour groups: halves (dims e / e + 4), row pairs
         // (e / e + 2), then lanes l ^ 8 (e / e + 1)
         float r4[4], r2[2];
@@ -252,8 +264,6 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
         const float keep = odd8 ? r2[1] : r2[0], give = odd8 ? r2[0] : r2[1];
         const float o = keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(give), 0x128, 0xf, 0xf, false));
         out[(int64_t)b * p.H * 64] = (bf16_t)(pack_bf16x2(o, 0.f) & 0xffffu);
-#pragma unroll
-        for (int i = 0; i < NSLOT; ++i) { kw[i] = kn[i]; vw[i] = vn[i]; }
     }
 }
 
@@ -265,7 +275,8 @@ hipError_t launch_slots(const InterpParams& p, unsigned wgs, hipStream_t s) {
     const int64_t vmax = (int64_t)(p.S_from - 1) * p.v_sn + (int64_t)(p.H - 1) * p.v_sh + 64;
     const bool off32 = p.k_sn >= 0 && p.k_sh >= 0 && p.v_sn >= 0 && p.v_sh >= 0 &&
                        2 * kmax <= 0xffffffffLL && 2 * vmax <= 0xffffffffLL;
-    const void* fn = off32 ? (const void*)&knn_attn_kernel<NSLOT, true> : (const void*)&knn_attn_kernel<NSLOT, false>;
+    const void* fn = off32 ? (p.scale_pow2 ? (const void*)&knn_attn_kernel<NSLOT, true, true> : (const void*)&knn_attn_kernel<NSLOT, true, false>)
+                           : (p.scale_pow2 ? (const void*)&knn_attn_kernel<NSLOT, false, true> : (const void*)&knn_attn_kernel<NSLOT, false, false>);
     return hipLaunchKernel(fn, dim3(wgs), dim3(kInterpWaves * 64), args, 0, s);
 }
 

@@ -150,3 +150,43 @@ def test_knn_attention_random_neighbour_lists():
     w_q = rand(2 * 64, 3, seed=33)
     got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
     close(got, IO.knn_attention(k, v, nb, rel, w_q, 0.125))
+
+
+@pytest.mark.parametrize("scale", [0.1, 0.3])
+def test_knn_attention_scale_not_a_power_of_two(scale):
+    """A scale that is not a power of two rounds bf16(score) * scale to bf16 again (the
+    kernel's other path; 0.125 = 64^-0.5 skips that exact rounding)."""
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(ll, hp, 24)
+    k, v = rand(len(ll), 2, 3, 64, seed=40, scale=2.0), rand(len(ll), 2, 3, 64, seed=41)
+    w_q = rand(3 * 64, 3, seed=42, scale=2.0)
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), scale)
+    close(got, IO.knn_attention(k, v, nb, rel, w_q, scale))
+
+
+def test_knn_attention_negative_point_stride_equals_forward_order():
+    """k / v handed over through the C ABI as views with a negative point stride over copies
+    stored in reverse row order (point n is still k[n]): the kernel's 64-bit offset path,
+    which must give the same output as the forward-order call (32-bit offsets)."""
+    from mosaic_amd import _lib
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(hp, ll, 24)
+    S, B, H = len(hp), 2, 3
+    k, v = rand(S, B, H, 64, seed=50).to(DEV), rand(S, B, H, 64, seed=51).to(DEV)
+    w_q = rand(H * 64, 3, seed=52).to(DEV)
+    nb_d, rel_d = nb.to(DEV), rel.to(DEV)
+    fwd = knn_attention(k, v, nb_d, rel_d, w_q, 0.125)
+    kr, vr = k.flip(0).contiguous(), v.flip(0).contiguous()      # row S-1-n holds point n
+
+    def reversed_view(t):     # starts at row S-1 (point 0) and steps back one row per point
+        last = t[S - 1]
+        return _lib.Bnhd(last.data_ptr(), t.stride(1), -t.stride(0), t.stride(2))
+    nb32 = nb_d.to(torch.int32).contiguous()
+    out = torch.empty_like(fwd)
+    st = _lib.lib().mosaic_knn_interp_fwd(reversed_view(kr), reversed_view(vr), nb32.data_ptr(),
+                                          rel_d.float().contiguous().data_ptr(), w_q.data_ptr(),
+                                          S, len(ll), B, H, 64, 24, 0.125, out.data_ptr(),
+                                          torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "mosaic_knn_interp_fwd")
+    torch.cuda.synchronize()
+    assert torch.equal(out, fwd)
