@@ -27,7 +27,7 @@ attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v), --
 times the op with the input side's RoPE fused into its pooling pass, mosaic_bsa_fwd_rope,
 against eager torch RoPE followed by the op, both on unrotated q/k), --interp (also times the
 k-nearest-neighbour cross-attention between the model's lat-lon and HEALPix grids,
-mosaic_knn_interp_fwd, at --interp-batch members), --branches (also times the local and the
+mosaic_knn_interp_fwd_ordered, at --interp-batch members), --branches (also times the local and the
 selected branch as standalone kernels).  Unless --no-unet, the line also carries
 one forecast step of the full U-Net at --unet-members ensemble members (default 24:
 ``unet_24_member_step_ms``, the metric's second half); --unet-only times only that step.
@@ -254,13 +254,14 @@ def rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream):
 
 
 def interp_leg(L, args, dev, stream):
-    """k-nearest-neighbour cross-attention between the model's grids (mosaic_knn_interp_fwd):
-    121 x 240 lat-lon (29040 points) <-> HEALPix nside 64 (49152), 24 neighbours, 12 heads of
-    64, ``--interp-batch`` members, both directions.  Algorithmic bytes per launch: every k / v
+    """k-nearest-neighbour cross-attention between the model's grids
+    (mosaic_knn_interp_fwd_ordered, targets in the model's spatial order): 121 x 240 lat-lon
+    (29040 points) <-> HEALPix nside 64 (49152), 24 neighbours, 12 heads of 64,
+    ``--interp-batch`` members, both directions.  Algorithmic bytes per launch: every k / v
     row read once, the output written once, the neighbour lists and relative positions read."""
     import numpy as np
     from mosaic_amd.healpix import get_healpix_grid
-    from mosaic_amd.interp import get_neighbors, rad_to_xyz
+    from mosaic_amd.interp import get_neighbors, rad_to_xyz, spatial_order
     lon = torch.linspace(0, 358.5, 240)
     lat = torch.linspace(-90, 90, 121)
     ll = torch.deg2rad(torch.stack(torch.meshgrid(lon, lat, indexing="ij"), -1).reshape(-1, 2))
@@ -273,6 +274,7 @@ def interp_leg(L, args, dev, stream):
         nb = torch.from_numpy(np.ascontiguousarray(get_neighbors(src.numpy(), dst.numpy(), k=K)))
         rel = torch.nn.functional.normalize(rad_to_xyz(dst).unsqueeze(1) - rad_to_xyz(src)[nb], dim=-1)
         nb_d, rel_d = nb.to(dev, torch.int32), rel.to(dev)
+        order = spatial_order(dst).to(dev, torch.int32)
         kv = torch.randn(len(src), B, 2 * H * 64, generator=gd, device=dev, dtype=torch.bfloat16)
         k = kv[..., :H * 64].unflatten(-1, (H, 64))
         v = kv[..., H * 64:].unflatten(-1, (H, 64))
@@ -283,8 +285,9 @@ def interp_leg(L, args, dev, stream):
             _lib.Bnhd(v.data_ptr(), v.stride(1), v.stride(0), v.stride(2))
 
         def call():
-            st = L.mosaic_knn_interp_fwd(kb, vb, nb_d.data_ptr(), rel_d.data_ptr(), w_q.data_ptr(), len(src),
-                                         len(dst), B, H, 64, K, 0.125, out.data_ptr(), sp)
+            st = L.mosaic_knn_interp_fwd_ordered(kb, vb, nb_d.data_ptr(), rel_d.data_ptr(), w_q.data_ptr(),
+                                                 order.data_ptr(), len(src), len(dst), B, H, 64, K, 0.125,
+                                                 out.data_ptr(), sp)
             if st:
                 raise RuntimeError(_lib.strerror(st))
         for _ in range(3):

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 8
+#define MOSAIC_BSA_ABI_VERSION 9
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -215,6 +215,21 @@ MOSAIC_API int mosaic_knn_interp_fwd(mosaic_bnhd k, mosaic_bnhd v, const int32_t
                                      int32_t num_to, int32_t batch, int32_t num_heads,
                                      int32_t head_dim, int32_t num_neighbors, float scale,
                                      void* out, void* stream);
+
+/* mosaic_knn_interp_fwd with the targets taken in a given order: target_order (int32
+   [num_to], 4-byte aligned) is a permutation of 0..num_to-1, or NULL for index order.  The
+   output is the same in any order (each target's row is computed alone); the order decides
+   which targets run at the same time, so an order along a space-filling curve of the target
+   positions keeps the neighbour rows they share in L2.  Entries outside [0, num_to) are
+   clamped; an order that is not a permutation leaves some rows of out unwritten.  Same
+   replacement as mosaic_knn_interp_fwd (primitives.py:265-283); the order is computed once
+   per grid pair with the neighbours (primitives.py:250-263). */
+MOSAIC_API int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors,
+                                             const float* rel_pos, const void* w_q,
+                                             const int32_t* target_order, int32_t num_from,
+                                             int32_t num_to, int32_t batch, int32_t num_heads,
+                                             int32_t head_dim, int32_t num_neighbors, float scale,
+                                             void* out, void* stream);
 
 /*
  * Selected-branch attention given block indices.  Replaces mosaic_sparse_attn /

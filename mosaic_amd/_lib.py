@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # mosaic_bsa_mode
 MODE_FULL = 0
@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_bsa_fwd_rope",
     "mosaic_bsa_fwd_proj",
     "mosaic_knn_interp_fwd",
+    "mosaic_knn_interp_fwd_ordered",
     "mosaic_sparse_attn_bwd_workspace_size",
     "mosaic_sparse_attn_bwd",
     "mosaic_rms_norm_fwd",
@@ -123,6 +124,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_knn_interp_fwd.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
                                           c_f, c_vp, c_vp]
     lib.mosaic_knn_interp_fwd.restype = c_int
+    lib.mosaic_knn_interp_fwd_ordered.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32,
+                                                  c_i32, c_i32, c_f, c_vp, c_vp]
+    lib.mosaic_knn_interp_fwd_ordered.restype = c_int
     c_i64 = ctypes.c_int64
     lib.mosaic_rms_norm_fwd.argtypes = [c_vp, c_vp, c_i32, c_i64, c_i32, c_i64, c_i64, c_vp, c_f, c_vp, c_vp,
                                         c_i32, c_vp]

@@ -515,6 +515,14 @@ int mosaic_pool_mean_fwd(mosaic_bnhd x, int32_t batch, int32_t seq_len, int32_t 
 int mosaic_knn_interp_fwd(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors, const float* rel_pos,
                           const void* w_q, int32_t num_from, int32_t num_to, int32_t batch, int32_t num_heads,
                           int32_t head_dim, int32_t num_neighbors, float scale, void* out, void* stream) {
+    return mosaic_knn_interp_fwd_ordered(k, v, neighbors, rel_pos, w_q, nullptr, num_from, num_to, batch,
+                                         num_heads, head_dim, num_neighbors, scale, out, stream);
+}
+
+int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors, const float* rel_pos,
+                                  const void* w_q, const int32_t* target_order, int32_t num_from, int32_t num_to,
+                                  int32_t batch, int32_t num_heads, int32_t head_dim, int32_t num_neighbors,
+                                  float scale, void* out, void* stream) {
     if (num_from <= 0 || num_to <= 0 || batch <= 0 || num_heads <= 0) return MOSAIC_ERR_SHAPE;
     if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
     if (num_neighbors <= 0 || num_neighbors > 32) return MOSAIC_ERR_BLOCK_COUNT;
@@ -522,9 +530,10 @@ int mosaic_knn_interp_fwd(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors
     if (int e = check_bnhd(v)) return e;
     if (neighbors == nullptr || rel_pos == nullptr || w_q == nullptr || out == nullptr) return MOSAIC_ERR_NULL_POINTER;
     if (!aligned16(out) || !aligned16(w_q) || reinterpret_cast<uintptr_t>(rel_pos) % 4 ||
-        reinterpret_cast<uintptr_t>(neighbors) % 4)
+        reinterpret_cast<uintptr_t>(neighbors) % 4 || reinterpret_cast<uintptr_t>(target_order) % 4)
         return MOSAIC_ERR_ALIGNMENT;
     InterpParams p{};
+    p.target_order = target_order;
     p.k = static_cast<const bf16_t*>(k.ptr); p.k_sn = k.stride_n; p.k_sb = k.stride_b; p.k_sh = k.stride_h;
     p.v = static_cast<const bf16_t*>(v.ptr); p.v_sn = v.stride_n; p.v_sb = v.stride_b; p.v_sh = v.stride_h;
     p.neighbors = neighbors;

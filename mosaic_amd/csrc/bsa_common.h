@@ -327,6 +327,7 @@ struct InterpParams {
     const bf16_t* k; int64_t k_sn, k_sb, k_sh;   // [S_from, B, H, 64]: point, member, head strides
     const bf16_t* v; int64_t v_sn, v_sb, v_sh;
     const int32_t* neighbors;                    // [S_to, K] source points of each target
+    const int32_t* target_order;                 // [S_to] order the targets are taken in, or null
     const float* rel_pos;                        // [S_to, K, 3] normalised relative positions
     const bf16_t* w_q;                           // [H * 64, 3] query projection (to_q.weight)
     bf16_t* out;                                 // [S_to, B, H, 64] contiguous

@@ -20,13 +20,15 @@
 // hides the latency of the reduction chains.
 //
 // One wave per (target s, head h) pair, looping over the batch members b with the next
-// member's rows in flight.  Lane l = 8 jg + dc holds the 8-dim chunk dc of neighbours
+// member's k / v loaded as soon as the current member is done with them.  Lane l = 8 jg + dc holds the 8-dim chunk dc of neighbours
 // jg + 8 i (its "slots"): every k / v read is a 16-byte load and each 128-byte row is read
 // by 8 adjacent lanes.  Scores are summed over the 8 chunk lanes with DPP (lanes l ^ 1,
 // l ^ 2, l ^ 4), the softmax max / sum over the 8 neighbour groups with DPP row_ror:8,
 // v_permlane16_swap and v_permlane32_swap; the output's 8 partial sums per lane are
 // reduce-scattered over the groups by the same three exchanges, leaving one dimension per
-// lane.  Workgroups are remapped so that each XCD takes one contiguous range of targets.
+// lane.  Workgroups are remapped so that each XCD takes one contiguous range of targets, in
+// the caller's target order when one is given: with targets sorted along a space-filling
+// curve, the waves in flight on an XCD share most of their neighbours' rows in its L2.
 #include "bsa_common.h"
 
 #include <type_traits>
@@ -136,7 +138,9 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t pair = (int64_t)xcd_remap(blockIdx.x, gridDim.x) * kInterpWaves + wave;
     if (pair >= (int64_t)p.S_to * p.H) return;  // wave-uniform; the kernel has no barrier
-    const int s = (int)(pair / p.H), h = (int)(pair - (int64_t)s * p.H);
+    const int pos = (int)(pair / p.H), h = (int)(pair - (int64_t)pos * p.H);
+    // targets outside [0, S_to) in the order are clamped (memory safety)
+    const int s = p.target_order ? min(max(p.target_order[pos], 0), p.S_to - 1) : pos;
     const int K = p.K, dc = lane & 7, jg = lane >> 3;
 
     // to_q rows h*64 + 8 dc .. + 7 (three bf16 weights each: 48 bytes, 16-byte aligned)

@@ -2,7 +2,7 @@
 
 Mirrors ``CrossAttentionInterpolate`` (primitives.py:230-283) and its helpers
 ``rad_to_xyz`` / ``get_neighbors`` (utils.py:7-17, 33-41).  The gather-attention in the
-middle of the forward runs in libmosaic_bsa.so (``mosaic_knn_interp_fwd``): the queries
+middle of the forward runs in libmosaic_bsa.so (``mosaic_knn_interp_fwd_ordered``): the queries
 ``to_q(rel_pos)`` and the gathered keys / values are never materialised.  The RMSNorm and the
 ``to_kv`` / ``to_o`` projections stay torch modules (library GEMMs).  Precision is that of the
 model under bf16 autocast: bf16 projections, fp32 softmax, bf16 output.
@@ -37,19 +37,36 @@ def get_neighbors(pos_from: np.ndarray, pos_to: np.ndarray, k: int = 8) -> np.nd
     return idx
 
 
+def spatial_order(pos_rad: torch.Tensor, bits: int = 10) -> torch.Tensor:
+    """A processing order of points (lon, lat in radians) along a Z-order (Morton) curve of
+    their unit vectors, each coordinate quantised to ``bits`` bits: int64 [len(pos_rad)], a
+    permutation.  Points close on the sphere come close in the order, so the targets that run
+    at the same time in the k-NN kernel share most of their neighbours."""
+    xyz = rad_to_xyz(pos_rad.detach().double().cpu()).numpy()
+    q = np.rint((xyz + 1.0) * 0.5 * ((1 << bits) - 1)).astype(np.int64)
+    code = np.zeros(len(q), dtype=np.int64)
+    for b in range(bits):
+        for c in range(3):
+            code |= ((q[:, c] >> b) & 1) << (3 * b + c)
+    return torch.from_numpy(np.argsort(code, kind="stable"))
+
+
 def _snhd(t: torch.Tensor) -> _lib.Bnhd:
     # [S, B, H, 64] -> the ABI's (stride_b = member, stride_n = point, stride_h = head)
     return _lib.Bnhd(t.data_ptr(), t.stride(1), t.stride(0), t.stride(2))
 
 
 def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel_pos: torch.Tensor,
-                  w_q: torch.Tensor, scale: float | None = None) -> torch.Tensor:
+                  w_q: torch.Tensor, scale: float | None = None,
+                  target_order: torch.Tensor | None = None) -> torch.Tensor:
     """The gather-attention of CrossAttentionInterpolate.forward (primitives.py:265-283).
 
     k, v: [S_from, B, H, 64] (views of the kv projection are fine); neighbors: [S_to, K]
     source indices; rel_pos: [S_to, K, 3]; w_q: [H*64, 3] (``to_q.weight``).  Returns
     [S_to, B, H, 64] bf16: for each target, softmax over its K neighbours of
-    ``to_q(rel_pos) . k * scale``, applied to v.
+    ``to_q(rel_pos) . k * scale``, applied to v.  ``target_order`` ([S_to], a permutation,
+    e.g. ``spatial_order`` of the target positions) changes only the order the targets are
+    computed in, not the result.
     """
     forward_only("knn_attention", k, v, rel_pos, w_q)
     if k.dim() != 4 or k.shape != v.shape or k.shape[-1] != 64:
@@ -73,11 +90,17 @@ def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel
     nb = neighbors.to(device=k.device, dtype=torch.int32).contiguous()
     rp = rel_pos.to(device=k.device, dtype=torch.float32).contiguous()
     wq = w_q.to(device=k.device, dtype=torch.bfloat16).contiguous()
+    order = None
+    if target_order is not None:
+        if tuple(target_order.shape) != (S_to,):
+            raise ValueError(f"target_order must be [S_to] = [{S_to}], got {tuple(target_order.shape)}")
+        order = target_order.to(device=k.device, dtype=torch.int32).contiguous()
     out = torch.empty(S_to, B, H, d, dtype=torch.bfloat16, device=k.device)
-    st = _lib.lib().mosaic_knn_interp_fwd(_snhd(k), _snhd(v), nb.data_ptr(), rp.data_ptr(), wq.data_ptr(),
-                                          S_from, S_to, B, H, d, K, 0.0 if scale is None else float(scale),
-                                          out.data_ptr(), stream_of(k))
-    _lib.check(st, "mosaic_knn_interp_fwd")
+    st = _lib.lib().mosaic_knn_interp_fwd_ordered(_snhd(k), _snhd(v), nb.data_ptr(), rp.data_ptr(), wq.data_ptr(),
+                                                  None if order is None else order.data_ptr(),
+                                                  S_from, S_to, B, H, d, K, 0.0 if scale is None else float(scale),
+                                                  out.data_ptr(), stream_of(k))
+    _lib.check(st, "mosaic_knn_interp_fwd_ordered")
     return out
 
 
@@ -103,6 +126,9 @@ class CrossAttentionInterpolate(nn.Module):
         self.to_o = nn.Linear(dim, dim, bias=False)
         self.register_buffer("neighbors", None, persistent=True)
         self.register_buffer("rel_pos", None, persistent=True)
+        # the kernel's target order (int32, not part of the state dict): derived from the
+        # target positions with the neighbours
+        self.register_buffer("target_order", None, persistent=False)
 
     @torch.no_grad()
     def initialize_interpolation_scheme(self, pos_from_rad: torch.Tensor, pos_to_rad: torch.Tensor):
@@ -113,6 +139,7 @@ class CrossAttentionInterpolate(nn.Module):
         rel = (to_xyz.unsqueeze(1) - from_xyz[neighbors]).contiguous()
         self.neighbors = neighbors
         self.rel_pos = torch.nn.functional.normalize(rel, dim=-1).contiguous()
+        self.target_order = spatial_order(pos_to_rad).to(device=pos_from_rad.device, dtype=torch.int32)
 
     def forward(self, x_from: torch.Tensor) -> torch.Tensor:
         if self.neighbors is None or self.rel_pos is None:
@@ -121,5 +148,5 @@ class CrossAttentionInterpolate(nn.Module):
         kv = self.to_kv(self.kv_norm(x_from))
         k = kv[..., :dim].unflatten(-1, (self.num_heads, self.head_dim))
         v = kv[..., dim:].unflatten(-1, (self.num_heads, self.head_dim))
-        out = knn_attention(k, v, self.neighbors, self.rel_pos, self.to_q.weight, self.scale)
+        out = knn_attention(k, v, self.neighbors, self.rel_pos, self.to_q.weight, self.scale, self.target_order)
         return self.to_o(out.to(x_from.dtype).flatten(-2))

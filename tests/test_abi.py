@@ -211,6 +211,13 @@ def test_knn_interp_entry_validates():
     assert call(wq=FAKE + 8) == 7 and call(out=FAKE + 2) == 7 and call(rel=FAKE + 2) == 7
     assert call(kk=_lib.Bnhd(FAKE + 2, 3 * 64, 2 * 3 * 64, 64)) == 7
 
+    def ordered(order=None, **kw):
+        a = {**ok, **kw}
+        return L.mosaic_knn_interp_fwd_ordered(t, t, FAKE, FAKE, FAKE, order, a["num_from"], a["num_to"], a["batch"],
+                                               a["heads"], a["d"], a["K"], 0.0, FAKE, None)
+    assert ordered(order=FAKE + 2) == 7                  # the order's int32 entries need 4-byte alignment
+    assert ordered(order=FAKE, d=32) == 2 and ordered(order=FAKE, K=33) == 5
+
 
 def test_backward_entry_validates():
     L = _lib.lib()

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from mosaic_amd.healpix import get_healpix_grid
-from mosaic_amd.interp import CrossAttentionInterpolate, get_neighbors, knn_attention, rad_to_xyz
+from mosaic_amd.interp import CrossAttentionInterpolate, get_neighbors, knn_attention, rad_to_xyz, spatial_order
 from oracle import interp_oracle as IO
 
 pytestmark = pytest.mark.gpu
@@ -190,3 +190,20 @@ def test_knn_attention_negative_point_stride_equals_forward_order():
     _lib.check(st, "mosaic_knn_interp_fwd")
     torch.cuda.synchronize()
     assert torch.equal(out, fwd)
+
+
+@pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
+def test_knn_attention_target_order_leaves_the_output_unchanged(direction):
+    """The targets taken in the spatial order, in a random order and in index order: the same
+    output bit for bit (each target's row is computed alone)."""
+    ll, hp = lonlat_grid(48, 25), torch.deg2rad(get_healpix_grid(8))
+    src, dst = (ll, hp) if direction == "ll_to_hp" else (hp, ll)
+    nb, rel = [t.to(DEV) for t in scheme(src, dst, 24)]
+    k, v = rand(len(src), 3, 2, 64, seed=60).to(DEV), rand(len(src), 3, 2, 64, seed=61).to(DEV)
+    w_q = rand(2 * 64, 3, seed=62).to(DEV)
+    base = knn_attention(k, v, nb, rel, w_q, 0.125)
+    g = torch.Generator().manual_seed(63)
+    for order in (spatial_order(dst), torch.randperm(len(dst), generator=g)):
+        assert torch.equal(knn_attention(k, v, nb, rel, w_q, 0.125, target_order=order.to(DEV)), base)
+    with pytest.raises(ValueError, match="target_order"):
+        knn_attention(k, v, nb, rel, w_q, 0.125, target_order=torch.arange(3, device=DEV))

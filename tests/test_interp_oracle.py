@@ -129,7 +129,26 @@ def test_module_scheme_on_cpu():
     nb, rel = _scheme(ll, hp, 8)
     assert torch.equal(m.neighbors, nb) and torch.equal(m.rel_pos, rel)
     assert set(m.state_dict()) >= {"neighbors", "rel_pos"}
+    assert "target_order" not in m.state_dict()          # derived, not a checkpoint entry
+    assert sorted(m.target_order.tolist()) == list(range(len(hp)))
     with torch.no_grad(), pytest.raises(ValueError):   # the gather-attention runs on the device only
         m(torch.zeros(84, 1, 128))
     with pytest.raises(RuntimeError, match="no backward"):   # to_q / to_kv weights require grad
         m(torch.zeros(84, 1, 128))
+
+
+def test_spatial_order_is_a_permutation_that_follows_the_sphere():
+    """The k-NN kernel's target order: a permutation whose consecutive points are close (a
+    shuffled HEALPix grid, nside 16: mean step < 2.5 grid spacings, against ~1.3 shuffled);
+    identical positions keep their given order (stable)."""
+    from mosaic_amd.interp import spatial_order
+    hp = torch.deg2rad(get_healpix_grid(16))
+    pts = hp[torch.randperm(len(hp), generator=torch.Generator().manual_seed(0))]
+    o = spatial_order(pts)
+    assert o.dtype == torch.int64 and sorted(o.tolist()) == list(range(len(pts)))
+    xyz = rad_to_xyz(pts.double())
+    step = lambda idx: (xyz[idx][1:] - xyz[idx][:-1]).norm(dim=-1).mean().item()
+    spacing = math.sqrt(4 * math.pi / len(pts))
+    assert step(o) < 2.5 * spacing and step(torch.arange(len(pts))) > 10 * spacing
+    same = torch.zeros(5, 2)
+    assert spatial_order(same).tolist() == [0, 1, 2, 3, 4]
