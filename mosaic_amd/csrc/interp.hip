@@ -77,7 +77,9 @@ __device__ __forceinline__ float group_sum(float x) {
 __device__ __forceinline__ float group_max(float x) {
     x = dpp_max<0x128>(x);
     const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return xor32_max(fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1])));
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // Eight exact bf16 products, rounded to bf16 in pairs:
@@ -132,8 +134,12 @@ __device__ __forceinline__ uint4 ld_member(const bf16_t* base, Off off) {
     }
 }
 
+// Waves per SIMD each instantiation is compiled for (the register budget): 6 at three slots
+// with 32-bit offsets (the model's K = 24), what fits without spilling elsewhere.
+constexpr int knn_waves(int nslot, bool off32) { return nslot <= 1 ? 8 : nslot == 2 ? 7 : nslot == 3 ? (off32 ? 6 : 5) : 4; }
+
 template <int NSLOT, bool OFF32, bool POW2>
-__global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParams p) {
+__global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_eu(knn_waves(NSLOT, OFF32)))) void knn_attn_kernel(InterpParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t pair = (int64_t)xcd_remap(blockIdx.x, gridDim.x) * kInterpWaves + wave;
@@ -189,7 +195,7 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
     for (int b = 0; b < p.B; ++b) {
         const bool more = b + 1 < p.B;
         // scores of this lane's slots (every lane of a neighbour group holds its score)
-        float sc[NSLOT], m = -INFINITY;
+        float sc[NSLOT], m;
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
             const uint32_t kd[8] = {kw[i].x, kw[i].x, kw[i].y, kw[i].y, kw[i].z, kw[i].z, kw[i].w, kw[i].w};
@@ -203,8 +209,9 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
             // to be normal is below 2^-126 in magnitude, and so is the difference its rounding
             // would make: the softmax weights come out the same)
             const float t = POW2 ? round_bf16(part) * p.scale : round_bf16(round_bf16(part) * p.scale);
-            sc[i] = jg + 8 * i < K ? t : -INFINITY;
-            m = fmaxf(m, sc[i]);
+            // only the last slot can hold absent neighbours (j >= K): NSLOT = ceil(K / 8)
+            sc[i] = i < NSLOT - 1 || jg + 8 * i < K ? t : -INFINITY;
+            m = i == 0 ? sc[0] : fmaxf(m, sc[i]);
         }
         if (more) {
 #pragma unroll
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_attn_kernel(InterpParam
         float ex[NSLOT], l = 0.f;
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
-            ex[i] = jg + 8 * i < K ? __expf(sc[i] - m) : 0.f;
+            ex[i] = __expf(sc[i] - m);  // 0 for an absent neighbour (score -inf; m is finite)
             l += ex[i];
         }
         const float inv = __builtin_amdgcn_rcpf(group_sum(l));
