@@ -109,9 +109,85 @@ __device__ __forceinline__ void prod8_round4(const uint32_t (&a)[8], const uint3
         : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
           "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(b[4]), "v"(b[5]), "v"(b[6]), "v"(b[7]));
 }
-// c + the two bf16 halves of the packed pair pr, by a dot product with (1, 1)
-__device__ __forceinline__ float add_pair(uint32_t pr, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr), __builtin_bit_cast(bf16x2_t, 0x3f803f80u), c, false);
+// A neighbour's score partial over this lane's 8 dimensions: the eight products q[i] . k
+// (q[i] = (x, 0) or (0, x) against the packed pairs of k, as above), rounded to bf16 in pairs
+// and added in fp32 by dot products with ones = (1, 1), in dimension order from 0.  The
+// additions chain through the accumulator operand of the same instruction, which needs no
+// wait; the result waits three states (s_nop 2) before any other instruction reads it.
+__device__ __forceinline__ float score_partial(const uint32_t (&q)[8], const uint4& k, uint32_t ones) {
+    float part, t0, t1, t2, t3, t4, t5, t6, t7;
+    uint32_t c0, c1, c2, c3;
+    asm("v_dot2_f32_bf16 %5, %13, %21, 0\n\t"
+        "v_dot2_f32_bf16 %6, %14, %21, 0\n\t"
+        "v_dot2_f32_bf16 %7, %15, %22, 0\n\t"
+        "v_dot2_f32_bf16 %8, %16, %22, 0\n\t"
+        "v_dot2_f32_bf16 %9, %17, %23, 0\n\t"
+        "v_dot2_f32_bf16 %10, %18, %23, 0\n\t"
+        "v_dot2_f32_bf16 %11, %19, %24, 0\n\t"
+        "v_dot2_f32_bf16 %12, %20, %24, 0\n\t"
+        "v_cvt_pk_bf16_f32 %1, %5, %6\n\t"
+        "v_cvt_pk_bf16_f32 %2, %7, %8\n\t"
+        "v_cvt_pk_bf16_f32 %3, %9, %10\n\t"
+        "v_cvt_pk_bf16_f32 %4, %11, %12\n\t"
+        "v_dot2_f32_bf16 %0, %1, %25, 0\n\t"
+        "v_dot2_f32_bf16 %0, %2, %25, %0\n\t"
+        "v_dot2_f32_bf16 %0, %3, %25, %0\n\t"
+        "v_dot2_f32_bf16 %0, %4, %25, %0\n\t"
+        "s_nop 2"
+        : "=v"(part), "=v"(c0), "=v"(c1), "=v"(c2), "=v"(c3),
+          "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
+        : "v"(q[0]), "v"(q[1]), "v"(q[2]), "v"(q[3]), "v"(q[4]), "v"(q[5]), "v"(q[6]), "v"(q[7]),
+          "v"(k.x), "v"(k.y), "v"(k.z), "v"(k.w), "s"(ones));
+    return part;
+}
+
+// Two neighbours' (weights a and b) contributions to four output dimensions 2m .. 2m + 3:
+// acc[e] (+)= bf16(wa v_a[d]) + bf16(wb v_b[d]) for d = 2m + e, the products formed as above
+// from (w, 0) / (0, w) and the packed pairs va0 = v_a[2m, 2m+1], va1 = v_a[2m+2, 2m+3] (vb0,
+// vb1 of b), each pair rounded by one v_cvt_pk_bf16_f32 and added by a dot product with
+// (1, 1) -- starting from 0 when FIRST.  Ends with the three wait states the sums need.
+template <bool FIRST>
+__device__ __forceinline__ void out_pair(uint32_t wa_lo, uint32_t wb_lo, uint32_t wa_hi, uint32_t wb_hi,
+                                         uint32_t va0, uint32_t vb0, uint32_t va1, uint32_t vb1, uint32_t ones,
+                                         float* acc) {
+    float t0, t1, t2, t3, t4, t5, t6, t7;
+    uint32_t c0, c1, c2, c3;
+#define MOSAIC_OUT_PAIR_PRODUCTS                          \
+    "v_dot2_f32_bf16 %8, %16, %20, 0\n\t"                \
+    "v_dot2_f32_bf16 %9, %17, %21, 0\n\t"                \
+    "v_dot2_f32_bf16 %10, %18, %20, 0\n\t"               \
+    "v_dot2_f32_bf16 %11, %19, %21, 0\n\t"               \
+    "v_dot2_f32_bf16 %12, %16, %22, 0\n\t"               \
+    "v_dot2_f32_bf16 %13, %17, %23, 0\n\t"               \
+    "v_dot2_f32_bf16 %14, %18, %22, 0\n\t"               \
+    "v_dot2_f32_bf16 %15, %19, %23, 0\n\t"               \
+    "v_cvt_pk_bf16_f32 %4, %8, %9\n\t"                   \
+    "v_cvt_pk_bf16_f32 %5, %10, %11\n\t"                 \
+    "v_cvt_pk_bf16_f32 %6, %12, %13\n\t"                 \
+    "v_cvt_pk_bf16_f32 %7, %14, %15\n\t"
+#define MOSAIC_OUT_PAIR_OPERANDS                                                                      \
+    "=v"(c0), "=v"(c1), "=v"(c2), "=v"(c3),                                                           \
+        "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)      \
+        : "v"(wa_lo), "v"(wb_lo), "v"(wa_hi), "v"(wb_hi), "v"(va0), "v"(vb0), "v"(va1), "v"(vb1), "s"(ones)
+    if constexpr (FIRST) {
+        asm(MOSAIC_OUT_PAIR_PRODUCTS
+            "v_dot2_f32_bf16 %0, %4, %24, 0\n\t"
+            "v_dot2_f32_bf16 %1, %5, %24, 0\n\t"
+            "v_dot2_f32_bf16 %2, %6, %24, 0\n\t"
+            "v_dot2_f32_bf16 %3, %7, %24, 0\n\t"
+            "s_nop 2"
+            : "=v"(acc[0]), "=v"(acc[1]), "=v"(acc[2]), "=v"(acc[3]), MOSAIC_OUT_PAIR_OPERANDS);
+    } else {
+        asm(MOSAIC_OUT_PAIR_PRODUCTS
+            "v_dot2_f32_bf16 %0, %4, %24, %0\n\t"
+            "v_dot2_f32_bf16 %1, %5, %24, %1\n\t"
+            "v_dot2_f32_bf16 %2, %6, %24, %2\n\t"
+            "v_dot2_f32_bf16 %3, %7, %24, %3\n\t"
+            "s_nop 2"
+            : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), MOSAIC_OUT_PAIR_OPERANDS);
+    }
+#undef MOSAIC_OUT_PAIR_PRODUCTS
+#undef MOSAIC_OUT_PAIR_OPERANDS
 }
 
 __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
@@ -192,19 +268,14 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
     uint4 kw[NSLOT], vw[NSLOT];
 #pragma unroll
     for (int i = 0; i < NSLOT; ++i) { kw[i] = ld_member<OFF32>(p.k, koff[i]); vw[i] = ld_member<OFF32>(p.v, voff[i]); }
+    const uint32_t ones = 0x3f803f80u;  // the bf16 pair (1, 1)
     for (int b = 0; b < p.B; ++b) {
         const bool more = b + 1 < p.B;
         // scores of this lane's slots (every lane of a neighbour group holds its score)
         float sc[NSLOT], m;
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
-            const uint32_t kd[8] = {kw[i].x, kw[i].x, kw[i].y, kw[i].y, kw[i].z, kw[i].z, kw[i].w, kw[i].w};
-            uint32_t pr[4];
-            prod8_round4(qp[i], kd, pr);
-            float part = 0.f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) part = add_pair(pr[e], part);
-            part = chunk_sum(part);
+            const float part = chunk_sum(score_partial(qp[i], kw[i], ones));
             // a power-of-two scale leaves bf16(part) * scale a bf16 value (a product too small
             // to be normal is below 2^-126 in magnitude, and so is the difference its rounding
             // would make: the softmax weights come out the same)
@@ -231,32 +302,27 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
         // each product is one dot product of (w, 0) or (0, w) with a packed pair of v.
         float acc[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-#pragma unroll
         for (int i = 0; i < NSLOT; i += 2) {
-            const uint32_t va[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
             const uint32_t wa_hi = __float_as_uint(round_bf16(ex[i] * inv)), wa_lo = wa_hi >> 16;
             if (i + 1 < NSLOT) {
-                const uint32_t vb[4] = {vw[i + 1].x, vw[i + 1].y, vw[i + 1].z, vw[i + 1].w};
                 const uint32_t wb_hi = __float_as_uint(round_bf16(ex[i + 1] * inv)), wb_lo = wb_hi >> 16;
-                const uint32_t w8[8] = {wa_lo, wb_lo, wa_hi, wb_hi, wa_lo, wb_lo, wa_hi, wb_hi};
-#pragma unroll
-                for (int m = 0; m < 4; m += 2) {
-                    const uint32_t v8[8] = {va[m], vb[m], va[m], vb[m], va[m + 1], vb[m + 1], va[m + 1], vb[m + 1]};
-                    uint32_t pr[4];
-                    prod8_round4(w8, v8, pr);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[2 * m + e] = add_pair(pr[e], acc[2 * m + e]);
+                const uint4 &va = vw[i], &vb = vw[i + 1];
+                if (i == 0) {
+                    out_pair<true>(wa_lo, wb_lo, wa_hi, wb_hi, va.x, vb.x, va.y, vb.y, ones, acc);
+                    out_pair<true>(wa_lo, wb_lo, wa_hi, wb_hi, va.z, vb.z, va.w, vb.w, ones, acc + 4);
+                } else {
+                    out_pair<false>(wa_lo, wb_lo, wa_hi, wb_hi, va.x, vb.x, va.y, vb.y, ones, acc);
+                    out_pair<false>(wa_lo, wb_lo, wa_hi, wb_hi, va.z, vb.z, va.w, vb.w, ones, acc + 4);
                 }
             } else {
                 const uint32_t w8[8] = {wa_lo, wa_hi, wa_lo, wa_hi, wa_lo, wa_hi, wa_lo, wa_hi};
-                const uint32_t v8[8] = {va[0], va[0], va[1], va[1], va[2], va[2], va[3], va[3]};
+                const uint32_t v8[8] = {vw[i].x, vw[i].x, vw[i].y, vw[i].y, vw[i].z, vw[i].z, vw[i].w, vw[i].w};
                 uint32_t pr[4];
                 prod8_round4(w8, v8, pr);
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
-                    acc[2 * m] += bf_lo(pr[m]);
-                    acc[2 * m + 1] += bf_hi(pr[m]);
+                    acc[2 * m] = i == 0 ? bf_lo(pr[m]) : acc[2 * m] + bf_lo(pr[m]);
+                    acc[2 * m + 1] = i == 0 ? bf_hi(pr[m]) : acc[2 * m + 1] + bf_hi(pr[m]);
                 }
             }
         }
