@@ -343,9 +343,9 @@ STAGE2_NSIDE32_B24_MODEL = Workload("bsa_nside32_b24_h16kv4_bl1024_bs128_top12",
                                     True)
 
 
-@pytest.mark.parametrize("wl,nsample", [(STAGE1_NSIDE64, 24), (STAGE2_NSIDE32_B24, 6), (scaling_workload(32), 16),
-                                         (scaling_workload(128), 16), (STAGE1_NSIDE64_MODEL, 12),
-                                         (STAGE2_NSIDE32_B24_MODEL, 6)],
+@pytest.mark.parametrize("wl,nsample", [(STAGE1_NSIDE64, 96), (STAGE2_NSIDE32_B24, 24), (scaling_workload(32), 48),
+                                         (scaling_workload(128), 48), (STAGE1_NSIDE64_MODEL, 48),
+                                         (STAGE2_NSIDE32_B24_MODEL, 24)],
                          ids=["nside64", "nside32_b24", "sweep_nside32", "sweep_nside128", "nside64_model_blocks",
                               "nside32_b24_model_blocks"])
 def test_full_size_workloads(wl, nsample):
