@@ -544,6 +544,7 @@ int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const int32_t* n
     p.scale = resolve_scale(scale, head_dim);
     int exp2 = 0;
     p.scale_pow2 = std::isfinite(p.scale) && p.scale >= 0x1p-126f && std::frexp(p.scale, &exp2) == 0.5f;
+    p.scale_log2e = p.scale * kLog2e;
     return launch_status(launch_knn_attn(p, static_cast<hipStream_t>(stream)));
 }
 

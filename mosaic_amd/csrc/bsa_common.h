@@ -333,6 +333,7 @@ struct InterpParams {
     bf16_t* out;                                 // [S_to, B, H, 64] contiguous
     int S_from, S_to, B, H, K;
     float scale;
+    float scale_log2e;                           // scale * log2 e
     int scale_pow2;                              // scale is a power of two
 };
 hipError_t launch_knn_attn(const InterpParams& p, hipStream_t s);

@@ -82,38 +82,18 @@ __device__ __forceinline__ float group_max(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// Eight exact bf16 products, rounded to bf16 in pairs:
-//   c[j] = (bf16(t[2j]), bf16(t[2j + 1])) packed,  t[i] = a[i] . b[i]  (v_dot2_f32_bf16)
-// where a[i] is (x, 0) or (0, x), x bf16 in the low or high half, so t[i] is x times the
-// matching half of the packed pair b[i] (a bf16 x bf16 product is exact in fp32) -- no
-// element is unpacked to fp32.  A dot product's result needs three wait states before another
-// VALU instruction reads it, and the compiler does not track that through inline assembly:
-// the eight products go first and every rounding reads products at least three instructions
-// old.  c may share registers with a and b (read only by the products); t may not.
-__device__ __forceinline__ void prod8_round4(const uint32_t (&a)[8], const uint32_t (&b)[8], uint32_t (&c)[4]) {
-    float t0, t1, t2, t3, t4, t5, t6, t7;
-    asm("v_dot2_f32_bf16 %4, %12, %20, 0\n\t"
-        "v_dot2_f32_bf16 %5, %13, %21, 0\n\t"
-        "v_dot2_f32_bf16 %6, %14, %22, 0\n\t"
-        "v_dot2_f32_bf16 %7, %15, %23, 0\n\t"
-        "v_dot2_f32_bf16 %8, %16, %24, 0\n\t"
-        "v_dot2_f32_bf16 %9, %17, %25, 0\n\t"
-        "v_dot2_f32_bf16 %10, %18, %26, 0\n\t"
-        "v_dot2_f32_bf16 %11, %19, %27, 0\n\t"
-        "v_cvt_pk_bf16_f32 %0, %4, %5\n\t"
-        "v_cvt_pk_bf16_f32 %1, %6, %7\n\t"
-        "v_cvt_pk_bf16_f32 %2, %8, %9\n\t"
-        "v_cvt_pk_bf16_f32 %3, %10, %11"
-        : "=v"(c[0]), "=v"(c[1]), "=v"(c[2]), "=v"(c[3]),
-          "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)
-        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
-          "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]), "v"(b[4]), "v"(b[5]), "v"(b[6]), "v"(b[7]));
-}
+// Exact bf16 products without unpacking: with a = (x, 0) or (0, x) (x bf16 in the low or
+// high half), v_dot2_f32_bf16 of a and a packed bf16 pair b is x times the matching half of b,
+// plus 0 (a bf16 x bf16 product is exact in fp32).  A dot product's result needs three wait
+// states before another VALU instruction reads it, and the compiler does not track that
+// through inline assembly, so the blocks below put their eight products first, every
+// rounding (v_cvt_pk_bf16_f32 of a pair) reads products at least three instructions old, and
+// each block ends with s_nop 2 before its sums are read.  The additions are dot products
+// too, chained through the accumulator operand of the same instruction, which needs no wait.
+//
 // A neighbour's score partial over this lane's 8 dimensions: the eight products q[i] . k
-// (q[i] = (x, 0) or (0, x) against the packed pairs of k, as above), rounded to bf16 in pairs
-// and added in fp32 by dot products with ones = (1, 1), in dimension order from 0.  The
-// additions chain through the accumulator operand of the same instruction, which needs no
-// wait; the result waits three states (s_nop 2) before any other instruction reads it.
+// (q[i] = (x, 0) or (0, x) against the packed pairs of k), rounded to bf16 in pairs and added
+// in fp32 by dot products with ones = (1, 1), in dimension order from 0.
 __device__ __forceinline__ float score_partial(const uint32_t (&q)[8], const uint4& k, uint32_t ones) {
     float part, t0, t1, t2, t3, t4, t5, t6, t7;
     uint32_t c0, c1, c2, c3;
@@ -188,6 +168,64 @@ __device__ __forceinline__ void out_pair(uint32_t wa_lo, uint32_t wb_lo, uint32_
     }
 #undef MOSAIC_OUT_PAIR_PRODUCTS
 #undef MOSAIC_OUT_PAIR_OPERANDS
+}
+
+// One neighbour (weight w, as (w, 0) and (0, w)) against all eight output dimensions of the
+// lane: acc[d] (+)= bf16(w v[d]), the pair (2m, 2m + 1) rounded by one v_cvt_pk_bf16_f32 and
+// its halves added by dot products with pick_lo = (1, 0) and pick_hi = (0, 1) (scalar
+// registers: as a constant operand the compiler would encode (1, 0) as the inline constant
+// 1.0, which the dot product reads as (0, 1)) -- starting from 0 when FIRST.
+template <bool FIRST>
+__device__ __forceinline__ void out_single(uint32_t w_lo, uint32_t w_hi, const uint4& v, uint32_t pick_lo,
+                                           uint32_t pick_hi, float* acc) {
+    float t0, t1, t2, t3, t4, t5, t6, t7;
+    uint32_t c0, c1, c2, c3;
+#define MOSAIC_OUT_SINGLE_PRODUCTS                        \
+    "v_dot2_f32_bf16 %12, %20, %22, 0\n\t"               \
+    "v_dot2_f32_bf16 %13, %21, %22, 0\n\t"               \
+    "v_dot2_f32_bf16 %14, %20, %23, 0\n\t"               \
+    "v_dot2_f32_bf16 %15, %21, %23, 0\n\t"               \
+    "v_dot2_f32_bf16 %16, %20, %24, 0\n\t"               \
+    "v_dot2_f32_bf16 %17, %21, %24, 0\n\t"               \
+    "v_dot2_f32_bf16 %18, %20, %25, 0\n\t"               \
+    "v_dot2_f32_bf16 %19, %21, %25, 0\n\t"               \
+    "v_cvt_pk_bf16_f32 %8, %12, %13\n\t"                 \
+    "v_cvt_pk_bf16_f32 %9, %14, %15\n\t"                 \
+    "v_cvt_pk_bf16_f32 %10, %16, %17\n\t"                \
+    "v_cvt_pk_bf16_f32 %11, %18, %19\n\t"
+#define MOSAIC_OUT_SINGLE_OPERANDS                                                                    \
+    "=v"(c0), "=v"(c1), "=v"(c2), "=v"(c3),                                                           \
+        "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5), "=&v"(t6), "=&v"(t7)      \
+        : "v"(w_lo), "v"(w_hi), "v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w), "s"(pick_lo), "s"(pick_hi)
+    if constexpr (FIRST) {
+        asm(MOSAIC_OUT_SINGLE_PRODUCTS
+            "v_dot2_f32_bf16 %0, %8, %26, 0\n\t"
+            "v_dot2_f32_bf16 %1, %8, %27, 0\n\t"
+            "v_dot2_f32_bf16 %2, %9, %26, 0\n\t"
+            "v_dot2_f32_bf16 %3, %9, %27, 0\n\t"
+            "v_dot2_f32_bf16 %4, %10, %26, 0\n\t"
+            "v_dot2_f32_bf16 %5, %10, %27, 0\n\t"
+            "v_dot2_f32_bf16 %6, %11, %26, 0\n\t"
+            "v_dot2_f32_bf16 %7, %11, %27, 0\n\t"
+            "s_nop 2"
+            : "=v"(acc[0]), "=v"(acc[1]), "=v"(acc[2]), "=v"(acc[3]), "=v"(acc[4]), "=v"(acc[5]), "=v"(acc[6]),
+              "=v"(acc[7]), MOSAIC_OUT_SINGLE_OPERANDS);
+    } else {
+        asm(MOSAIC_OUT_SINGLE_PRODUCTS
+            "v_dot2_f32_bf16 %0, %8, %26, %0\n\t"
+            "v_dot2_f32_bf16 %1, %8, %27, %1\n\t"
+            "v_dot2_f32_bf16 %2, %9, %26, %2\n\t"
+            "v_dot2_f32_bf16 %3, %9, %27, %3\n\t"
+            "v_dot2_f32_bf16 %4, %10, %26, %4\n\t"
+            "v_dot2_f32_bf16 %5, %10, %27, %5\n\t"
+            "v_dot2_f32_bf16 %6, %11, %26, %6\n\t"
+            "v_dot2_f32_bf16 %7, %11, %27, %7\n\t"
+            "s_nop 2"
+            : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]), "+v"(acc[6]),
+              "+v"(acc[7]), MOSAIC_OUT_SINGLE_OPERANDS);
+    }
+#undef MOSAIC_OUT_SINGLE_PRODUCTS
+#undef MOSAIC_OUT_SINGLE_OPERANDS
 }
 
 __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
@@ -268,7 +306,7 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
     uint4 kw[NSLOT], vw[NSLOT];
 #pragma unroll
     for (int i = 0; i < NSLOT; ++i) { kw[i] = ld_member<OFF32>(p.k, koff[i]); vw[i] = ld_member<OFF32>(p.v, voff[i]); }
-    const uint32_t ones = 0x3f803f80u;  // the bf16 pair (1, 1)
+    const uint32_t ones = 0x3f803f80u, pick_lo = 0x3f80u, pick_hi = 0x3f800000u;  // bf16 pairs (1, 1), (1, 0), (0, 1)
     for (int b = 0; b < p.B; ++b) {
         const bool more = b + 1 < p.B;
         // scores of this lane's slots (every lane of a neighbour group holds its score)
@@ -276,10 +314,11 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
             const float part = chunk_sum(score_partial(qp[i], kw[i], ones));
-            // a power-of-two scale leaves bf16(part) * scale a bf16 value (a product too small
-            // to be normal is below 2^-126 in magnitude, and so is the difference its rounding
-            // would make: the softmax weights come out the same)
-            const float t = POW2 ? round_bf16(part) * p.scale : round_bf16(round_bf16(part) * p.scale);
+            // the score in base-2 units, sc = bf16(bf16(part) * scale) * log2 e.  A power-of-two
+            // scale leaves bf16(part) * scale a bf16 value (a product too small to be normal is
+            // below 2^-126 in magnitude, and so is the difference its rounding would make), so
+            // that case takes one multiply by scale * log2 e.
+            const float t = POW2 ? round_bf16(part) * p.scale_log2e : round_bf16(round_bf16(part) * p.scale) * kLog2e;
             // only the last slot can hold absent neighbours (j >= K): NSLOT = ceil(K / 8)
             sc[i] = i < NSLOT - 1 || jg + 8 * i < K ? t : -INFINITY;
             m = i == 0 ? sc[0] : fmaxf(m, sc[i]);
@@ -292,7 +331,7 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
         float ex[NSLOT], l = 0.f;
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
-            ex[i] = __expf(sc[i] - m);  // 0 for an absent neighbour (score -inf; m is finite)
+            ex[i] = __builtin_amdgcn_exp2f(sc[i] - m);  // 0 for an absent neighbour (score -inf; m is finite)
             l += ex[i];
         }
         const float inv = __builtin_amdgcn_rcpf(group_sum(l));
@@ -303,9 +342,12 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
         float acc[8];
 #pragma unroll
         for (int i = 0; i < NSLOT; i += 2) {
-            const uint32_t wa_hi = __float_as_uint(round_bf16(ex[i] * inv)), wa_lo = wa_hi >> 16;
+            // the weight as (w, 0) and (0, w): one conversion each
+            const float xa = ex[i] * inv;
+            const uint32_t wa_lo = pack_bf16x2(xa, 0.f), wa_hi = pack_bf16x2(0.f, xa);
             if (i + 1 < NSLOT) {
-                const uint32_t wb_hi = __float_as_uint(round_bf16(ex[i + 1] * inv)), wb_lo = wb_hi >> 16;
+                const float xb = ex[i + 1] * inv;
+                const uint32_t wb_lo = pack_bf16x2(xb, 0.f), wb_hi = pack_bf16x2(0.f, xb);
                 const uint4 &va = vw[i], &vb = vw[i + 1];
                 if (i == 0) {
                     out_pair<true>(wa_lo, wb_lo, wa_hi, wb_hi, va.x, vb.x, va.y, vb.y, ones, acc);
@@ -314,16 +356,10 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
                     out_pair<false>(wa_lo, wb_lo, wa_hi, wb_hi, va.x, vb.x, va.y, vb.y, ones, acc);
                     out_pair<false>(wa_lo, wb_lo, wa_hi, wb_hi, va.z, vb.z, va.w, vb.w, ones, acc + 4);
                 }
+            } else if (i == 0) {
+                out_single<true>(wa_lo, wa_hi, vw[i], pick_lo, pick_hi, acc);
             } else {
-                const uint32_t w8[8] = {wa_lo, wa_hi, wa_lo, wa_hi, wa_lo, wa_hi, wa_lo, wa_hi};
-                const uint32_t v8[8] = {vw[i].x, vw[i].x, vw[i].y, vw[i].y, vw[i].z, vw[i].z, vw[i].w, vw[i].w};
-                uint32_t pr[4];
-                prod8_round4(w8, v8, pr);
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    acc[2 * m] = i == 0 ? bf_lo(pr[m]) : acc[2 * m] + bf_lo(pr[m]);
-                    acc[2 * m + 1] = i == 0 ? bf_hi(pr[m]) : acc[2 * m + 1] + bf_hi(pr[m]);
-                }
+                out_single<false>(wa_lo, wa_hi, vw[i], pick_lo, pick_hi, acc);
             }
         }
         if (more) {
