@@ -325,7 +325,9 @@ def interp_leg(L, args, dev, stream):
 
 def bwd_leg(L, q, k, v, wl, args, dev, stream):
     """Backward of the selected branch (MosaicAttnFunction.backward, ops.py:437-554) on the
-    workload's q/k/v with a random top-K selection per (query block, kv head).  FLOPs per
+    workload's q/k/v with a random top-K selection per (query block, kv head), or with
+    ``--bwd-selection local`` the K blocks around each query block (selections that follow
+    spatial proximity, as the model's do on the HEALPix nested order).  FLOPs per
     (64-query tile, 64-key tile, head): 3 products of 2*64^3 for grad q (q'k, do.v, dS.k) and 4
     for grad k / v (k.q', v.do, P.do, dS.q')."""
     from mosaic_amd.ops import mosaic_attn_bwd, mosaic_attn_fwd
@@ -334,7 +336,11 @@ def bwd_leg(L, q, k, v, wl, args, dev, stream):
     bs, K = wl.sparse_block_size, wl.sparse_block_count
     nb = N // bs
     g = torch.Generator().manual_seed(args.seed)
-    idx = torch.stack([torch.randperm(nb, generator=g)[:K] for _ in range(B * nb * Hk)]).view(B, nb, Hk, K).to(dev)
+    if args.bwd_selection == "local":
+        start = (torch.arange(nb).view(nb, 1) - K // 2).clamp(0, nb - K)
+        idx = (start + torch.arange(K).view(1, K)).view(1, nb, 1, K).expand(B, nb, Hk, K).contiguous().to(dev)
+    else:
+        idx = torch.stack([torch.randperm(nb, generator=g)[:K] for _ in range(B * nb * Hk)]).view(B, nb, Hk, K).to(dev)
     do = torch.randn(B, N, Hq, d, generator=torch.Generator(device=dev).manual_seed(args.seed), device=dev,
                      dtype=torch.bfloat16)
     o, lse = mosaic_attn_fwd(q, k, v, idx, bs, 0.125)
@@ -359,7 +365,7 @@ def bwd_leg(L, q, k, v, wl, args, dev, stream):
     ev.close()
     units = B * Hq * (N // 64) * (K * bs // 64)
     flops = units * 7 * 2 * 64 ** 3
-    return {"ms": round(ms, 4), "flops": flops, "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+    return {"ms": round(ms, 4), "selection": args.bwd_selection, "flops": flops, "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
             "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "calls": n,
             "timing": "median of per-call HIP event intervals after a settle of up to 0.5 s"}
 
@@ -519,6 +525,8 @@ def main():
     ap.add_argument("--interp", action="store_true")
     ap.add_argument("--interp-batch", type=int, default=24)
     ap.add_argument("--bwd", action="store_true", help="also time the selected-branch backward")
+    ap.add_argument("--bwd-selection", choices=("random", "local"), default="random",
+                    help="the backward's block selection: random top-K, or the K blocks around each query block")
     ap.add_argument("--no-unet", action="store_true", help="skip the 24-member U-Net step")
     ap.add_argument("--unet-only", action="store_true", help="time only the U-Net step (prints its JSON)")
     ap.add_argument("--unet-members", type=int, default=24)

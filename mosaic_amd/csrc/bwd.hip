@@ -378,7 +378,12 @@ void bwd_dkv_kernel(BwdParams p) {
     constexpr int kSlotElems = 2 * kTileElems + 256;
     __shared__ __attribute__((aligned(1024))) bf16_t ring0[kSlotElems], ring1[kSlotElems], ring2[kSlotElems];
     __shared__ uint64_t mark[kMaxBwdBlocks / 64];   // bit t: query block t selected this block
-    const int kt = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    // key tiles in XCD-contiguous ranges: with selections that follow spatial proximity,
+    // neighbouring key tiles are selected by the same query blocks and share their (q', do)
+    // tiles in one L2
+    const int ntiles = gridDim.x;
+    const int L = xcd_remap(blockIdx.x + ntiles * (blockIdx.y + gridDim.y * blockIdx.z), ntiles * gridDim.y * gridDim.z);
+    const int kt = L % ntiles, c = (L / ntiles) % (int)gridDim.y, b = L / (ntiles * (int)gridDim.y);
     const int key0 = kt * 64;
     const int64_t u = key0 / p.bs;
     const int lane = threadIdx.x & 63, r = lane & 31, hh = lane >> 5;
