@@ -12,13 +12,14 @@
 //            over the block's rows (the attention kernel's logit bound)
 // so q, k and v are written once and never read back by a pooling pass.
 //
-// Tiling: one workgroup = 256 tokens of one member x 256 output columns (four 64-column
-// groups: a q, k or v head, the gate logits, or zero padding), K = model dim in steps of 64.
-// Eight waves, two per SIMD; wave (wm, wn) computes rows 128 wm .. + 127 of group wn with
-// v_mfma_f32_32x32x16_bf16 (eight 32 x 32 accumulators), so each wave's epilogue handles one
-// head (or the gates) and whole pooled blocks.  x rows and W rows go from global memory straight into LDS
-// (direct-to-LDS loads, two stages), XOR-swizzled so the 16-byte operand reads are
-// conflict-free.  The accumulator layout gives a lane one output column and 16 rows: RoPE
+// Tiling: one workgroup = 256 tokens of one member x 128 output columns (two 64-column
+// groups: a q, k or v head, the gate logits, or zero padding), K = model dim in steps of 32.
+// Four waves, one per SIMD, and two workgroups per CU (72 KB of LDS each), so one
+// workgroup's epilogue overlaps the other's products; wave (wm, wn) computes rows
+// 128 wm .. + 127 of group wn with v_mfma_f32_32x32x16_bf16 (eight 32 x 32 accumulators), so
+// each wave's epilogue handles one head (or the gates) and whole pooled blocks.  x rows and W
+// rows go from global memory straight into LDS (direct-to-LDS loads, a three-slot ring),
+// XOR-swizzled so the 16-byte operand reads are conflict-free.  The accumulator layout gives a lane one output column and 16 rows: RoPE
 // pairs are neighbouring lanes (one DPP swap), pooling over a block's rows is an in-lane sum
 // plus one cross-half add.  The rounded results are staged in LDS (reusing the stages) and
 // leave as 16-byte rows.  Workgroups that share an x tile are dispatched to the same XCD.
@@ -28,9 +29,11 @@ namespace mosaic {
 namespace {
 
 constexpr int kProjM = 256;                 // tokens per workgroup
-constexpr int kProjN = 256;                 // output columns per workgroup
+constexpr int kProjN = 128;                 // output columns per workgroup
 constexpr int kProjK = 32;                  // reduction step
-constexpr int kSlot = kProjM * kProjK;      // bf16 elements of one operand's ring slot (16 KB)
+constexpr int kSlotA = kProjM * kProjK;     // bf16 elements of an x ring slot (16 KB)
+constexpr int kSlotB = kProjN * kProjK;     // bf16 elements of a weight ring slot (8 KB)
+constexpr int kRing = 3;                    // ring slots (k steps in flight)
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -97,45 +100,47 @@ __device__ __forceinline__ int stage_off(int row, int col) {
     return row * 64 + 8 * ((col >> 3) ^ (4 * ((row >> 2) & 1))) + (col & 7);
 }
 
-__global__ __attribute__((amdgpu_flat_work_group_size(512, 512), amdgpu_waves_per_eu(2, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2, 2)))
 void proj_kernel(ProjParams p) {
-    // a ring of four k-steps, each slot an array of its own per operand (so the compiler sees
-    // that reads of one slot and the loads in flight into the others touch different objects);
-    // after the loop each wave stages its 128 x 64 result in one of the eight arrays
-    __shared__ __attribute__((aligned(1024))) bf16_t A0[kSlot], A1[kSlot], A2[kSlot], A3[kSlot];
-    __shared__ __attribute__((aligned(1024))) bf16_t B0[kSlot], B1[kSlot], B2[kSlot], B3[kSlot];
+    // a ring of three k-steps (x rows in As, weight rows in Bs); after the loop each wave
+    // stages its 128 x 64 result (16 KB) in As[w] (waves 0-2) or Bs[0..1] (wave 3).  72 KB per
+    // workgroup: two workgroups share a CU, so one's epilogue overlaps the other's products.
+    __shared__ __attribute__((aligned(1024))) bf16_t As[kRing][kSlotA];
+    __shared__ __attribute__((aligned(1024))) bf16_t Bs[kRing][kSlotB];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = w >> 2, wn = w & 3;
+    const int wm = w >> 1, wn = w & 1;
     // logical tile: n fastest, then member, then token range, so the n tiles of one x tile
     // are neighbours and xcd_remap keeps them on one XCD (its L2 serves the x tile's re-reads)
     const int id = xcd_remap(blockIdx.x, gridDim.x);
-    const int ntile = id % p.n_tiles;
-    const int mtile = id / p.n_tiles;
+    const int n_tiles = p.n_tiles * (256 / kProjN);
+    const int ntile = id % n_tiles;
+    const int mtile = id / n_tiles;
     const int b = mtile % p.B, s0 = (mtile / p.B) * kProjM;
     const int n0 = ntile * kProjN;
 
-    // direct-to-LDS loads of a slot (rows of 32 k = 64 bytes): wave w fills rows 32 w .. + 31 of
-    // both operands, sixteen rows (1 KB) per instruction; lane l lands at row 16 i + l / 4,
-    // position l % 4, and fetches the row's chunk (l % 4) ^ ((row / 4) % 4).  A 16-byte LDS
-    // read serves 16 lanes per cycle from 64 banks (256 bytes): the 16 consecutive rows of one
-    // read then cover the four 64-byte quarters of the banks (row % 4) with four distinct
-    // chunk positions each ((row / 4) % 4), so no two lanes share a bank.
+    // direct-to-LDS loads of a slot (rows of 32 k = 64 bytes), sixteen rows (1 KB) per
+    // instruction: wave w fills x rows 64 w .. + 63 and weight rows 32 w .. + 31; lane l lands
+    // at row 16 i + l / 4, position l % 4, and fetches the row's chunk (l % 4) ^ ((row / 4) % 4).
+    // A 16-byte LDS read serves 16 lanes per cycle from 64 banks (256 bytes): the 16
+    // consecutive rows of one read then cover the four 64-byte quarters of the banks (row % 4)
+    // with four distinct chunk positions each ((row / 4) % 4), so no two lanes share a bank.
     const int r16 = lane >> 2, gch = (lane & 3) ^ ((lane >> 4) & 3);
     // uniform bases (scalar registers) plus one 32-bit byte offset per lane and operand
-    const char* xbase = reinterpret_cast<const char*>(p.x + (int64_t)(s0 + 32 * w) * p.x_sn + (int64_t)b * p.x_sb);
+    const char* xbase = reinterpret_cast<const char*>(p.x + (int64_t)(s0 + 64 * w) * p.x_sn + (int64_t)b * p.x_sb);
     const char* wbase = reinterpret_cast<const char*>(p.w + (int64_t)(n0 + 32 * w) * p.D);
     const uint32_t xoff = 2u * (uint32_t)(r16 * p.x_sn + 8 * gch);
     const uint32_t woff = 2u * (uint32_t)(r16 * p.D + 8 * gch);
     const int64_t xstep = 32 * p.x_sn, wstep = 32 * (int64_t)p.D;   // bytes per 16 rows
-    auto issue = [&](int k0, bf16_t* As, bf16_t* Bs) __attribute__((always_inline)) {
+    auto issue = [&](int k0, int slot) __attribute__((always_inline)) {
         const char* xk = xbase + 2 * k0;
         const char* wk = wbase + 2 * k0;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            __builtin_amdgcn_global_load_lds(xk + i * xstep + xoff, (lds_void*)(As + (32 * w + 16 * i) * kProjK), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(wk + i * wstep + woff, (lds_void*)(Bs + (32 * w + 16 * i) * kProjK), 16, 0, 0);
-        }
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(xk + i * xstep + xoff, (lds_void*)(As[slot] + (64 * w + 16 * i) * kProjK), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(wk + i * wstep + woff, (lds_void*)(Bs[slot] + (32 * w + 16 * i) * kProjK), 16, 0, 0);
     };
     // operand reads: row 32 t + lane % 32 of a 32-row block, chunk 2 kk + lane / 32 (kk = 0, 1)
     int rd[2];
@@ -151,12 +156,12 @@ void proj_kernel(ProjParams p) {
             for (int e = 0; e < 16; ++e) acc[mt][nt][e] = 0.f;
     // both k sub-steps' operands are requested at once; the first six reads are waited for
     // (lgkmcnt 6: LDS reads complete in order) while the second six are in flight
-    auto compute = [&](const bf16_t* As, const bf16_t* Bs) __attribute__((always_inline)) {
+    auto compute = [&](int slot) __attribute__((always_inline)) {
         bf16x8 a[2][4], bb[2][2];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            const uint32_t aa = lds_addr(As + 128 * wm * kProjK + rd[kk]);
-            const uint32_t ba = lds_addr(Bs + 64 * wn * kProjK + rd[kk]);
+            const uint32_t aa = lds_addr(As[slot] + 128 * wm * kProjK + rd[kk]);
+            const uint32_t ba = lds_addr(Bs[slot] + 64 * wn * kProjK + rd[kk]);
             constexpr int T = 32 * kProjK * 2;   // bytes between 32-row blocks
             a[kk][0] = lds_read16<0>(aa);
             a[kk][1] = lds_read16<T>(aa);
@@ -176,27 +181,24 @@ void proj_kernel(ProjParams p) {
 #pragma unroll
             for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(a[1][mt], bb[1][nt], acc[mt][nt]);
     };
-    // Step i uses slot i % 4; its loads were requested three steps earlier.  Wait for them,
-    // leaving the two newer steps' loads in flight (four per wave and step), then the barrier
-    // publishes every wave's loads and frees slot (i + 3) % 4, whose step is requested before
-    // step i is computed.  D is a multiple of 128, so the loop runs whole rings and has one exit.
+    // Step i uses slot i % 3; its loads (six per wave) were requested two steps earlier.  Wait
+    // for them, leaving the next step's six in flight, then the barrier publishes every wave's
+    // loads and frees slot (i + 2) % 3 (computed at step i - 1 by every wave), whose step is
+    // requested before step i is computed.
     const int steps = p.D / kProjK;
-    issue(0, A0, B0);
-    issue(kProjK, A1, B1);
-    issue(2 * kProjK, A2, B2);
-    auto ring_step = [&](int i, const bf16_t* As, const bf16_t* Bs, bf16_t* An, bf16_t* Bn) __attribute__((always_inline)) {
-        if (i + 2 < steps) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else if (i + 1 < steps) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    issue(0, 0);
+    issue(kProjK, 1);
+    auto ring_step = [&](int i, int slot, int next_slot) __attribute__((always_inline)) {
+        if (i + 1 < steps) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
         else wait_vmem();
         lds_barrier();
-        if (i + 3 < steps) issue(kProjK * (i + 3), An, Bn);
-        compute(As, Bs);
+        if (i + 2 < steps) issue(kProjK * (i + 2), next_slot);
+        compute(slot);
     };
-    for (int i = 0; i < steps; i += 4) {
-        ring_step(i, A0, B0, A3, B3);
-        ring_step(i + 1, A1, B1, A0, B0);
-        ring_step(i + 2, A2, B2, A1, B1);
-        ring_step(i + 3, A3, B3, A2, B2);
+    for (int i = 0; i < steps; i += 3) {
+        ring_step(i, 0, 2);
+        if (i + 1 < steps) ring_step(i + 1, 1, 0);
+        if (i + 2 < steps) ring_step(i + 2, 2, 1);
     }
     __syncthreads();  // every wave is done with the ring: its arrays become the output staging
 
@@ -209,7 +211,7 @@ void proj_kernel(ProjParams p) {
     int head;
     const int role = group_role(p, n0 / 64 + wn, head);
     // this wave's staging array (128 rows x 64 columns, 16 KB)
-    bf16_t* stg = w == 0 ? A0 : w == 1 ? A1 : w == 2 ? A2 : w == 3 ? A3 : w == 4 ? B0 : w == 5 ? B1 : w == 6 ? B2 : B3;
+    bf16_t* stg = w < 3 ? As[w] : Bs[0];
     if (role != kRolePad) {
         const bool rope = p.rope_cos != nullptr && (role == kRoleQ || role == kRoleK);
         const bool pool = p.bs > 0 && role != kRoleGate;
@@ -372,8 +374,8 @@ void proj_kernel(ProjParams p) {
 hipError_t launch_proj(const ProjParams& p, hipStream_t s) {
     ProjParams q = p;
     void* args[] = {&q};
-    const int grid = (p.S / kProjM) * p.B * p.n_tiles;
-    return hipLaunchKernel((const void*)proj_kernel, dim3(grid), dim3(512), args, 0, s);
+    const int grid = (p.S / kProjM) * p.B * p.n_tiles * (256 / kProjN);
+    return hipLaunchKernel((const void*)proj_kernel, dim3(grid), dim3(256), args, 0, s);
 }
 
 }  // namespace mosaic
