@@ -19,10 +19,10 @@
 // 128 wm .. + 127 of group wn with v_mfma_f32_32x32x16_bf16 (eight 32 x 32 accumulators), so
 // each wave's epilogue handles one head (or the gates) and whole pooled blocks.  x rows and W
 // rows go from global memory straight into LDS (direct-to-LDS loads, a three-slot ring),
-// XOR-swizzled so the 16-byte operand reads are conflict-free.  The accumulator layout gives a lane one output column and 16 rows: RoPE
-// pairs are neighbouring lanes (one DPP swap), pooling over a block's rows is an in-lane sum
-// plus one cross-half add.  The rounded results are staged in LDS (reusing the stages) and
-// leave as 16-byte rows.  Workgroups that share an x tile are dispatched to the same XCD.
+// XOR-swizzled so the 16-byte operand reads are conflict-free.  The rounded results are
+// staged in LDS (reusing the stages) and leave as 16-byte row chunks; RoPE and pooling run on
+// those chunks (a RoPE pair in one lane, the pooled sums of a chunk added across the lanes
+// that hold its rows).  Workgroups that share an x tile are dispatched to the same XCD.
 #include "bsa_common.h"
 
 namespace mosaic {
@@ -73,13 +73,15 @@ __device__ __forceinline__ float dpp(float x) {
 }
 // x of the other lane of the pair (l, l ^ 1): quad_perm [1, 0, 3, 2]
 __device__ __forceinline__ float swap_pair(float x) { return dpp<0xb1>(x); }
-// sum over the 8 lanes of an aligned group: xor 1 and xor 2 (quad permutes), then the other
-// quad of the eight (row_half_mirror: lane i <- lane 7 - i, which lies in the other quad)
-__device__ __forceinline__ float sum8(float x) {
-    x += dpp<0xb1>(x);
-    x += dpp<0x4e>(x);
-    x += dpp<0x141>(x);
-    return x;
+// x[l] + x[l ^ 16] and max(x[l], x[l ^ 16]) in every lane: one v_permlane16_swap (rows 1 and
+// 3 of one copy trade places with rows 0 and 2 of the other)
+__device__ __forceinline__ float swap16_add(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 enum GroupRole { kRoleQ = 0, kRoleK = 1, kRoleV = 2, kRoleGate = 3, kRolePad = 4 };
@@ -203,118 +205,123 @@ void proj_kernel(ProjParams p) {
     __syncthreads();  // every wave is done with the ring: its arrays become the output staging
 
     // ------------------------------------------------------------------ epilogue
-    // lane: column 32 nt + lane % 32 of the wave's group, rows 8 (e / 4) + 4 (lane / 32) + e % 4
-    // of each 32-row tile mt of its 128 rows
+    // Phase 1: each wave rounds its accumulators to bf16 and stages its 128 x 64 result.  The
+    // accumulator layout gives lane l column 32 nt + l % 32 of the wave's group and rows
+    // 8 (e / 4) + 4 (l / 32) + e % 4 of each 32-row tile mt of its 128 rows.
     const int hh = lane >> 5, odd = lane & 1;
-    const int bpw = p.bs == 64 ? 2 : 1;                 // pooled blocks per 128 rows (bs 64 or 128)
-    const int tpb = p.bs == 64 ? 2 : 4;                 // 32-row tiles per block
     int head;
     const int role = group_role(p, n0 / 64 + wn, head);
     // this wave's staging array (128 rows x 64 columns, 16 KB)
     bf16_t* stg = w < 3 ? As[w] : Bs[0];
     if (role != kRolePad) {
-        const bool rope = p.rope_cos != nullptr && (role == kRoleQ || role == kRoleK);
-        const bool pool = p.bs > 0 && role != kRoleGate;
-        float psum[2][2], sqm[2][2];                    // [32-column half][block of the wave]
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) { psum[j][k2] = 0.f; sqm[j][k2] = 0.f; }
-        // RoPE table values of a tile's 16 rows at this lane's pair; the next tile's are loaded
-        // before the current tile is processed, so their latency overlaps its arithmetic
-        float tc[2][16], ts[2][16];
-        auto load_tables = [&](int i, float (&c)[16], float (&sv)[16]) __attribute__((always_inline)) {
-            const int m = (32 * (i >> 2) + (lane & 31)) >> 1;
-            const int64_t r0 = s0 + 128 * wm + 32 * (i & 3) + 4 * hh;
-            const float* ct = p.rope_cos + r0 * 32 + m;
-            const float* st = p.rope_sin + r0 * 32 + m;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int dr = 8 * (e >> 2) + (e & 3);
-                c[e] = ct[dr * 32];
-                sv[e] = st[dr * 32];
-            }
-        };
-        // even lane (x0, partner x1): x0 c - x1 s = x0 c + x1 (-s); odd lane (x1, partner x0):
-        // x1 c + x0 s.  Negating s is exact, so one product-sum with the sign folded into s
-        // rounds exactly as the reference's two forms.
-        const float sgn = odd ? 1.f : -1.f;
-        if (rope) load_tables(0, tc[0], ts[0]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {                   // tile i: 32-column half j, 32-row tile mt
             const int j = i >> 2, mt = i & 3;
             const int col = 32 * j + (lane & 31);       // column within the group (head dim)
-            if (rope && i + 1 < 8) load_tables(i + 1, tc[(i + 1) & 1], ts[(i + 1) & 1]);
-            {
-                float x[16];
+            float x[16];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) x[e] = round_bf16(acc[mt][j][e]);
-                const int rbase = 128 * wm + 32 * mt + 4 * hh;   // tile row of register e: rbase + 8 (e/4) + e%4
-                if (rope) {
-                    const float* cs = tc[i & 1];
-                    const float* sn = ts[i & 1];
+            for (int e = 0; e < 16; ++e) x[e] = round_bf16(acc[mt][j][e]);
+            // stage rows r, r + 1 as bf16 pairs of columns (c, c + 1): even lanes write row r,
+            // odd lanes row r + 1, each after one swap with the pair's other lane
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const float other = swap_pair(x[e]);
-                        x[e] = round_bf16(rope_mul_add(x[e], cs[e], other, sgn * sn[e]));
-                    }
+            for (int e = 0; e < 16; e += 2) {
+                const float other = swap_pair(odd ? x[e] : x[e + 1]);
+                const uint32_t word = odd ? pack_bf16x2(other, x[e + 1]) : pack_bf16x2(x[e], other);
+                const int row = 32 * mt + 4 * hh + 8 * (e >> 2) + (e & 3) + odd;   // row of the wave's 128
+                *reinterpret_cast<uint32_t*>(stg + stage_off(row, col & ~1)) = word;
+            }
+        }
+    }
+
+    // Phase 2, from each wave's own staging (no workgroup barrier: a wave's LDS writes and
+    // reads are ordered).  q / k / v: lane l takes the 8 columns 8 (l % 8) .. + 7 of rows
+    // 8 it + l / 8 (it = 0 .. 15), so a RoPE pair lies in one lane and the table values of its
+    // four frequencies are one 16-byte load each of cos and sin; each rotated chunk leaves as
+    // a 16-byte row chunk to [B, S, H, 64], and the lane sums its rows of each pooled block,
+    // which three exchanges (lanes l ^ 8, l ^ 16, l ^ 32) then add up.  The gates: the softmax
+    // of each head's three logits to [B, S, Hq, 3].
+    if (role == kRoleQ || role == kRoleK || role == kRoleV) {
+        bf16_t* dst = role == kRoleQ ? p.q : (role == kRoleK ? p.k : p.v);
+        const int H = role == kRoleQ ? p.Hq : p.Hk;
+        bf16_t* rowp = dst + (((int64_t)b * p.S + s0 + 128 * wm) * H + head) * 64;
+        const bool rope = p.rope_cos != nullptr && role != kRoleV;
+        const bool pool = p.bs > 0;
+        const bool bound = role == kRoleK && p.kbnd != nullptr;
+        const int ch = lane & 7, r8 = lane >> 3;
+        const int bpw = p.bs == 64 ? 2 : 1;             // pooled blocks per 128 rows (bs 64 or 128)
+        float ps[2][8], sqm[2];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+            sqm[k2] = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ps[k2][e] = 0.f;
+        }
+        const float* ctab = rope ? p.rope_cos + (int64_t)(s0 + 128 * wm) * 32 + 4 * ch : nullptr;
+        const float* stab = rope ? p.rope_sin + (int64_t)(s0 + 128 * wm) * 32 + 4 * ch : nullptr;
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int row = 8 * it + r8;
+            uint4 u = *reinterpret_cast<const uint4*>(stg + stage_off(row, 8 * ch));
+            if (rope) {
+                // (x0, x1) -> (x0 c - x1 s, x1 c + x0 s), products and sum rounded separately
+                const float4 c = *reinterpret_cast<const float4*>(ctab + row * 32);
+                const float4 sn = *reinterpret_cast<const float4*>(stab + row * 32);
+                u.x = rope_pair(u.x, c.x, sn.x);
+                u.y = rope_pair(u.y, c.y, sn.y);
+                u.z = rope_pair(u.z, c.z, sn.z);
+                u.w = rope_pair(u.w, c.w, sn.w);
+            }
+            *reinterpret_cast<uint4*>(rowp + (int64_t)row * H * 64 + 8 * ch) = u;
+            if (pool) {
+                const int k2 = bpw == 2 ? it >> 3 : 0;   // rows 0-63 and 64-127 at bs 64
+                const float xs[8] = {bf_lo(u.x), bf_hi(u.x), bf_lo(u.y), bf_hi(u.y),
+                                     bf_lo(u.z), bf_hi(u.z), bf_lo(u.w), bf_hi(u.w)};
+                float sq = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    ps[k2][e] += xs[e];
+                    sq = fmaf(xs[e], xs[e], sq);
                 }
-                if (pool) {
-                    float sm = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) sm += x[e];
-                    const bool second = mt >= tpb;      // the wave's second block (bs 64)
-                    psum[j][0] += second ? 0.f : sm;
-                    psum[j][1] += second ? sm : 0.f;
-                    if (role == kRoleK && p.kbnd != nullptr) {
-                        float mx = 0.f;
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sum8(x[e] * x[e]));
-                        if (second) sqm[j][1] = fmaxf(sqm[j][1], mx);
-                        else sqm[j][0] = fmaxf(sqm[j][0], mx);
-                    }
-                }
-                // stage rows r, r + 1 as bf16 pairs of columns (c, c + 1): even lanes write row
-                // r, odd lanes row r + 1, each after one swap with the pair's other lane
-#pragma unroll
-                for (int e = 0; e < 16; e += 2) {
-                    const float other = swap_pair(odd ? x[e] : x[e + 1]);
-                    const uint32_t word = odd ? pack_bf16x2(other, x[e + 1]) : pack_bf16x2(x[e], other);
-                    const int row = rbase - 128 * wm + 8 * (e >> 2) + (e & 3) + odd;   // row of the wave's 128
-                    *reinterpret_cast<uint32_t*>(stg + stage_off(row, col & ~1)) = word;
-                }
+                sqm[k2] = fmaxf(sqm[k2], sq);
             }
         }
         if (pool) {
-            // pooled outputs: the lanes l and l + 32 hold the same column, different rows
+            // pooled outputs: every lane holds its chunk's block sums after the exchanges; lanes
+            // 0-7 (l / 8 = 0) write them
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = 32 * j + (lane & 31);
+            for (int k2 = 0; k2 < 2; ++k2) {
+                if (k2 >= bpw) break;
+                const int t = (s0 + 128 * wm) / p.bs + k2;    // block index
+                float mean[8];
 #pragma unroll
-                for (int k2 = 0; k2 < 2; ++k2) {
-                    if (k2 >= bpw) break;
-                    const float total = xor32_add(psum[j][k2]);
-                    const float mean = total / (float)p.bs;
-                    const int t = (s0 + 128 * wm) / p.bs + k2;    // block index
-                    if (lane < 32) {
-                        const bf16_t mv = (bf16_t)(pack_bf16x2(mean, 0.f) & 0xffffu);
-                        if (role == kRoleQ) {
-                            p.qc[(((int64_t)b * p.nb + t) * p.Hq + head) * 64 + col] = mv;
-                        } else if (role == kRoleK) {
-                            const int ch = col >> 3;
-                            p.kfrag[kfrag_index(b, head, p.Hk, p.nb_pad >> 5, t >> 5, ch >> 1, 32 * (ch & 1) + (t & 31)) +
-                                    (col & 7)] = mv;
-                        } else if (p.vfrag != nullptr) {
-                            const int wt = t & 31, s2 = wt >> 4, rem = wt & 15;
-                            const int slot = 4 * (rem >> 3) + (rem & 3), h2 = (rem & 7) >> 2;
+                for (int e = 0; e < 8; ++e) {
+                    float v = ps[k2][e];
+                    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));  // l ^ 8
+                    v = xor32_add(swap16_add(v));
+                    mean[e] = v / (float)p.bs;
+                }
+                float mx = sqm[k2];
+                mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(mx), 0x128, 0xf, 0xf, false)));
+                mx = xor32_max(swap16_max(mx));
+                if (r8 == 0) {
+                    uint4 m4;
+                    m4.x = pack_bf16x2(mean[0], mean[1]); m4.y = pack_bf16x2(mean[2], mean[3]);
+                    m4.z = pack_bf16x2(mean[4], mean[5]); m4.w = pack_bf16x2(mean[6], mean[7]);
+                    if (role == kRoleQ) {
+                        *reinterpret_cast<uint4*>(p.qc + (((int64_t)b * p.nb + t) * p.Hq + head) * 64 + 8 * ch) = m4;
+                    } else if (role == kRoleK) {
+                        *reinterpret_cast<uint4*>(p.kfrag + kfrag_index(b, head, p.Hk, p.nb_pad >> 5, t >> 5, ch >> 1,
+                                                                         32 * (ch & 1) + (t & 31))) = m4;
+                        if (bound) p.kbnd[(((int64_t)b * p.nb + t) * p.Hk + head) * 8 + ch] = mx;
+                    } else if (p.vfrag != nullptr) {
+                        const int wt = t & 31, s2 = wt >> 4, rem = wt & 15;
+                        const int slot = 4 * (rem >> 3) + (rem & 3), h2 = (rem & 7) >> 2;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int col = 8 * ch + e;
                             p.vfrag[vfrag_index(b, head, p.Hk, p.nb_pad >> 5, t >> 5, col >> 5, s2, 32 * h2 + (col & 31)) +
-                                    slot] = mv;
+                                    slot] = (bf16_t)(pack_bf16x2(mean[e], 0.f) & 0xffffu);
                         }
-                    }
-                    if (role == kRoleK && p.kbnd != nullptr) {
-                        const float mx = xor32_max(sqm[j][k2]);
-                        if (lane < 32 && (lane & 7) == 0)
-                            p.kbnd[(((int64_t)b * p.nb + t) * p.Hk + head) * 8 + (col >> 3)] = mx;
                     }
                 }
             }
@@ -325,8 +332,8 @@ void proj_kernel(ProjParams p) {
                 for (int i = lane; i < (p.nb_pad - p.nb) * 64; i += 64) {
                     const int t = p.nb + (i >> 6), col = i & 63;
                     if (role == kRoleK) {
-                        const int ch = col >> 3;
-                        p.kfrag[kfrag_index(b, head, p.Hk, UT, t >> 5, ch >> 1, 32 * (ch & 1) + (t & 31)) + (col & 7)] = 0;
+                        const int c8 = col >> 3;
+                        p.kfrag[kfrag_index(b, head, p.Hk, UT, t >> 5, c8 >> 1, 32 * (c8 & 1) + (t & 31)) + (col & 7)] = 0;
                     } else {
                         const int wt = t & 31, s2 = wt >> 4, rem = wt & 15;
                         const int slot = 4 * (rem >> 3) + (rem & 3), h2 = (rem & 7) >> 2;
@@ -334,22 +341,6 @@ void proj_kernel(ProjParams p) {
                     }
                 }
             }
-        }
-    }
-
-    // ------------------------------------------------------------------ write-out
-    // each wave from its own staging (no workgroup barrier: a wave's LDS writes and reads are
-    // ordered): q / k / v as 16-byte row chunks to [B, S, H, 64]; the gates as the softmax of
-    // each head's three logits to [B, S, Hq, 3]
-    if (role == kRoleQ || role == kRoleK || role == kRoleV) {
-        bf16_t* dst = role == kRoleQ ? p.q : (role == kRoleK ? p.k : p.v);
-        const int H = role == kRoleQ ? p.Hq : p.Hk;
-        bf16_t* rowp = dst + (((int64_t)b * p.S + s0 + 128 * wm) * H + head) * 64;
-#pragma unroll
-        for (int it = 0; it < 16; ++it) {
-            const int idx = 64 * it + lane, row = idx >> 3, ch = idx & 7;
-            const uint4 u = *reinterpret_cast<const uint4*>(stg + stage_off(row, 8 * ch));
-            *reinterpret_cast<uint4*>(rowp + (int64_t)row * H * 64 + 8 * ch) = u;
         }
     } else if (role == kRoleGate) {
         for (int idx = lane; idx < 128 * p.Hq; idx += 64) {

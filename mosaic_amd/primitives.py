@@ -490,9 +490,9 @@ class MosaicAttention(nn.Module):
 
     # class-wide switch of the fused input side (mosaic_attn_proj).  Off by default: on the
     # shipped stage-1 shape (1.18 M rows, 768 -> 1280, 24 members) a whole attention block
-    # measures 18.00 ms with the library GEMM and the RoPE pooling pass against 18.16 ms with the
-    # fused kernel (3.11 ms), whose GEMM core alone is slower than the library's; set True (or
-    # per instance) to take it.
+    # measures 18.0 ms with the library GEMM and the RoPE pooling pass against 18.2 ms with the
+    # fused kernel (3.09 ms: its GEMM core is slower than the library's, and every workgroup
+    # re-reads its tokens' RoPE tables); set True (or per instance) to take it.
     fused_input_side = False
 
     def _fused_input_side(self, x):
