@@ -38,7 +38,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     f32x2 v = {a, b};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
-__device__ __forceinline__ float round_bf16(float a) { return bf_lo(pack_bf16x2(a, 0.f)); }
+// a rounded to bf16 (round to nearest even), as an fp32 value: the conversion puts bf16(a) in
+// the high half of a word whose low half is bf16(0) = 0, which is that fp32 value (one
+// instruction, no shift)
+__device__ __forceinline__ float round_bf16(float a) { return __uint_as_float(pack_bf16x2(0.f, a)); }
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
