@@ -94,3 +94,69 @@ def test_oracle_linear_rounds_once():
     assert ((got.double() - exact).abs() <= exact.abs() * 2 ** -8 + 1e-4).all()
     assert math.isclose(unet_oracle.rms_norm(torch.full((1, 4), 3.0), {torch.float32: torch.float32})[0, 0].item(),
                         1.0, rel_tol=1e-6)
+
+
+def _tiny_unet_cpu(seed=0):
+    """The tiny three-resolution U-Net of the GPU model tests (nside 16 / 8 / 4, head_dim 64),
+    random init with the residual outputs at full scale, on the CPU, as a state dict."""
+    from mosaic_amd.model import BottleneckConfig, ModelConfig, StageConfig
+    stages = [StageConfig(nside=16, dim=256, num_heads=4, block_attn_size=256, sparse_block_size=64,
+                          sparse_block_count=6, encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4),
+              StageConfig(nside=8, dim=512, num_heads=8, block_attn_size=256, sparse_block_size=64,
+                          sparse_block_count=4, encoder_depth=1, decoder_depth=1, mlp_ratio=2.0, gqa_ratio=4)]
+    bottleneck = BottleneckConfig(nside=4, dim=512, num_heads=8, block_attn_size=192, sparse_block_size=64,
+                                  sparse_block_count=2, depth=1, mlp_ratio=2.0, gqa_ratio=4)
+    cfg = ModelConfig(dim=256, num_heads=4, k_neighbors=8, qk_norm=False, rope=True, rope_theta=10000,
+                      sparse_every=1, variables=[f"v{i}" for i in range(5)], static_variables=["a", "b", "c"],
+                      qkv_compress_ratio=1, cg_stage_cfgs=stages, bottleneck_cfg=bottleneck,
+                      num_history_steps=2, noise_dim=32, rmsnorm_elementwise_affine=False)
+    torch.manual_seed(seed)
+    model = Transformer(cfg, seed=11)
+    g = torch.Generator().manual_seed(seed + 1)
+    for name, p in model.named_parameters():
+        if name.endswith(("to_o.weight", "w2.weight", "proj_x.weight", "proj_pos.weight")) and "interp" not in name:
+            p.data = torch.randn(p.shape, generator=g) / math.sqrt(p.shape[1])
+    lon, lat = torch.linspace(0, 345, 24), torch.linspace(-90, 90, 13)
+    model.initialize_interpolation(lon, lat)
+    model.initialize_static_vars(torch.randn(24, 13, 3, generator=g), lon, lat)
+    probe = {dt: torch.nn.functional.rms_norm(torch.zeros(1, 8, dtype=dt), (8,)).dtype
+             for dt in (torch.bfloat16, torch.float32)}
+    return cfg, model.state_dict(), probe
+
+
+def test_unet_oracle_members_are_independent_and_ordered():
+    """The oracle's composition of the whole forward keeps ensemble members apart (mosaic.py:
+    301-309: each member is the same input with its own noise row): two members at once give
+    each member's one-member forecast, and swapping the noise rows swaps the members.  A
+    rearrange that mixed the member and pixel axes anywhere in the chain (the einops patterns
+    of the stages, the attention, the interpolation) would fail; so does a planted one."""
+    cfg, P, probe = _tiny_unet_cpu()
+    # the noise projection at a scale where the members' forecasts differ clearly (it is
+    # initialised at std 0.01)
+    P = dict(P)
+    P["noise_generator.to_noise.weight"] = P["noise_generator.to_noise.weight"] * 100
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 1, 2, 24, 13, 5, generator=g)
+    dyt = torch.rand(1, 1, 2, generator=g)
+    noise = torch.randn(2, cfg.noise_dim, generator=g)
+    both = unet_oracle.forward(P, cfg, x, dyt, 2, noise, probe).float()
+    one = [unet_oracle.forward(P, cfg, x, dyt, 1, noise[i:i + 1], probe).float() for i in range(2)]
+    swapped = unet_oracle.forward(P, cfg, x, dyt, 2, noise.flip(0), probe).float()
+    assert both.shape == (1, 2, 24, 13, 5)
+    # the members differ by ~45% (relative L2); one member alone or in the pair agrees to ~1%
+    # (the CPU products sum in another order for another batch size, and bf16 roundings
+    # propagate through the layers)
+    assert ((both[:, 0] - both[:, 1]).norm() / both[:, 0].norm()).item() > 0.2
+    for i in range(2):
+        rel = ((both[:, i] - one[i][:, 0]).norm() / one[i].norm()).item()
+        assert rel <= 3e-2, (i, rel)
+    assert ((swapped.flip(1) - both).norm() / both.norm()).item() <= 3e-2
+
+    # planted: the attention output of every layer rolled by one member
+    real = unet_oracle.mosaic_attention
+    try:
+        unet_oracle.mosaic_attention = lambda *a, **k: real(*a, **k).roll(1, dims=1)
+        mixed = unet_oracle.forward(P, cfg, x, dyt, 2, noise, probe).float()
+    finally:
+        unet_oracle.mosaic_attention = real
+    assert ((mixed[:, 0] - one[0][:, 0]).norm() / one[0].norm()).item() > 6e-2   # ~12%
