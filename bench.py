@@ -27,7 +27,7 @@ attention over the whole sequence, mosaic_dense_attn_fwd, on the same q/k/v), --
 times the op with the input side's RoPE fused into its pooling pass, mosaic_bsa_fwd_rope,
 against eager torch RoPE followed by the op, both on unrotated q/k), --interp (also times the
 k-nearest-neighbour cross-attention between the model's lat-lon and HEALPix grids,
-mosaic_knn_interp_fwd_ordered, at --interp-batch members), --branches (also times the local and the
+mosaic_knn_interp_fwd_ex, at --interp-batch members), --branches (also times the local and the
 selected branch as standalone kernels).  Unless --no-unet, the line also carries
 one forecast step of the full U-Net at --unet-members ensemble members (default 24:
 ``unet_24_member_step_ms``, the metric's second half); --unet-only times only that step.
@@ -255,10 +255,12 @@ def rope_fused(L, a, ws_ptr, nbytes, v, out, wl, args, stream):
 
 def interp_leg(L, args, dev, stream):
     """k-nearest-neighbour cross-attention between the model's grids
-    (mosaic_knn_interp_fwd_ordered, targets in the model's spatial order): 121 x 240 lat-lon
+    (mosaic_knn_interp_fwd_ex, targets in the model's spatial order): 121 x 240 lat-lon
     (29040 points) <-> HEALPix nside 64 (49152), 24 neighbours, 12 heads of 64,
-    ``--interp-batch`` members, both directions.  Algorithmic bytes per launch: every k / v
-    row read once, the output written once, the neighbour lists and relative positions read."""
+    ``--interp-batch`` members, both directions; ``ms`` is the model's form (exact products
+    summed in fp32), ``ms_rounded_products`` the eager form (every product rounded to bf16).
+    Algorithmic bytes per launch: every k / v row read once, the output written once, the
+    neighbour lists and relative positions read."""
     import numpy as np
     from mosaic_amd.healpix import get_healpix_grid
     from mosaic_amd.interp import get_neighbors, rad_to_xyz, spatial_order
@@ -284,26 +286,31 @@ def interp_leg(L, args, dev, stream):
         kb, vb = _lib.Bnhd(k.data_ptr(), k.stride(1), k.stride(0), k.stride(2)), \
             _lib.Bnhd(v.data_ptr(), v.stride(1), v.stride(0), v.stride(2))
 
-        def call():
-            st = L.mosaic_knn_interp_fwd_ordered(kb, vb, nb_d.data_ptr(), rel_d.data_ptr(), w_q.data_ptr(),
-                                                 order.data_ptr(), len(src), len(dst), B, H, 64, K, 0.125,
-                                                 out.data_ptr(), sp)
+        def call(flags=0):
+            st = L.mosaic_knn_interp_fwd_ex(kb, vb, nb_d.data_ptr(), rel_d.data_ptr(), w_q.data_ptr(),
+                                            order.data_ptr(), len(src), len(dst), B, H, 64, K, 0.125, flags,
+                                            out.data_ptr(), sp)
             if st:
                 raise RuntimeError(_lib.strerror(st))
-        for _ in range(3):
-            call()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(args.steps):
-            call()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / args.steps
+
+        def timed(flags):
+            for _ in range(3):
+                call(flags)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(args.steps):
+                call(flags)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / args.steps
+        ms_rounded = timed(_lib.KNN_ROUND_PRODUCTS)
+        ms = timed(0)
         nbytes = len(src) * B * H * 64 * 2 * 2 + len(dst) * B * H * 64 * 2 + len(dst) * K * (4 + 12)
         gbs = nbytes / (ms * 1e-3) / 1e9
         leg = {"num_from": len(src), "num_to": len(dst), "ms": round(ms, 4), "bytes": nbytes,
-               "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+               "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+               "ms_rounded_products": round(ms_rounded, 4)}
         if B <= 4:   # the reference's formulation in eager torch (materialised q and gathers)
             def eager():
                 q = (rel_d.to(torch.bfloat16) @ w_q.t()).view(len(dst), K, 1, H, 64)

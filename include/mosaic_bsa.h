@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOSAIC_BSA_ABI_VERSION 9
+#define MOSAIC_BSA_ABI_VERSION 10
 
 #if defined(__GNUC__) || defined(__clang__)
 #define MOSAIC_API __attribute__((visibility("default")))
@@ -230,6 +230,24 @@ MOSAIC_API int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const
                                              int32_t num_to, int32_t batch, int32_t num_heads,
                                              int32_t head_dim, int32_t num_neighbors, float scale,
                                              void* out, void* stream);
+
+/* Flags of mosaic_knn_interp_fwd_ex. */
+#define MOSAIC_KNN_ROUND_PRODUCTS 1u /* round every q*k and w*v product to bf16 before summing */
+
+/* mosaic_knn_interp_fwd_ordered with a choice of product rounding (same replacement,
+   primitives.py:265-283).  With MOSAIC_KNN_ROUND_PRODUCTS every product of (q * k).sum(-1)
+   and (w * v).sum(1) is rounded to bf16 before the fp32 sum, as the reference's eager bf16
+   elementwise ops do (mosaic_knn_interp_fwd and _ordered are this form).  Without it the
+   products are exact and summed in fp32, as the reference's default inference path computes
+   them (its torch.compile'd model, inference.py:470-473, fuses each product into its
+   reduction); the roundings of the score, the scaled score, the weights and the output are
+   the same in both.  Unknown flag bits return MOSAIC_ERR_MODE. */
+MOSAIC_API int mosaic_knn_interp_fwd_ex(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors,
+                                        const float* rel_pos, const void* w_q,
+                                        const int32_t* target_order, int32_t num_from, int32_t num_to,
+                                        int32_t batch, int32_t num_heads, int32_t head_dim,
+                                        int32_t num_neighbors, float scale, uint32_t flags, void* out,
+                                        void* stream);
 
 /*
  * Selected-branch attention given block indices.  Replaces mosaic_sparse_attn /

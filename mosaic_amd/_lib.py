@@ -12,7 +12,7 @@ import threading
 
 LIB_NAME = "libmosaic_bsa.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # mosaic_bsa_mode
 MODE_FULL = 0
@@ -27,7 +27,11 @@ STAGE_TOPK = 2
 STAGE_ATTN = 3
 
 # mosaic_status values the Python side names
+ERR_MODE = 10
 ERR_SCRATCH_LIMIT = 12
+
+# mosaic_knn_interp_fwd_ex flags
+KNN_ROUND_PRODUCTS = 1
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
 # mosaic_dtype
@@ -44,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "mosaic_bsa_fwd_proj",
     "mosaic_knn_interp_fwd",
     "mosaic_knn_interp_fwd_ordered",
+    "mosaic_knn_interp_fwd_ex",
     "mosaic_sparse_attn_bwd_workspace_size",
     "mosaic_sparse_attn_bwd",
     "mosaic_rms_norm_fwd",
@@ -127,6 +132,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_knn_interp_fwd_ordered.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32,
                                                   c_i32, c_i32, c_f, c_vp, c_vp]
     lib.mosaic_knn_interp_fwd_ordered.restype = c_int
+    lib.mosaic_knn_interp_fwd_ex.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32,
+                                             c_i32, c_i32, c_f, ctypes.c_uint32, c_vp, c_vp]
+    lib.mosaic_knn_interp_fwd_ex.restype = c_int
     c_i64 = ctypes.c_int64
     lib.mosaic_rms_norm_fwd.argtypes = [c_vp, c_vp, c_i32, c_i64, c_i32, c_i64, c_i64, c_vp, c_f, c_vp, c_vp,
                                         c_i32, c_vp]

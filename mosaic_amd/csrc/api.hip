@@ -523,6 +523,15 @@ int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const int32_t* n
                                   const void* w_q, const int32_t* target_order, int32_t num_from, int32_t num_to,
                                   int32_t batch, int32_t num_heads, int32_t head_dim, int32_t num_neighbors,
                                   float scale, void* out, void* stream) {
+    return mosaic_knn_interp_fwd_ex(k, v, neighbors, rel_pos, w_q, target_order, num_from, num_to, batch, num_heads,
+                                    head_dim, num_neighbors, scale, MOSAIC_KNN_ROUND_PRODUCTS, out, stream);
+}
+
+int mosaic_knn_interp_fwd_ex(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors, const float* rel_pos,
+                             const void* w_q, const int32_t* target_order, int32_t num_from, int32_t num_to,
+                             int32_t batch, int32_t num_heads, int32_t head_dim, int32_t num_neighbors, float scale,
+                             uint32_t flags, void* out, void* stream) {
+    if (flags & ~MOSAIC_KNN_ROUND_PRODUCTS) return MOSAIC_ERR_MODE;
     if (num_from <= 0 || num_to <= 0 || batch <= 0 || num_heads <= 0) return MOSAIC_ERR_SHAPE;
     if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
     if (num_neighbors <= 0 || num_neighbors > 32) return MOSAIC_ERR_BLOCK_COUNT;
@@ -545,6 +554,7 @@ int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const int32_t* n
     int exp2 = 0;
     p.scale_pow2 = std::isfinite(p.scale) && p.scale >= 0x1p-126f && std::frexp(p.scale, &exp2) == 0.5f;
     p.scale_log2e = p.scale * kLog2e;
+    p.round_products = (flags & MOSAIC_KNN_ROUND_PRODUCTS) != 0;
     return launch_status(launch_knn_attn(p, static_cast<hipStream_t>(stream)));
 }
 

@@ -338,6 +338,7 @@ struct InterpParams {
     float scale;
     float scale_log2e;                           // scale * log2 e
     int scale_pow2;                              // scale is a power of two
+    int round_products;                          // products rounded to bf16 (eager) or fp32
 };
 hipError_t launch_knn_attn(const InterpParams& p, hipStream_t s);
 

@@ -228,6 +228,29 @@ __device__ __forceinline__ void out_single(uint32_t w_lo, uint32_t w_hi, const u
 #undef MOSAIC_OUT_SINGLE_OPERANDS
 }
 
+// fp32 products (the reference under torch.compile: its fused reductions of (q * k).sum and
+// (w * v).sum multiply and add in fp32 and round only the sums).  A neighbour's score partial
+// over this lane's 8 dimensions: four dot products of packed (q, q) pairs against k's pairs,
+// chained through the accumulator, in dimension order from 0.
+__device__ __forceinline__ bf16x2_t as_bf2(uint32_t w) { return __builtin_bit_cast(bf16x2_t, w); }
+__device__ __forceinline__ float score_dot(const uint32_t (&q)[4], const uint4& k) {
+    float a = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q[0]), as_bf2(k.x), 0.f, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q[1]), as_bf2(k.y), a, false);
+    a = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q[2]), as_bf2(k.z), a, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(as_bf2(q[3]), as_bf2(k.w), a, false);
+}
+// One neighbour (weight w as (w, 0) and (0, w)) against the lane's eight output dimensions in
+// fp32: acc[d] (+)= w v[d], one dot product per product.
+template <bool FIRST>
+__device__ __forceinline__ void out_fp32(uint32_t w_lo, uint32_t w_hi, const uint4& v, float* acc) {
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        acc[2 * e] = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w_lo), as_bf2(vv[e]), FIRST ? 0.f : acc[2 * e], false);
+        acc[2 * e + 1] = __builtin_amdgcn_fdot2_f32_bf16(as_bf2(w_hi), as_bf2(vv[e]), FIRST ? 0.f : acc[2 * e + 1], false);
+    }
+}
+
 __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
     const uint32_t a[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -252,7 +275,8 @@ __device__ __forceinline__ uint4 ld_member(const bf16_t* base, Off off) {
 // with 32-bit offsets (the model's K = 24), what fits without spilling elsewhere.
 constexpr int knn_waves(int nslot, bool off32) { return nslot <= 1 ? 8 : nslot == 2 ? 7 : nslot == 3 ? (off32 ? 6 : 5) : 4; }
 
-template <int NSLOT, bool OFF32, bool POW2>
+// RP: products rounded to bf16 (the reference's eager elementwise ops); else fp32 products
+template <int NSLOT, bool OFF32, bool POW2, bool RP>
 __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_eu(knn_waves(NSLOT, OFF32)))) void knn_attn_kernel(InterpParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -281,7 +305,9 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
     // byte offsets of this lane's k / v chunks within a member (32 bits when they fit)
     using Off = typename std::conditional<OFF32, uint32_t, int64_t>::type;
     Off koff[NSLOT], voff[NSLOT];
-    uint32_t qp[NSLOT][8];  // q[j][d] as a bf16 in the half of a word that k's dim d occupies
+    // RP: q[j][d] as a bf16 in the half of a word that k's dim d occupies; else the packed
+    // pairs (q[j][2m], q[j][2m + 1])
+    uint32_t qp[NSLOT][RP ? 8 : 4];
 #pragma unroll
     for (int i = 0; i < NSLOT; ++i) {
         const int64_t sj = (int64_t)s * K + min(jg + 8 * i, K - 1);
@@ -294,7 +320,9 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const uint32_t bits = __float_as_uint(round_bf16(fmaf(r2, wq[3 * e + 2], fmaf(r1, wq[3 * e + 1], r0 * wq[3 * e]))));
-            qp[i][e] = (e & 1) ? bits : bits >> 16;
+            if constexpr (RP) qp[i][e] = (e & 1) ? bits : bits >> 16;
+            else if (e & 1) qp[i][e >> 1] |= bits;
+            else qp[i][e >> 1] = bits >> 16;
         }
     }
     // the output dimension this lane ends up holding after the reduce-scatter
@@ -309,11 +337,17 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
     const uint32_t ones = 0x3f803f80u, pick_lo = 0x3f80u, pick_hi = 0x3f800000u;  // bf16 pairs (1, 1), (1, 0), (0, 1)
     for (int b = 0; b < p.B; ++b) {
         const bool more = b + 1 < p.B;
+        // the fp32-product form loads the next member unconditionally (the last member again
+        // after the last): a conditional load made the compiler copy every k / v register at
+        // the loop's end
+        const int64_t bn = more ? b + 1 : b;
         // scores of this lane's slots (every lane of a neighbour group holds its score)
         float sc[NSLOT], m;
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
-            const float part = chunk_sum(score_partial(qp[i], kw[i], ones));
+            float part;
+            if constexpr (RP) part = chunk_sum(score_partial(qp[i], kw[i], ones));
+            else part = chunk_sum(score_dot(qp[i], kw[i]));
             // the score in base-2 units, sc = bf16(bf16(part) * scale) * log2 e.  A power-of-two
             // scale leaves bf16(part) * scale a bf16 value (a product too small to be normal is
             // below 2^-126 in magnitude, and so is the difference its rounding would make), so
@@ -323,9 +357,9 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
             sc[i] = i < NSLOT - 1 || jg + 8 * i < K ? t : -INFINITY;
             m = i == 0 ? sc[0] : fmaxf(m, sc[i]);
         }
-        if (more) {
+        if (!RP || more) {
 #pragma unroll
-            for (int i = 0; i < NSLOT; ++i) kw[i] = ld_member<OFF32>(p.k + (int64_t)(b + 1) * p.k_sb, koff[i]);
+            for (int i = 0; i < NSLOT; ++i) kw[i] = ld_member<OFF32>(p.k + bn * p.k_sb, koff[i]);
         }
         m = group_max(m);
         float ex[NSLOT], l = 0.f;
@@ -340,6 +374,16 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
         // row (a duplicate of a present one) then adds bf16(0 * v) = 0.  The weights are bf16, so
         // each product is one dot product of (w, 0) or (0, w) with a packed pair of v.
         float acc[8];
+        if constexpr (!RP) {
+            // fp32 products: one dot product each, accumulated slot by slot
+#pragma unroll
+            for (int i = 0; i < NSLOT; ++i) {
+                const float x = ex[i] * inv;
+                const uint32_t w_lo = pack_bf16x2(x, 0.f), w_hi = pack_bf16x2(0.f, x);
+                if (i == 0) out_fp32<true>(w_lo, w_hi, vw[i], acc);
+                else out_fp32<false>(w_lo, w_hi, vw[i], acc);
+            }
+        } else {
 #pragma unroll
         for (int i = 0; i < NSLOT; i += 2) {
             // the weight as (w, 0) and (0, w): one conversion each
@@ -362,9 +406,10 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
                 out_single<false>(wa_lo, wa_hi, vw[i], pick_lo, pick_hi, acc);
             }
         }
-        if (more) {
+        }
+        if (!RP || more) {
 #pragma unroll
-            for (int i = 0; i < NSLOT; ++i) vw[i] = ld_member<OFF32>(p.v + (int64_t)(b + 1) * p.v_sb, voff[i]);
+            for (int i = 0; i < NSLOT; ++i) vw[i] = ld_member<OFF32>(p.v + bn * p.v_sb, voff[i]);
         }
         // reduce-scatter over the 8 neighbour groups: halves (dims e / e + 4), row pairs
         // (e / e + 2), then lanes l ^ 8 (e / e + 1)
@@ -380,6 +425,12 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
     }
 }
 
+template <int NSLOT, bool RP>
+const void* pick(bool off32, bool pow2) {
+    return off32 ? (pow2 ? (const void*)&knn_attn_kernel<NSLOT, true, true, RP> : (const void*)&knn_attn_kernel<NSLOT, true, false, RP>)
+                 : (pow2 ? (const void*)&knn_attn_kernel<NSLOT, false, true, RP> : (const void*)&knn_attn_kernel<NSLOT, false, false, RP>);
+}
+
 template <int NSLOT>
 hipError_t launch_slots(const InterpParams& p, unsigned wgs, hipStream_t s) {
     void* args[] = {const_cast<InterpParams*>(&p)};
@@ -388,8 +439,7 @@ hipError_t launch_slots(const InterpParams& p, unsigned wgs, hipStream_t s) {
     const int64_t vmax = (int64_t)(p.S_from - 1) * p.v_sn + (int64_t)(p.H - 1) * p.v_sh + 64;
     const bool off32 = p.k_sn >= 0 && p.k_sh >= 0 && p.v_sn >= 0 && p.v_sh >= 0 &&
                        2 * kmax <= 0xffffffffLL && 2 * vmax <= 0xffffffffLL;
-    const void* fn = off32 ? (p.scale_pow2 ? (const void*)&knn_attn_kernel<NSLOT, true, true> : (const void*)&knn_attn_kernel<NSLOT, true, false>)
-                           : (p.scale_pow2 ? (const void*)&knn_attn_kernel<NSLOT, false, true> : (const void*)&knn_attn_kernel<NSLOT, false, false>);
+    const void* fn = p.round_products ? pick<NSLOT, true>(off32, p.scale_pow2) : pick<NSLOT, false>(off32, p.scale_pow2);
     return hipLaunchKernel(fn, dim3(wgs), dim3(kInterpWaves * 64), args, 0, s);
 }
 

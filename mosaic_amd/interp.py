@@ -2,10 +2,14 @@
 
 Mirrors ``CrossAttentionInterpolate`` (primitives.py:230-283) and its helpers
 ``rad_to_xyz`` / ``get_neighbors`` (utils.py:7-17, 33-41).  The gather-attention in the
-middle of the forward runs in libmosaic_bsa.so (``mosaic_knn_interp_fwd_ordered``): the queries
+middle of the forward runs in libmosaic_bsa.so (``mosaic_knn_interp_fwd_ex``): the queries
 ``to_q(rel_pos)`` and the gathered keys / values are never materialised.  The RMSNorm and the
 ``to_kv`` / ``to_o`` projections stay torch modules (library GEMMs).  Precision is that of the
-model under bf16 autocast: bf16 projections, fp32 softmax, bf16 output.
+model under bf16 autocast: bf16 projections, fp32 softmax, bf16 output.  The products of
+``(q * k).sum(-1)`` and ``(w * v).sum(1)`` are exact and summed in fp32, as the reference's
+default inference path computes them (``torch.compile`` fuses each product into its reduction,
+inference.py:470-473); ``round_products=True`` rounds each to bf16 first, as its eager
+elementwise ops do.
 """
 
 from __future__ import annotations
@@ -58,7 +62,7 @@ def _snhd(t: torch.Tensor) -> _lib.Bnhd:
 
 def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel_pos: torch.Tensor,
                   w_q: torch.Tensor, scale: float | None = None,
-                  target_order: torch.Tensor | None = None) -> torch.Tensor:
+                  target_order: torch.Tensor | None = None, round_products: bool = False) -> torch.Tensor:
     """The gather-attention of CrossAttentionInterpolate.forward (primitives.py:265-283).
 
     k, v: [S_from, B, H, 64] (views of the kv projection are fine); neighbors: [S_to, K]
@@ -66,7 +70,9 @@ def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel
     [S_to, B, H, 64] bf16: for each target, softmax over its K neighbours of
     ``to_q(rel_pos) . k * scale``, applied to v.  ``target_order`` ([S_to], a permutation,
     e.g. ``spatial_order`` of the target positions) changes only the order the targets are
-    computed in, not the result.
+    computed in, not the result.  ``round_products`` rounds every product of the two weighted
+    sums to bf16 before it is added (the reference's eager elementwise ops); by default the
+    products are exact and summed in fp32 (its compiled path).
     """
     forward_only("knn_attention", k, v, rel_pos, w_q)
     if k.dim() != 4 or k.shape != v.shape or k.shape[-1] != 64:
@@ -96,11 +102,12 @@ def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel
             raise ValueError(f"target_order must be [S_to] = [{S_to}], got {tuple(target_order.shape)}")
         order = target_order.to(device=k.device, dtype=torch.int32).contiguous()
     out = torch.empty(S_to, B, H, d, dtype=torch.bfloat16, device=k.device)
-    st = _lib.lib().mosaic_knn_interp_fwd_ordered(_snhd(k), _snhd(v), nb.data_ptr(), rp.data_ptr(), wq.data_ptr(),
-                                                  None if order is None else order.data_ptr(),
-                                                  S_from, S_to, B, H, d, K, 0.0 if scale is None else float(scale),
-                                                  out.data_ptr(), stream_of(k))
-    _lib.check(st, "mosaic_knn_interp_fwd_ordered")
+    flags = _lib.KNN_ROUND_PRODUCTS if round_products else 0
+    st = _lib.lib().mosaic_knn_interp_fwd_ex(_snhd(k), _snhd(v), nb.data_ptr(), rp.data_ptr(), wq.data_ptr(),
+                                             None if order is None else order.data_ptr(),
+                                             S_from, S_to, B, H, d, K, 0.0 if scale is None else float(scale),
+                                             flags, out.data_ptr(), stream_of(k))
+    _lib.check(st, "mosaic_knn_interp_fwd_ex")
     return out
 
 
@@ -112,6 +119,9 @@ class CrossAttentionInterpolate(nn.Module):
     """
 
     space_dim = 3
+    # products of the two weighted sums rounded to bf16 (the reference's eager ops) or exact
+    # and summed in fp32 (its compiled inference path, the default here)
+    round_products = False
 
     def __init__(self, config):
         super().__init__()
@@ -148,5 +158,6 @@ class CrossAttentionInterpolate(nn.Module):
         kv = self.to_kv(self.kv_norm(x_from))
         k = kv[..., :dim].unflatten(-1, (self.num_heads, self.head_dim))
         v = kv[..., dim:].unflatten(-1, (self.num_heads, self.head_dim))
-        out = knn_attention(k, v, self.neighbors, self.rel_pos, self.to_q.weight, self.scale, self.target_order)
+        out = knn_attention(k, v, self.neighbors, self.rel_pos, self.to_q.weight, self.scale, self.target_order,
+                            round_products=self.round_products)
         return self.to_o(out.to(x_from.dtype).flatten(-2))

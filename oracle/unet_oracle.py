@@ -108,12 +108,13 @@ def mosaic_block(P: dict, pre: str, x: torch.Tensor, z, cfg, norm_dtype: dict, i
     return x + cswiglu(P, pre + "ffn.", rms_norm(x, norm_dtype), z)
 
 
-def interpolate(P: dict, pre: str, x: torch.Tensor, num_heads: int, norm_dtype: dict) -> torch.Tensor:
+def interpolate(P: dict, pre: str, x: torch.Tensor, num_heads: int, norm_dtype: dict,
+                products: str = "fp32") -> torch.Tensor:
     dim = x.shape[-1]
     kv = linear(rms_norm(x, norm_dtype), P[pre + "to_kv.weight"])
     kv = rearrange(kv, "s b (n h d) -> n s b h d", h=num_heads, n=2)
     out = interp_oracle.knn_attention(kv[0], kv[1], P[pre + "neighbors"], P[pre + "rel_pos"],
-                                      P[pre + "to_q.weight"], (dim // num_heads) ** -0.5)
+                                      P[pre + "to_q.weight"], (dim // num_heads) ** -0.5, products=products)
     return linear(rearrange(out, "s b h d -> s b (h d)"), P[pre + "to_o.weight"])
 
 
@@ -139,7 +140,8 @@ def _stage_cfg(config, stage_cfg):
 
 
 def forward(P: dict, config, x: torch.Tensor, day_year_time: torch.Tensor, num_noise_samples: int,
-            noise: torch.Tensor | None, norm_dtype: dict, block_indices=None, band_stats=None) -> torch.Tensor:
+            noise: torch.Tensor | None, norm_dtype: dict, block_indices=None, band_stats=None,
+            interp_products: str = "fp32") -> torch.Tensor:
     """The Transformer forward (mosaic.py:304-337) on CPU tensors; P = the model's state dict.
 
     ``block_indices``: optional list of the selected block indices of every attention call, in
@@ -152,7 +154,11 @@ def forward(P: dict, config, x: torch.Tensor, day_year_time: torch.Tensor, num_n
     ``{"bad", "ambiguous", "rows", "band"}`` to ``calls``; with a callable ``"planted"`` in the
     dict, the indices it returns for the given ones are checked as well (``"bad_planted"``).  The band is relative because the
     given indices come from a device whose projections may round q and k differently in
-    the last place."""
+    the last place.
+
+    ``interp_products``: the product form of the two interpolations' gather-attention
+    (``interp_oracle.knn_attention``): "fp32" as the reference's compiled inference path
+    computes it, "bf16" as its eager ops do."""
     it = iter(block_indices) if block_indices is not None else None
     P = {k: v.detach().cpu() for k, v in P.items()}
     b, n, t, lon, lat, c = x.shape
@@ -171,7 +177,7 @@ def forward(P: dict, config, x: torch.Tensor, day_year_time: torch.Tensor, num_n
     h = torch.nn.functional.silu(h)
     h = linear(h, P["preprocess.3.weight"])
     h = rms_norm(h, norm_dtype)
-    h = interpolate(P, "interp_to_hp.", h, config.num_heads, norm_dtype)
+    h = interpolate(P, "interp_to_hp.", h, config.num_heads, norm_dtype, interp_products)
 
     stages = [*config.cg_stage_cfgs, config.bottleneck_cfg]
     skips = []
@@ -189,7 +195,7 @@ def forward(P: dict, config, x: torch.Tensor, day_year_time: torch.Tensor, num_n
         for j in range(st.decoder_depth):
             h = mosaic_block(P, f"decoder_stages.{u}.blocks.{j}.", h, z, _stage_cfg(config, st), norm_dtype, it, band_stats)
     h = rms_norm(h, norm_dtype)
-    h = interpolate(P, "interp_to_ll.", h, config.num_heads, norm_dtype)
+    h = interpolate(P, "interp_to_ll.", h, config.num_heads, norm_dtype, interp_products)
     h = rms_norm(h, norm_dtype)
     h = linear(h, P["postprocess.1.weight"])
     h = torch.nn.functional.silu(h)

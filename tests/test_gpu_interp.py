@@ -1,10 +1,15 @@
 """GPU parity of the k-nearest-neighbour cross-attention (CrossAttentionInterpolate's
 gather-attention, primitives.py:265-283) against the CPU oracle (marked ``gpu``).
 
-Bars: max-abs 2e-2 and relative L2 1e-2 (bf16 in, fp32 accumulate); the kernel rounds where
-the reference's elementwise bf16 tensor ops round, so nearly every output is bit-equal to the
-oracle's (sums in another order and the exponential's last fp32 bits aside): at least 97% of
-the elements must be.
+Both product forms are tested: exact products summed in fp32 (the default, as the reference's
+compiled inference path fuses them into the sums) against the oracle's ``products="fp32"``,
+and products rounded to bf16 (``round_products=True``, the reference's eager elementwise ops)
+against its ``products="bf16"``.  Bars: max-abs 2e-2 and relative L2 1e-2 (bf16 in, fp32
+accumulate); the kernel rounds where its oracle form rounds, so nearly every output is
+bit-equal to it (sums in another order and the exponential's last fp32 bits aside): at least
+97% of the elements must be.  Against the eager form the fp32 form is held to relative L2
+1e-2 (the two differ by up to two bf16 spacings where the softmax is sharp), and against a
+float64 evaluation of the same formula it must be at least as accurate as the eager form.
 """
 
 import pytest
@@ -31,6 +36,23 @@ def close(got, ref, min_equal=0.97):
     assert err <= MAX_ABS and rel <= REL_L2 and eq >= min_equal, f"max_abs {err:.3e} rel_l2 {rel:.3e} equal {eq:.4f}"
 
 
+FORMS = pytest.mark.parametrize("round_products", [False, True], ids=["fp32_products", "bf16_products"])
+
+
+def oracle(k, v, nb, rel, w_q, scale, round_products):
+    return IO.knn_attention(k, v, nb, rel, w_q, scale, products="bf16" if round_products else "fp32")
+
+
+def exact(k, v, nb, rel, w_q, scale):
+    """The gather-attention in float64 from the bf16 queries (to_q's bf16 output)."""
+    H = k.shape[2]
+    q = (rel.to(torch.bfloat16).float() @ w_q.float().t()).to(torch.bfloat16).double()
+    q = q.view(*q.shape[:2], 1, H, 64)
+    kg, vg = k.double()[nb], v.double()[nb]
+    p = torch.softmax((q * kg).sum(-1, keepdim=True) * scale, dim=1)
+    return (p * vg).sum(dim=1)
+
+
 def lonlat_grid(n_lon, n_lat):
     lon = torch.linspace(0, 360 - 360 / n_lon, n_lon)
     lat = torch.linspace(-90, 90, n_lat)
@@ -48,34 +70,46 @@ def rand(*shape, seed, scale=1.0):
     return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
 
 
+@FORMS
 @pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
 @pytest.mark.parametrize("K", [32, 29, 24, 20, 7, 1])
-def test_knn_attention_matches_oracle(direction, K):
+def test_knn_attention_matches_oracle(direction, K, round_products):
     ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))    # 312 and 192 points
     src, dst = (ll, hp) if direction == "ll_to_hp" else (hp, ll)
     nb, rel = scheme(src, dst, K)
     B, H = 2, 3
     k, v = rand(len(src), B, H, 64, seed=K), rand(len(src), B, H, 64, seed=K + 100)
     w_q = rand(H * 64, 3, seed=K + 200, scale=2.0)
-    ref = IO.knn_attention(k, v, nb, rel, w_q, 0.125)
-    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
+    ref = oracle(k, v, nb, rel, w_q, 0.125, round_products)
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125,
+                        round_products=round_products)
     torch.cuda.synchronize()
     if K == 1:
         assert torch.equal(got.cpu(), v[nb[:, 0]])
     close(got, ref)
+    if not round_products:   # the fp32 form against the eager form and against float64
+        eager = IO.knn_attention(k, v, nb, rel, w_q, 0.125).double()
+        g = got.cpu().double()
+        assert ((g - eager).norm() / eager.norm()).item() <= REL_L2
+        x = exact(k, v, nb, rel, w_q, 0.125)
+        err_got, err_eager = ((g - x).norm() / x.norm()).item(), ((eager - x).norm() / x.norm()).item()
+        assert err_got <= 1.05 * err_eager, (err_got, err_eager)
 
 
-def test_knn_attention_zero_queries_and_large_scores():
+@FORMS
+def test_knn_attention_zero_queries_and_large_scores(round_products):
     ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
     nb, rel = scheme(ll, hp, 24)
     k, v = rand(len(ll), 1, 4, 64, seed=1, scale=3.0), rand(len(ll), 1, 4, 64, seed=2)
     for w_q, scale in ((torch.zeros(4 * 64, 3, dtype=torch.bfloat16), 0.125), (rand(4 * 64, 3, seed=3, scale=4.0), 1.0)):
-        ref = IO.knn_attention(k, v, nb, rel, w_q, scale)
-        got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), scale)
+        ref = oracle(k, v, nb, rel, w_q, scale, round_products)
+        got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), scale,
+                            round_products=round_products)
         close(got, ref)
 
 
-def test_knn_attention_strided_views_equal_contiguous():
+@FORMS
+def test_knn_attention_strided_views_equal_contiguous(round_products):
     ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
     nb, rel = scheme(hp, ll, 20)
     S, B, H = len(hp), 3, 2
@@ -83,14 +117,16 @@ def test_knn_attention_strided_views_equal_contiguous():
     k = kv[..., :H * 64].unflatten(-1, (H, 64))
     v = kv[..., H * 64:].unflatten(-1, (H, 64))
     w_q = rand(H * 64, 3, seed=5).to(DEV)
-    a = knn_attention(k, v, nb.to(DEV), rel.to(DEV), w_q, 0.125)
-    b = knn_attention(k.contiguous(), v.contiguous(), nb.to(DEV), rel.to(DEV), w_q, 0.125)
+    a = knn_attention(k, v, nb.to(DEV), rel.to(DEV), w_q, 0.125, round_products=round_products)
+    b = knn_attention(k.contiguous(), v.contiguous(), nb.to(DEV), rel.to(DEV), w_q, 0.125,
+                      round_products=round_products)
     assert torch.equal(a, b)
-    close(a, IO.knn_attention(k.cpu(), v.cpu(), nb, rel, w_q.cpu(), 0.125))
+    close(a, oracle(k.cpu(), v.cpu(), nb, rel, w_q.cpu(), 0.125, round_products))
 
 
+@FORMS
 @pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
-def test_knn_attention_full_size_sampled(direction):
+def test_knn_attention_full_size_sampled(direction, round_products):
     """Model grids: 121 x 240 lat-lon (29040 points) and HEALPix nside 64 (49152), K 24,
     12 heads; every target computed on the device, a sample of targets against the oracle."""
     ll, hp = lonlat_grid(240, 121), torch.deg2rad(get_healpix_grid(64))
@@ -99,24 +135,28 @@ def test_knn_attention_full_size_sampled(direction):
     nb, rel = scheme(src, dst, K)
     k, v = rand(len(src), B, H, 64, seed=7), rand(len(src), B, H, 64, seed=8)
     w_q = rand(H * 64, 3, seed=9)
-    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125).cpu()
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125,
+                        round_products=round_products).cpu()
     g = torch.Generator().manual_seed(10)
     sample = torch.cat([torch.arange(64), len(dst) - 64 + torch.arange(64),
                         torch.randint(0, len(dst), (1024,), generator=g)])
-    ref = IO.knn_attention(k, v, nb[sample], rel[sample], w_q, 0.125)
+    ref = oracle(k, v, nb[sample], rel[sample], w_q, 0.125, round_products)
     close(got[sample], ref)
 
 
-def test_knn_attention_deterministic():
+@FORMS
+def test_knn_attention_deterministic(round_products):
     ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
     nb, rel = [t.to(DEV) for t in scheme(ll, hp, 24)]
     k, v = rand(len(ll), 2, 3, 64, seed=11).to(DEV), rand(len(ll), 2, 3, 64, seed=12).to(DEV)
     w_q = rand(3 * 64, 3, seed=13).to(DEV)
-    a = knn_attention(k, v, nb, rel, w_q, 0.125)
-    assert all(torch.equal(a, knn_attention(k, v, nb, rel, w_q, 0.125)) for _ in range(3))
+    a = knn_attention(k, v, nb, rel, w_q, 0.125, round_products=round_products)
+    assert all(torch.equal(a, knn_attention(k, v, nb, rel, w_q, 0.125, round_products=round_products))
+               for _ in range(3))
 
 
-def test_cross_attention_interpolate_module():
+@FORMS
+def test_cross_attention_interpolate_module(round_products):
     from types import SimpleNamespace
     cfg = SimpleNamespace(k_neighbors=20, dim=192, num_heads=3, rmsnorm_elementwise_affine=True)
     torch.manual_seed(0)
@@ -124,6 +164,7 @@ def test_cross_attention_interpolate_module():
     ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
     m.initialize_interpolation_scheme(ll, hp)
     m = m.to(DEV).to(torch.bfloat16)
+    m.round_products = round_products
     x = torch.randn(len(ll), 2, 192, device=DEV).to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="no backward"):   # parameters require grad
         m(x)
@@ -134,13 +175,14 @@ def test_cross_attention_interpolate_module():
         kv = m.to_kv(m.kv_norm(x))
         k = kv[..., :192].unflatten(-1, (3, 64)).cpu()
         v = kv[..., 192:].unflatten(-1, (3, 64)).cpu()
-        att = IO.knn_attention(k, v, m.neighbors.cpu(), m.rel_pos.float().cpu(), m.to_q.weight.cpu(), m.scale)
+        att = oracle(k, v, m.neighbors.cpu(), m.rel_pos.float().cpu(), m.to_q.weight.cpu(), m.scale, round_products)
         ref = m.to_o(att.to(DEV).flatten(-2))
     assert y.shape == (len(hp), 2, 192)
     close(y, ref, min_equal=0.9)
 
 
-def test_knn_attention_random_neighbour_lists():
+@FORMS
+def test_knn_attention_random_neighbour_lists(round_products):
     """Neighbour lists with no spatial structure (repeats allowed), K = 13 (a partial slot)."""
     S_from, S_to, K = 2000, 160, 13
     g = torch.Generator().manual_seed(30)
@@ -148,23 +190,27 @@ def test_knn_attention_random_neighbour_lists():
     rel = torch.nn.functional.normalize(torch.randn(S_to, K, 3, generator=g), dim=-1)
     k, v = rand(S_from, 2, 2, 64, seed=31), rand(S_from, 2, 2, 64, seed=32)
     w_q = rand(2 * 64, 3, seed=33)
-    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
-    close(got, IO.knn_attention(k, v, nb, rel, w_q, 0.125))
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125,
+                        round_products=round_products)
+    close(got, oracle(k, v, nb, rel, w_q, 0.125, round_products))
 
 
+@FORMS
 @pytest.mark.parametrize("scale", [0.1, 0.3])
-def test_knn_attention_scale_not_a_power_of_two(scale):
+def test_knn_attention_scale_not_a_power_of_two(scale, round_products):
     """A scale that is not a power of two rounds bf16(score) * scale to bf16 again (the
     kernel's other path; 0.125 = 64^-0.5 skips that exact rounding)."""
     ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
     nb, rel = scheme(ll, hp, 24)
     k, v = rand(len(ll), 2, 3, 64, seed=40, scale=2.0), rand(len(ll), 2, 3, 64, seed=41)
     w_q = rand(3 * 64, 3, seed=42, scale=2.0)
-    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), scale)
-    close(got, IO.knn_attention(k, v, nb, rel, w_q, scale))
+    got = knn_attention(k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), scale,
+                        round_products=round_products)
+    close(got, oracle(k, v, nb, rel, w_q, scale, round_products))
 
 
-def test_knn_attention_negative_point_stride_equals_forward_order():
+@FORMS
+def test_knn_attention_negative_point_stride_equals_forward_order(round_products):
     """k / v handed over through the C ABI as views with a negative point stride over copies
     stored in reverse row order (point n is still k[n]): the kernel's 64-bit offset path,
     which must give the same output as the forward-order call (32-bit offsets)."""
@@ -175,7 +221,7 @@ def test_knn_attention_negative_point_stride_equals_forward_order():
     k, v = rand(S, B, H, 64, seed=50).to(DEV), rand(S, B, H, 64, seed=51).to(DEV)
     w_q = rand(H * 64, 3, seed=52).to(DEV)
     nb_d, rel_d = nb.to(DEV), rel.to(DEV)
-    fwd = knn_attention(k, v, nb_d, rel_d, w_q, 0.125)
+    fwd = knn_attention(k, v, nb_d, rel_d, w_q, 0.125, round_products=round_products)
     kr, vr = k.flip(0).contiguous(), v.flip(0).contiguous()      # row S-1-n holds point n
 
     def reversed_view(t):     # starts at row S-1 (point 0) and steps back one row per point
@@ -183,17 +229,19 @@ def test_knn_attention_negative_point_stride_equals_forward_order():
         return _lib.Bnhd(last.data_ptr(), t.stride(1), -t.stride(0), t.stride(2))
     nb32 = nb_d.to(torch.int32).contiguous()
     out = torch.empty_like(fwd)
-    st = _lib.lib().mosaic_knn_interp_fwd(reversed_view(kr), reversed_view(vr), nb32.data_ptr(),
-                                          rel_d.float().contiguous().data_ptr(), w_q.data_ptr(),
-                                          S, len(ll), B, H, 64, 24, 0.125, out.data_ptr(),
-                                          torch.cuda.current_stream().cuda_stream)
-    _lib.check(st, "mosaic_knn_interp_fwd")
+    flags = _lib.KNN_ROUND_PRODUCTS if round_products else 0
+    st = _lib.lib().mosaic_knn_interp_fwd_ex(reversed_view(kr), reversed_view(vr), nb32.data_ptr(),
+                                             rel_d.float().contiguous().data_ptr(), w_q.data_ptr(), None,
+                                             S, len(ll), B, H, 64, 24, 0.125, flags, out.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "mosaic_knn_interp_fwd_ex")
     torch.cuda.synchronize()
     assert torch.equal(out, fwd)
 
 
+@FORMS
 @pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
-def test_knn_attention_target_order_leaves_the_output_unchanged(direction):
+def test_knn_attention_target_order_leaves_the_output_unchanged(direction, round_products):
     """The targets taken in the spatial order, in a random order and in index order: the same
     output bit for bit (each target's row is computed alone)."""
     ll, hp = lonlat_grid(48, 25), torch.deg2rad(get_healpix_grid(8))
@@ -201,9 +249,34 @@ def test_knn_attention_target_order_leaves_the_output_unchanged(direction):
     nb, rel = [t.to(DEV) for t in scheme(src, dst, 24)]
     k, v = rand(len(src), 3, 2, 64, seed=60).to(DEV), rand(len(src), 3, 2, 64, seed=61).to(DEV)
     w_q = rand(2 * 64, 3, seed=62).to(DEV)
-    base = knn_attention(k, v, nb, rel, w_q, 0.125)
+    base = knn_attention(k, v, nb, rel, w_q, 0.125, round_products=round_products)
     g = torch.Generator().manual_seed(63)
     for order in (spatial_order(dst), torch.randperm(len(dst), generator=g)):
-        assert torch.equal(knn_attention(k, v, nb, rel, w_q, 0.125, target_order=order.to(DEV)), base)
+        assert torch.equal(knn_attention(k, v, nb, rel, w_q, 0.125, target_order=order.to(DEV),
+                                         round_products=round_products), base)
     with pytest.raises(ValueError, match="target_order"):
         knn_attention(k, v, nb, rel, w_q, 0.125, target_order=torch.arange(3, device=DEV))
+
+
+def test_knn_attention_legacy_entry_points_round_products():
+    """mosaic_knn_interp_fwd / _ordered are the rounded-product form; unknown flag bits are
+    refused before any launch."""
+    from mosaic_amd import _lib
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(ll, hp, 24)
+    S, B, H = len(ll), 2, 2
+    k, v = rand(S, B, H, 64, seed=70).to(DEV), rand(S, B, H, 64, seed=71).to(DEV)
+    w_q = rand(H * 64, 3, seed=72).to(DEV)
+    nb32, rel32 = nb.to(DEV, torch.int32).contiguous(), rel.to(DEV).float().contiguous()
+    want = knn_attention(k, v, nb.to(DEV), rel.to(DEV), w_q, 0.125, round_products=True)
+    out = torch.empty_like(want)
+    kv = [_lib.Bnhd(t.data_ptr(), t.stride(1), t.stride(0), t.stride(2)) for t in (k, v)]
+    stream = torch.cuda.current_stream().cuda_stream
+    st = _lib.lib().mosaic_knn_interp_fwd(kv[0], kv[1], nb32.data_ptr(), rel32.data_ptr(), w_q.data_ptr(),
+                                          S, len(hp), B, H, 64, 24, 0.125, out.data_ptr(), stream)
+    _lib.check(st, "mosaic_knn_interp_fwd")
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    st = _lib.lib().mosaic_knn_interp_fwd_ex(kv[0], kv[1], nb32.data_ptr(), rel32.data_ptr(), w_q.data_ptr(), None,
+                                             S, len(hp), B, H, 64, 24, 0.125, 2, out.data_ptr(), stream)
+    assert st == _lib.ERR_MODE

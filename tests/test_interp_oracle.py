@@ -82,15 +82,16 @@ def test_zero_queries_give_the_mean():
     assert (out - mean).abs().max().item() <= 2 ** -7 * v.double().abs().max().item()
 
 
+@pytest.mark.parametrize("products", ["bf16", "fp32"])
 @pytest.mark.parametrize("K", [7, 24])
-def test_matches_float64_brute_force(K):
+def test_matches_float64_brute_force(K, products):
     ll, hp = _grids()
     nb, rel = _scheme(ll, hp, K)
     H = 2
     k, v = _kv(len(ll), 2, H, seed=3)
     w_q = (torch.randn(H * 64, 3, generator=torch.Generator().manual_seed(4)) * 0.6).to(torch.bfloat16)
     scale = 64 ** -0.5
-    out = IO.knn_attention(k, v, nb, rel, w_q, scale).double()
+    out = IO.knn_attention(k, v, nb, rel, w_q, scale, products=products).double()
     ref = torch.zeros_like(out)
     W = w_q.double()
     for t in range(len(hp)):
@@ -103,6 +104,32 @@ def test_matches_float64_brute_force(K):
     err = (out - ref).abs().max().item()
     assert err <= 2e-2, err
     assert ((out - ref).norm() / ref.norm()).item() <= 1e-2
+
+
+def test_product_forms_agree_where_products_are_exact_in_bf16():
+    """Inputs whose products all fit bf16 (one-hot rel_pos, so q = a column of w_q in steps of
+    1/4; integer k; v in {0, +-1/2, +-1, +-2}; a scale that keeps the weights within a factor
+    e^2 of each other, so every fp32 sum is exact): rounding the products changes nothing, and
+    the two forms must be equal bit for bit.  On general inputs they must differ somewhere."""
+    ll, hp = _grids()
+    K, B, H = 16, 2, 2
+    nb, _ = _scheme(ll, hp, K)
+    g = torch.Generator().manual_seed(11)
+    rel = torch.nn.functional.one_hot(torch.randint(0, 3, (len(hp), K), generator=g), 3).float()
+    w_q = (torch.randint(-8, 9, (H * 64, 3), generator=g) / 4).to(torch.bfloat16)
+    k = torch.randint(-7, 8, (len(ll), B, H, 64), generator=g).to(torch.bfloat16)
+    pow2 = torch.tensor([0.0, 0.5, -0.5, 1.0, -1.0, 2.0, -2.0])
+    v = pow2[torch.randint(0, len(pow2), (len(ll), B, H, 64), generator=g)].to(torch.bfloat16)
+    scale = 1 / 2048                      # |q . k| <= 2 * 7 * 64: scaled scores within [-0.44, 0.44]
+    a = IO.knn_attention(k, v, nb, rel, w_q, scale, products="bf16")
+    b = IO.knn_attention(k, v, nb, rel, w_q, scale, products="fp32")
+    assert torch.equal(a, b)
+    assert (a != 0).float().mean() > 0.5   # not a degenerate all-zero case
+    kr, vr = _kv(len(ll), B, H, seed=12)
+    _, relr = _scheme(ll, hp, K)
+    wr = torch.randn(H * 64, 3, generator=g).to(torch.bfloat16)
+    assert not torch.equal(IO.knn_attention(kr, vr, nb, relr, wr, 0.125, products="bf16"),
+                           IO.knn_attention(kr, vr, nb, relr, wr, 0.125, products="fp32"))
 
 
 def test_neighbour_order_does_not_matter():
