@@ -258,12 +258,14 @@ def interp_leg(L, args, dev, stream):
     (mosaic_knn_interp_fwd_ex, targets in the model's spatial order): 121 x 240 lat-lon
     (29040 points) <-> HEALPix nside 64 (49152), 24 neighbours, 12 heads of 64,
     ``--interp-batch`` members, both directions; ``ms`` is the model's form (exact products
-    summed in fp32), ``ms_rounded_products`` the eager form (every product rounded to bf16).
+    summed in fp32, the LDS-staged kernel over the module's target tiles), ``ms_per_target``
+    the same form without tiles and ``ms_rounded_products`` the eager form (every product
+    rounded to bf16).
     Algorithmic bytes per launch: every k / v row read once, the output written once, the
     neighbour lists and relative positions read."""
     import numpy as np
     from mosaic_amd.healpix import get_healpix_grid
-    from mosaic_amd.interp import get_neighbors, rad_to_xyz, spatial_order
+    from mosaic_amd.interp import get_neighbors, knn_tiles, rad_to_xyz, spatial_order
     lon = torch.linspace(0, 358.5, 240)
     lat = torch.linspace(-90, 90, 121)
     ll = torch.deg2rad(torch.stack(torch.meshgrid(lon, lat, indexing="ij"), -1).reshape(-1, 2))
@@ -276,7 +278,11 @@ def interp_leg(L, args, dev, stream):
         nb = torch.from_numpy(np.ascontiguousarray(get_neighbors(src.numpy(), dst.numpy(), k=K)))
         rel = torch.nn.functional.normalize(rad_to_xyz(dst).unsqueeze(1) - rad_to_xyz(src)[nb], dim=-1)
         nb_d, rel_d = nb.to(dev, torch.int32), rel.to(dev)
-        order = spatial_order(dst).to(dev, torch.int32)
+        order_cpu = spatial_order(dst)
+        order = order_cpu.to(dev, torch.int32)
+        tiles = {n: (t.to(dev) if torch.is_tensor(t) else t) for n, t in knn_tiles(nb, order_cpu).items()}
+        tl = _lib.KnnTiles(tiles["start"].data_ptr(), tiles["src"].data_ptr(), tiles["nsrc"].data_ptr(),
+                           tiles["slot"].data_ptr(), tiles["start"].numel() - 1, tiles["max_rows"])
         kv = torch.randn(len(src), B, 2 * H * 64, generator=gd, device=dev, dtype=torch.bfloat16)
         k = kv[..., :H * 64].unflatten(-1, (H, 64))
         v = kv[..., H * 64:].unflatten(-1, (H, 64))
@@ -286,31 +292,33 @@ def interp_leg(L, args, dev, stream):
         kb, vb = _lib.Bnhd(k.data_ptr(), k.stride(1), k.stride(0), k.stride(2)), \
             _lib.Bnhd(v.data_ptr(), v.stride(1), v.stride(0), v.stride(2))
 
-        def call(flags=0):
+        def call(flags=0, tiled=True):
             st = L.mosaic_knn_interp_fwd_ex(kb, vb, nb_d.data_ptr(), rel_d.data_ptr(), w_q.data_ptr(),
-                                            order.data_ptr(), len(src), len(dst), B, H, 64, K, 0.125, flags,
-                                            out.data_ptr(), sp)
+                                            order.data_ptr(), ctypes.byref(tl) if tiled else None, len(src),
+                                            len(dst), B, H, 64, K, 0.125, flags, out.data_ptr(), sp)
             if st:
                 raise RuntimeError(_lib.strerror(st))
 
-        def timed(flags):
+        def timed(flags, tiled=True):
             for _ in range(3):
-                call(flags)
+                call(flags, tiled)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             e0.record(stream)
             for _ in range(args.steps):
-                call(flags)
+                call(flags, tiled)
             e1.record(stream)
             torch.cuda.synchronize()
             return e0.elapsed_time(e1) / args.steps
         ms_rounded = timed(_lib.KNN_ROUND_PRODUCTS)
+        ms_direct = timed(0, tiled=False)
         ms = timed(0)
         nbytes = len(src) * B * H * 64 * 2 * 2 + len(dst) * B * H * 64 * 2 + len(dst) * K * (4 + 12)
         gbs = nbytes / (ms * 1e-3) / 1e9
         leg = {"num_from": len(src), "num_to": len(dst), "ms": round(ms, 4), "bytes": nbytes,
                "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
-               "ms_rounded_products": round(ms_rounded, 4)}
+               "ms_per_target": round(ms_direct, 4), "ms_rounded_products": round(ms_rounded, 4),
+               "tiles": tiles["start"].numel() - 1, "tile_rows": tiles["max_rows"]}
         if B <= 4:   # the reference's formulation in eager torch (materialised q and gathers)
             def eager():
                 q = (rel_d.to(torch.bfloat16) @ w_q.t()).view(len(dst), K, 1, H, 64)

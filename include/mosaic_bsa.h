@@ -234,20 +234,40 @@ MOSAIC_API int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const
 /* Flags of mosaic_knn_interp_fwd_ex. */
 #define MOSAIC_KNN_ROUND_PRODUCTS 1u /* round every q*k and w*v product to bf16 before summing */
 
-/* mosaic_knn_interp_fwd_ordered with a choice of product rounding (same replacement,
-   primitives.py:265-283).  With MOSAIC_KNN_ROUND_PRODUCTS every product of (q * k).sum(-1)
-   and (w * v).sum(1) is rounded to bf16 before the fp32 sum, as the reference's eager bf16
-   elementwise ops do (mosaic_knn_interp_fwd and _ordered are this form).  Without it the
-   products are exact and summed in fp32, as the reference's default inference path computes
-   them (its torch.compile'd model, inference.py:470-473, fuses each product into its
-   reduction); the roundings of the score, the scaled score, the weights and the output are
-   the same in both.  Unknown flag bits return MOSAIC_ERR_MODE. */
+/* Tiles of targets for mosaic_knn_interp_fwd_ex (int32 device arrays, 4-byte aligned).  Tile i
+   holds the targets at positions [start[i], start[i+1]) of the target order (at most 16;
+   start[0] = 0, start[num_tiles] = num_to); src[i, 0 .. nsrc[i]-1] are the distinct source
+   points its targets use (at most max_rows; src is [num_tiles, max_rows]); slot[pos, j] is the
+   row of that list holding neighbour j of the target at order position pos (slot is
+   [num_to, num_neighbors]).  Static per grid pair and order: built once with the neighbours.
+   Entries out of range are clamped; tiles that do not partition the order leave rows of out
+   unwritten. */
+typedef struct {
+    const int32_t* start;
+    const int32_t* src;
+    const int32_t* nsrc;
+    const int32_t* slot;
+    int32_t num_tiles;
+    int32_t max_rows; /* a multiple of 8, at most 128 */
+} mosaic_knn_tiles;
+
+/* mosaic_knn_interp_fwd_ordered with a choice of product rounding and optional target tiles
+   (same replacement, primitives.py:265-283).  With MOSAIC_KNN_ROUND_PRODUCTS every product of
+   (q * k).sum(-1) and (w * v).sum(1) is rounded to bf16 before the fp32 sum, as the
+   reference's eager bf16 elementwise ops do (mosaic_knn_interp_fwd and _ordered are this
+   form).  Without it the products are exact and summed in fp32, as the reference's default
+   inference path computes them (its torch.compile'd model, inference.py:470-473, fuses each
+   product into its reduction); the roundings of the score, the scaled score, the weights and
+   the output are the same in both.  tiles (optional, fp32 products only; ignored with
+   MOSAIC_KNN_ROUND_PRODUCTS): each tile's distinct source rows are staged once per member and
+   head for all its targets; the output is the same bit for bit (neighbors is then not read;
+   the tiles were built from it).  Unknown flag bits return MOSAIC_ERR_MODE. */
 MOSAIC_API int mosaic_knn_interp_fwd_ex(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors,
                                         const float* rel_pos, const void* w_q,
-                                        const int32_t* target_order, int32_t num_from, int32_t num_to,
-                                        int32_t batch, int32_t num_heads, int32_t head_dim,
-                                        int32_t num_neighbors, float scale, uint32_t flags, void* out,
-                                        void* stream);
+                                        const int32_t* target_order, const mosaic_knn_tiles* tiles,
+                                        int32_t num_from, int32_t num_to, int32_t batch,
+                                        int32_t num_heads, int32_t head_dim, int32_t num_neighbors,
+                                        float scale, uint32_t flags, void* out, void* stream);
 
 /*
  * Selected-branch attention given block indices.  Replaces mosaic_sparse_attn /

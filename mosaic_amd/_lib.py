@@ -79,6 +79,11 @@ class Bnhd(ctypes.Structure):
                 ("stride_n", ctypes.c_int64), ("stride_h", ctypes.c_int64)]
 
 
+class KnnTiles(ctypes.Structure):
+    _fields_ = [("start", ctypes.c_void_p), ("src", ctypes.c_void_p), ("nsrc", ctypes.c_void_p),
+                ("slot", ctypes.c_void_p), ("num_tiles", ctypes.c_int32), ("max_rows", ctypes.c_int32)]
+
+
 class BsaArgs(ctypes.Structure):
     _fields_ = [
         ("batch", ctypes.c_int32), ("seq_len", ctypes.c_int32),
@@ -132,8 +137,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mosaic_knn_interp_fwd_ordered.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32,
                                                   c_i32, c_i32, c_f, c_vp, c_vp]
     lib.mosaic_knn_interp_fwd_ordered.restype = c_int
-    lib.mosaic_knn_interp_fwd_ex.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32,
-                                             c_i32, c_i32, c_f, ctypes.c_uint32, c_vp, c_vp]
+    lib.mosaic_knn_interp_fwd_ex.argtypes = [Bnhd, Bnhd, c_vp, c_vp, c_vp, c_vp, P(KnnTiles), c_i32, c_i32,
+                                             c_i32, c_i32, c_i32, c_i32, c_f, ctypes.c_uint32, c_vp, c_vp]
     lib.mosaic_knn_interp_fwd_ex.restype = c_int
     c_i64 = ctypes.c_int64
     lib.mosaic_rms_norm_fwd.argtypes = [c_vp, c_vp, c_i32, c_i64, c_i32, c_i64, c_i64, c_vp, c_f, c_vp, c_vp,

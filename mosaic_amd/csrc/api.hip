@@ -523,21 +523,32 @@ int mosaic_knn_interp_fwd_ordered(mosaic_bnhd k, mosaic_bnhd v, const int32_t* n
                                   const void* w_q, const int32_t* target_order, int32_t num_from, int32_t num_to,
                                   int32_t batch, int32_t num_heads, int32_t head_dim, int32_t num_neighbors,
                                   float scale, void* out, void* stream) {
-    return mosaic_knn_interp_fwd_ex(k, v, neighbors, rel_pos, w_q, target_order, num_from, num_to, batch, num_heads,
-                                    head_dim, num_neighbors, scale, MOSAIC_KNN_ROUND_PRODUCTS, out, stream);
+    return mosaic_knn_interp_fwd_ex(k, v, neighbors, rel_pos, w_q, target_order, nullptr, num_from, num_to, batch,
+                                    num_heads, head_dim, num_neighbors, scale, MOSAIC_KNN_ROUND_PRODUCTS, out, stream);
 }
 
 int mosaic_knn_interp_fwd_ex(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighbors, const float* rel_pos,
-                             const void* w_q, const int32_t* target_order, int32_t num_from, int32_t num_to,
-                             int32_t batch, int32_t num_heads, int32_t head_dim, int32_t num_neighbors, float scale,
-                             uint32_t flags, void* out, void* stream) {
+                             const void* w_q, const int32_t* target_order, const mosaic_knn_tiles* tiles,
+                             int32_t num_from, int32_t num_to, int32_t batch, int32_t num_heads, int32_t head_dim,
+                             int32_t num_neighbors, float scale, uint32_t flags, void* out, void* stream) {
     if (flags & ~MOSAIC_KNN_ROUND_PRODUCTS) return MOSAIC_ERR_MODE;
+    const bool tiled = tiles != nullptr && !(flags & MOSAIC_KNN_ROUND_PRODUCTS);
+    if (tiled) {
+        if (tiles->start == nullptr || tiles->src == nullptr || tiles->nsrc == nullptr || tiles->slot == nullptr)
+            return MOSAIC_ERR_NULL_POINTER;
+        if (tiles->num_tiles <= 0 || tiles->max_rows <= 0 || tiles->max_rows % 8 || tiles->max_rows > kKnnTileRows)
+            return MOSAIC_ERR_SHAPE;
+        for (const void* t : {(const void*)tiles->start, (const void*)tiles->src, (const void*)tiles->nsrc,
+                              (const void*)tiles->slot})
+            if (reinterpret_cast<uintptr_t>(t) % 4) return MOSAIC_ERR_ALIGNMENT;
+    }
     if (num_from <= 0 || num_to <= 0 || batch <= 0 || num_heads <= 0) return MOSAIC_ERR_SHAPE;
     if (head_dim != kHeadDim) return MOSAIC_ERR_HEAD_DIM;
     if (num_neighbors <= 0 || num_neighbors > 32) return MOSAIC_ERR_BLOCK_COUNT;
     if (int e = check_bnhd(k)) return e;
     if (int e = check_bnhd(v)) return e;
-    if (neighbors == nullptr || rel_pos == nullptr || w_q == nullptr || out == nullptr) return MOSAIC_ERR_NULL_POINTER;
+    if ((neighbors == nullptr && !tiled) || rel_pos == nullptr || w_q == nullptr || out == nullptr)
+        return MOSAIC_ERR_NULL_POINTER;
     if (!aligned16(out) || !aligned16(w_q) || reinterpret_cast<uintptr_t>(rel_pos) % 4 ||
         reinterpret_cast<uintptr_t>(neighbors) % 4 || reinterpret_cast<uintptr_t>(target_order) % 4)
         return MOSAIC_ERR_ALIGNMENT;
@@ -555,6 +566,13 @@ int mosaic_knn_interp_fwd_ex(mosaic_bnhd k, mosaic_bnhd v, const int32_t* neighb
     p.scale_pow2 = std::isfinite(p.scale) && p.scale >= 0x1p-126f && std::frexp(p.scale, &exp2) == 0.5f;
     p.scale_log2e = p.scale * kLog2e;
     p.round_products = (flags & MOSAIC_KNN_ROUND_PRODUCTS) != 0;
+    if (tiled && knn_tiled_supported(p)) {
+        KnnTiles t{};
+        t.start = tiles->start; t.src = tiles->src; t.nsrc = tiles->nsrc; t.slot = tiles->slot;
+        t.n = tiles->num_tiles; t.rows = tiles->max_rows;
+        return launch_status(launch_knn_attn_tiled(p, t, static_cast<hipStream_t>(stream)));
+    }
+    if (neighbors == nullptr) return MOSAIC_ERR_NULL_POINTER;  // tiles given, but not usable here
     return launch_status(launch_knn_attn(p, static_cast<hipStream_t>(stream)));
 }
 

@@ -342,6 +342,23 @@ struct InterpParams {
 };
 hipError_t launch_knn_attn(const InterpParams& p, hipStream_t s);
 
+// Tiles of consecutive targets (in the target order) for the LDS-staged k-NN kernel: each tile
+// stages the distinct source rows its targets use once per (member, head).  Built on the host
+// from the neighbour lists and the order (static per grid pair).
+constexpr int kKnnTileTargets = 16;  // targets per tile at most (4 per wave)
+constexpr int kKnnTileRows = 128;    // distinct source points per tile at most
+struct KnnTiles {
+    const int32_t* start;  // [n + 1]: tile i holds the targets at order positions [start[i], start[i + 1])
+    const int32_t* src;    // [n, rows]: the tile's distinct source points (the first nsrc[i] used)
+    const int32_t* nsrc;   // [n]
+    const int32_t* slot;   // [S_to, K]: neighbour j of the target at order position pos is row
+                           // slot[pos, j] of its tile's src
+    int n, rows;           // rows: a multiple of 8, at most kKnnTileRows (the LDS staging capacity)
+};
+hipError_t launch_knn_attn_tiled(const InterpParams& p, const KnnTiles& t, hipStream_t s);
+// whether launch_knn_attn_tiled takes p (fp32 products, 32-bit chunk offsets)
+bool knn_tiled_supported(const InterpParams& p);
+
 // Maximum number of selected blocks per query block (block indices are staged in LDS).
 constexpr int kMaxSelected = 1024;
 

@@ -42,7 +42,11 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float x) {
-    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+    // every lane's source lane exists for the patterns used here, so the old value and the
+    // bound control never matter; with an undefined old value the compiler folds the move
+    // into the add (with old = 0 it kept a separate move and a zeroing move for
+    // row_half_mirror)
+    return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, true));
 }
 template <int CTRL>
 __device__ __forceinline__ float dpp_max(float x) {
@@ -251,6 +255,57 @@ __device__ __forceinline__ void out_fp32(uint32_t w_lo, uint32_t w_hi, const uin
     }
 }
 
+// The score of a slot in base-2 units, sc = bf16(bf16(part) * scale) * log2 e.  A power-of-two
+// scale leaves bf16(part) * scale a bf16 value (a product too small to be normal is below
+// 2^-126 in magnitude, and so is the difference its rounding would make), so that case takes
+// one multiply by scale * log2 e.
+template <bool POW2>
+__device__ __forceinline__ float scaled_score(float part, const InterpParams& p) {
+    return POW2 ? round_bf16(part) * p.scale_log2e : round_bf16(round_bf16(part) * p.scale) * kLog2e;
+}
+
+// Softmax weights of the lane's slots over the K neighbours, from the slots' base-2 scores and
+// the lane's own maximum m: exp2(sc - max) / sum (0 for an absent neighbour: score -inf, the
+// maximum finite).
+template <int NSLOT>
+__device__ __forceinline__ void softmax_weights(const float (&sc)[NSLOT], float m, float (&w)[NSLOT]) {
+    m = group_max(m);
+    float l = 0.f;
+#pragma unroll
+    for (int i = 0; i < NSLOT; ++i) {
+        w[i] = __builtin_amdgcn_exp2f(sc[i] - m);
+        l += w[i];
+    }
+    const float inv = __builtin_amdgcn_rcpf(group_sum(l));
+#pragma unroll
+    for (int i = 0; i < NSLOT; ++i) w[i] *= inv;
+}
+
+// acc[d] = sum over the lane's slots of w * v[d] with exact products, slot by slot
+template <int NSLOT>
+__device__ __forceinline__ void weighted_sum_fp32(const float (&w)[NSLOT], const uint4 (&vw)[NSLOT], float (&acc)[8]) {
+#pragma unroll
+    for (int i = 0; i < NSLOT; ++i) {
+        const uint32_t w_lo = pack_bf16x2(w[i], 0.f), w_hi = pack_bf16x2(0.f, w[i]);
+        if (i == 0) out_fp32<true>(w_lo, w_hi, vw[i], acc);
+        else out_fp32<false>(w_lo, w_hi, vw[i], acc);
+    }
+}
+
+// The lane's 8 partial output dimensions reduce-scattered over the 8 neighbour groups: halves
+// (dims e / e + 4), row pairs (e / e + 2), then lanes l ^ 8 (e / e + 1); the lane ends up with
+// dimension 8 dc + 4 (l / 32) + 2 ((l / 16) % 2) + (l / 8) % 2 summed over all neighbours.
+__device__ __forceinline__ float reduce_scatter(const float (&acc)[8], int lane) {
+    float r4[4], r2[2];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r4[e] = swap32_add(acc[e], acc[e + 4]);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) r2[e] = swap16_add(r4[e], r4[e + 2]);
+    const bool odd8 = lane & 8;
+    const float keep = odd8 ? r2[1] : r2[0], give = odd8 ? r2[0] : r2[1];
+    return keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(give), 0x128, 0xf, 0xf, false));
+}
+
 __device__ __forceinline__ void unpack8(const uint4& w, float (&f)[8]) {
     const uint32_t a[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -425,20 +480,252 @@ __global__ __launch_bounds__(kInterpWaves * 64) __attribute__((amdgpu_waves_per_
     }
 }
 
+// LDS-staged form (fp32 products): one workgroup per (tile of up to 16 targets, head).  The
+// per-target kernel above issues 6 wave-wide 16-byte loads per (target, member, head), and at
+// one wave-instruction per ~32 cycles the texture addresser is then busy all the time; here
+// the tile's distinct source rows of k and v (the host-built tables) go into LDS once per
+// member with direct-to-LDS loads (lane l of an instruction lands at byte 16 l of a 1 KB run
+// of 8 rows), double-buffered, and the targets read them with ds_read_b128.  The arithmetic
+// per (target, member, head) is the fp32-product form of the kernel above in the same lane
+// layout and order, so both give the same bits.
+//
+// LDS: per group of 8 rows, four 1 KB runs [k buffer 0][k buffer 1][v buffer 0][v buffer 1],
+// so a row's k and v in either buffer sit at fixed distances from its k in buffer 0 (the
+// reads take them as immediate offsets; the member loop is unrolled by two for the buffer).
+// Wave w takes targets t0 + w + 4 r of the tile and staging instructions w + 4 r over the k
+// groups, then the v groups.  One barrier per member: after it the next member's rows have
+// landed (every wave waited for its own loads) and no wave still reads the buffer that the
+// next member's loads overwrite.
+__device__ __forceinline__ uint32_t lds_addr(const void* ptr) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)ptr;
+}
+// address = base (uniform) + voff (per lane); LDS destination M0 + 16 l.  Inline assembly: the
+// compiler's own direct-to-LDS builtin makes it wait for these loads before every LDS read of
+// the other buffer.  M0 is declared clobbered; the compiler sets it again before its own uses.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Three slots' score partials (K 17..24, the model's 24) as one block of dot products: the
+// three chains interleaved, each from a literal 0 addend, accumulating through their own
+// addend (no wait between them), then the three wait states a dot product's result needs
+// before another VALU instruction reads it.  The builtin form moves 0 into each accumulator
+// first.  Same products and order as score_dot.
+__device__ __forceinline__ void score_dot3(const uint32_t (&q)[3][4], const uint4 (&k)[3], float (&a)[3]) {
+    asm("v_dot2_f32_bf16 %0, %3, %15, 0\n\t"
+        "v_dot2_f32_bf16 %1, %7, %19, 0\n\t"
+        "v_dot2_f32_bf16 %2, %11, %23, 0\n\t"
+        "v_dot2_f32_bf16 %0, %4, %16, %0\n\t"
+        "v_dot2_f32_bf16 %1, %8, %20, %1\n\t"
+        "v_dot2_f32_bf16 %2, %12, %24, %2\n\t"
+        "v_dot2_f32_bf16 %0, %5, %17, %0\n\t"
+        "v_dot2_f32_bf16 %1, %9, %21, %1\n\t"
+        "v_dot2_f32_bf16 %2, %13, %25, %2\n\t"
+        "v_dot2_f32_bf16 %0, %6, %18, %0\n\t"
+        "v_dot2_f32_bf16 %1, %10, %22, %1\n\t"
+        "v_dot2_f32_bf16 %2, %14, %26, %2\n\t"
+        "s_nop 2"
+        : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2])
+        : "v"(q[0][0]), "v"(q[0][1]), "v"(q[0][2]), "v"(q[0][3]), "v"(q[1][0]), "v"(q[1][1]), "v"(q[1][2]),
+          "v"(q[1][3]), "v"(q[2][0]), "v"(q[2][1]), "v"(q[2][2]), "v"(q[2][3]), "v"(k[0].x), "v"(k[0].y),
+          "v"(k[0].z), "v"(k[0].w), "v"(k[1].x), "v"(k[1].y), "v"(k[1].z), "v"(k[1].w), "v"(k[2].x), "v"(k[2].y),
+          "v"(k[2].z), "v"(k[2].w));
+}
+// Three slots' weighted sum as one block: acc[2e] = sum_i (w_i, 0) . v_i[e], acc[2e + 1] =
+// sum_i (0, w_i) . v_i[e], slot by slot from a literal 0 addend (the order of
+// weighted_sum_fp32), then the three wait states.
+__device__ __forceinline__ void weighted_sum3(const uint32_t (&wl)[3], const uint32_t (&wh)[3], const uint4 (&v)[3],
+                                              float (&acc)[8]) {
+#define MOSAIC_PV_FIRST(W0, W1, X, Y, Z, T)        \
+    "v_dot2_f32_bf16 %0, " W0 ", " X ", 0\n\t"   \
+    "v_dot2_f32_bf16 %1, " W1 ", " X ", 0\n\t"   \
+    "v_dot2_f32_bf16 %2, " W0 ", " Y ", 0\n\t"   \
+    "v_dot2_f32_bf16 %3, " W1 ", " Y ", 0\n\t"   \
+    "v_dot2_f32_bf16 %4, " W0 ", " Z ", 0\n\t"   \
+    "v_dot2_f32_bf16 %5, " W1 ", " Z ", 0\n\t"   \
+    "v_dot2_f32_bf16 %6, " W0 ", " T ", 0\n\t"   \
+    "v_dot2_f32_bf16 %7, " W1 ", " T ", 0\n\t"
+#define MOSAIC_PV_NEXT(W0, W1, X, Y, Z, T)         \
+    "v_dot2_f32_bf16 %0, " W0 ", " X ", %0\n\t"  \
+    "v_dot2_f32_bf16 %1, " W1 ", " X ", %1\n\t"  \
+    "v_dot2_f32_bf16 %2, " W0 ", " Y ", %2\n\t"  \
+    "v_dot2_f32_bf16 %3, " W1 ", " Y ", %3\n\t"  \
+    "v_dot2_f32_bf16 %4, " W0 ", " Z ", %4\n\t"  \
+    "v_dot2_f32_bf16 %5, " W1 ", " Z ", %5\n\t"  \
+    "v_dot2_f32_bf16 %6, " W0 ", " T ", %6\n\t"  \
+    "v_dot2_f32_bf16 %7, " W1 ", " T ", %7\n\t"
+    asm(MOSAIC_PV_FIRST("%8", "%9", "%14", "%15", "%16", "%17")
+        MOSAIC_PV_NEXT("%10", "%11", "%18", "%19", "%20", "%21")
+        MOSAIC_PV_NEXT("%12", "%13", "%22", "%23", "%24", "%25")
+        "s_nop 2"
+        : "=&v"(acc[0]), "=&v"(acc[1]), "=&v"(acc[2]), "=&v"(acc[3]), "=&v"(acc[4]), "=&v"(acc[5]), "=&v"(acc[6]),
+          "=&v"(acc[7])
+        : "v"(wl[0]), "v"(wh[0]), "v"(wl[1]), "v"(wh[1]), "v"(wl[2]), "v"(wh[2]), "v"(v[0].x), "v"(v[0].y),
+          "v"(v[0].z), "v"(v[0].w), "v"(v[1].x), "v"(v[1].y), "v"(v[1].z), "v"(v[1].w), "v"(v[2].x), "v"(v[2].y),
+          "v"(v[2].z), "v"(v[2].w));
+#undef MOSAIC_PV_FIRST
+#undef MOSAIC_PV_NEXT
+}
+
+constexpr int kTileWaveTargets = kKnnTileTargets / kInterpWaves;     // 4
+constexpr int kTileWaveLoads = 2 * kKnnTileRows / 8 / kInterpWaves;  // 8 staging instructions per wave at most
+
+template <int NSLOT, bool POW2>
+__global__ __launch_bounds__(kInterpWaves * 64) void knn_tile_kernel(InterpParams p, KnnTiles tl) {
+    extern __shared__ __attribute__((aligned(16))) uint4 kv_lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int pair = xcd_remap(blockIdx.x, gridDim.x);
+    const int tile = pair / p.H, h = pair - tile * p.H;
+    const int K = p.K, dc = lane & 7, jg = lane >> 3;
+    const int rows = tl.rows;
+    // the tables are clamped into range (memory safety; a malformed table gives wrong rows)
+    const int t0 = __builtin_amdgcn_readfirstlane(min(max(tl.start[tile], 0), p.S_to));
+    const int t1 = __builtin_amdgcn_readfirstlane(min(max(tl.start[tile + 1], t0), min(t0 + kKnnTileTargets, p.S_to)));
+    const int nsrc = __builtin_amdgcn_readfirstlane(min(max(tl.nsrc[tile], 1), rows));
+    const int ng = (nsrc + 7) >> 3;  // 8-row groups per tensor
+
+    // staging offsets: instruction r of this wave loads group gi = wave + 4 r (k groups, then v)
+    uint32_t soff[kTileWaveLoads];
+#pragma unroll
+    for (int r = 0; r < kTileWaveLoads; ++r) {
+        const int gi = wave + kInterpWaves * r;
+        const bool isv = gi >= ng;
+        const int row = 8 * (isv ? gi - ng : gi) + (lane >> 3);
+        const int n = min(max(tl.src[(int64_t)tile * rows + min(row, nsrc - 1)], 0), p.S_from - 1);
+        soff[r] = isv ? (uint32_t)(2 * (n * p.v_sn + (int64_t)h * p.v_sh + 8 * dc))
+                      : (uint32_t)(2 * (n * p.k_sn + (int64_t)h * p.k_sh + 8 * dc));
+    }
+    const uint32_t lds0 = lds_addr(kv_lds);
+    auto stage = [&](int b, int buf) __attribute__((always_inline)) {
+        const char* kb = reinterpret_cast<const char*>(p.k + (int64_t)b * p.k_sb);
+        const char* vb = reinterpret_cast<const char*>(p.v + (int64_t)b * p.v_sb);
+#pragma unroll
+        for (int r = 0; r < kTileWaveLoads; ++r) {
+            const int gi = wave + kInterpWaves * r;
+            if (gi >= 2 * ng) break;  // uniform
+            const bool isv = gi >= ng;
+            const uint32_t dst = lds0 + (uint32_t)(4 * (isv ? gi - ng : gi) + 2 * isv + buf) * 1024u;
+            if (isv) dma16(vb, soff[r], __builtin_amdgcn_readfirstlane(dst));
+            else dma16(kb, soff[r], __builtin_amdgcn_readfirstlane(dst));
+        }
+    };
+
+    // to_q rows h*64 + 8 dc .. + 7
+    float wq[24];
+    {
+        const bf16_t* wr = p.w_q + ((int64_t)h * 64 + 8 * dc) * 3;
+        float t[8];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            unpack8(ld16(wr + 8 * c), t);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wq[8 * c + e] = t[e];
+        }
+    }
+    // per target of this wave: its index, its slots' k rows in buffer 0 (LDS byte offsets) and
+    // its query pairs
+    int tgt[kTileWaveTargets];
+    uint32_t koff[kTileWaveTargets][NSLOT];
+    uint32_t qp[kTileWaveTargets][NSLOT][4];
+#pragma unroll
+    for (int r = 0; r < kTileWaveTargets; ++r) {
+        const int pos = min(t0 + wave + kInterpWaves * r, p.S_to - 1);
+        const int s = p.target_order ? min(max(p.target_order[pos], 0), p.S_to - 1) : pos;
+        tgt[r] = s;
+#pragma unroll
+        for (int i = 0; i < NSLOT; ++i) {
+            const int j = min(jg + 8 * i, K - 1);
+            const int sl = min(max(tl.slot[(int64_t)pos * K + j], 0), rows - 1);
+            koff[r][i] = lds0 + (uint32_t)(4096 * (sl >> 3) + 128 * (sl & 7) + 16 * dc);
+            const int64_t sj = (int64_t)s * K + j;
+            const float r0 = round_bf16(p.rel_pos[3 * sj]), r1 = round_bf16(p.rel_pos[3 * sj + 1]),
+                        r2 = round_bf16(p.rel_pos[3 * sj + 2]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t bits = __float_as_uint(round_bf16(fmaf(r2, wq[3 * e + 2], fmaf(r1, wq[3 * e + 1], r0 * wq[3 * e]))));
+                if (e & 1) qp[r][i][e >> 1] |= bits;
+                else qp[r][i][e >> 1] = bits >> 16;
+            }
+        }
+    }
+    const int dout = 8 * dc + 4 * (lane >> 5) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1);
+
+    // member b from buffer BUF (member b + 1 staged into the other one meanwhile)
+    auto member = [&](int b, auto BUF) __attribute__((always_inline)) {
+        constexpr int buf = decltype(BUF)::value;
+        if (b + 1 < p.B) stage(b + 1, buf ^ 1);
+        const char* lds = reinterpret_cast<const char*>(kv_lds) - lds0;  // koff holds absolute LDS addresses
+#pragma unroll
+        for (int r = 0; r < kTileWaveTargets; ++r) {
+            if (t0 + wave + kInterpWaves * r >= t1) break;  // uniform
+            uint4 kw[NSLOT], vw[NSLOT];
+#pragma unroll
+            for (int i = 0; i < NSLOT; ++i) {
+                kw[i] = *reinterpret_cast<const uint4*>(lds + koff[r][i] + 1024 * buf);
+                vw[i] = *reinterpret_cast<const uint4*>(lds + koff[r][i] + 2048 + 1024 * buf);
+            }
+            float part[NSLOT], sc[NSLOT], m;
+            if constexpr (NSLOT == 3) {
+                score_dot3(qp[r], kw, part);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NSLOT; ++i) part[i] = score_dot(qp[r][i], kw[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < NSLOT; ++i) {
+                sc[i] = i < NSLOT - 1 || jg + 8 * i < K ? scaled_score<POW2>(chunk_sum(part[i]), p) : -INFINITY;
+                m = i == 0 ? sc[0] : fmaxf(m, sc[i]);
+            }
+            float wt[NSLOT], acc[8];
+            softmax_weights(sc, m, wt);
+            if constexpr (NSLOT == 3) {
+                uint32_t wl[3], wh[3];
+#pragma unroll
+                for (int i = 0; i < 3; ++i) { wl[i] = pack_bf16x2(wt[i], 0.f); wh[i] = pack_bf16x2(0.f, wt[i]); }
+                weighted_sum3(wl, wh, vw, acc);
+            } else {
+                weighted_sum_fp32(wt, vw, acc);
+            }
+            const float o = reduce_scatter(acc, lane);
+            p.out[(((int64_t)tgt[r] * p.B + b) * p.H + h) * 64 + dout] = (bf16_t)(pack_bf16x2(o, 0.f) & 0xffffu);
+        }
+        wait_vmem();
+        __syncthreads();
+    };
+
+    stage(0, 0);
+    wait_vmem();
+    __syncthreads();
+    for (int b = 0; b < p.B; b += 2) {
+        member(b, std::integral_constant<int, 0>{});
+        if (b + 1 < p.B) member(b + 1, std::integral_constant<int, 1>{});
+    }
+}
+
 template <int NSLOT, bool RP>
 const void* pick(bool off32, bool pow2) {
     return off32 ? (pow2 ? (const void*)&knn_attn_kernel<NSLOT, true, true, RP> : (const void*)&knn_attn_kernel<NSLOT, true, false, RP>)
                  : (pow2 ? (const void*)&knn_attn_kernel<NSLOT, false, true, RP> : (const void*)&knn_attn_kernel<NSLOT, false, false, RP>);
 }
 
-template <int NSLOT>
-hipError_t launch_slots(const InterpParams& p, unsigned wgs, hipStream_t s) {
-    void* args[] = {const_cast<InterpParams*>(&p)};
+bool knn_off32(const InterpParams& p) {
     // 32-bit chunk offsets when every chunk of a member lies within 4 GiB of its start
     const int64_t kmax = (int64_t)(p.S_from - 1) * p.k_sn + (int64_t)(p.H - 1) * p.k_sh + 64;
     const int64_t vmax = (int64_t)(p.S_from - 1) * p.v_sn + (int64_t)(p.H - 1) * p.v_sh + 64;
-    const bool off32 = p.k_sn >= 0 && p.k_sh >= 0 && p.v_sn >= 0 && p.v_sh >= 0 &&
-                       2 * kmax <= 0xffffffffLL && 2 * vmax <= 0xffffffffLL;
+    return p.k_sn >= 0 && p.k_sh >= 0 && p.v_sn >= 0 && p.v_sh >= 0 && 2 * kmax <= 0xffffffffLL &&
+           2 * vmax <= 0xffffffffLL;
+}
+
+template <int NSLOT>
+hipError_t launch_slots(const InterpParams& p, unsigned wgs, hipStream_t s) {
+    void* args[] = {const_cast<InterpParams*>(&p)};
+    const bool off32 = knn_off32(p);
     const void* fn = p.round_products ? pick<NSLOT, true>(off32, p.scale_pow2) : pick<NSLOT, false>(off32, p.scale_pow2);
     return hipLaunchKernel(fn, dim3(wgs), dim3(kInterpWaves * 64), args, 0, s);
 }
@@ -457,6 +744,28 @@ hipError_t launch_knn_attn(const InterpParams& p, hipStream_t s) {
         case 4: return launch_slots<4>(p, (unsigned)wgs, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+// The LDS-staged form: fp32 products with 32-bit chunk offsets only (the caller falls back to
+// launch_knn_attn otherwise).
+bool knn_tiled_supported(const InterpParams& p) { return !p.round_products && knn_off32(p); }
+
+hipError_t launch_knn_attn_tiled(const InterpParams& p, const KnnTiles& t, hipStream_t s) {
+    if (!knn_tiled_supported(p) || t.rows <= 0 || t.rows % 8 || t.rows > kKnnTileRows) return hipErrorInvalidValue;
+    const int64_t wgs = (int64_t)t.n * p.H;
+    if (wgs <= 0) return hipSuccess;
+    if (wgs > 0x7fffffff) return hipErrorInvalidValue;
+    void* args[] = {const_cast<InterpParams*>(&p), const_cast<KnnTiles*>(&t)};
+    const void* fn = nullptr;
+    switch ((p.K + 7) / 8) {
+        case 1: fn = p.scale_pow2 ? (const void*)&knn_tile_kernel<1, true> : (const void*)&knn_tile_kernel<1, false>; break;
+        case 2: fn = p.scale_pow2 ? (const void*)&knn_tile_kernel<2, true> : (const void*)&knn_tile_kernel<2, false>; break;
+        case 3: fn = p.scale_pow2 ? (const void*)&knn_tile_kernel<3, true> : (const void*)&knn_tile_kernel<3, false>; break;
+        case 4: fn = p.scale_pow2 ? (const void*)&knn_tile_kernel<4, true> : (const void*)&knn_tile_kernel<4, false>; break;
+        default: return hipErrorInvalidValue;
+    }
+    const size_t lds = 4u * (size_t)t.rows * 128u;  // per 8-row group: k and v, two buffers each
+    return hipLaunchKernel(fn, dim3((unsigned)wgs), dim3(kInterpWaves * 64), args, lds, s);
 }
 
 }  // namespace mosaic

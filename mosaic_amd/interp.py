@@ -55,6 +55,52 @@ def spatial_order(pos_rad: torch.Tensor, bits: int = 10) -> torch.Tensor:
     return torch.from_numpy(np.argsort(code, kind="stable"))
 
 
+def knn_tiles(neighbors: torch.Tensor, order: torch.Tensor, max_targets: int = 16,
+              max_rows: int | None = None) -> dict:
+    """Tiles of consecutive targets of ``order`` for the LDS-staged k-NN kernel: each tile takes
+    as many targets (at most ``max_targets``, 16 at most) as keep its distinct source points
+    within ``max_rows`` (a multiple of 8, 128 at most).  Returns int32 CPU tensors ``start``
+    [n + 1] (order positions), ``src`` [n, max_rows] (the distinct source points, ascending,
+    padded with the last), ``nsrc`` [n] and ``slot`` [S_to, K] (the row of ``src`` holding
+    neighbour j of the target at order position pos), and ``max_rows``.
+
+    ``max_rows=None`` takes the smallest of 64, 96 and 128 whose tiles hold 12 targets or more
+    on average: the staging buffers are 512 bytes per row, so fewer rows keep more workgroups
+    on a compute unit, while fuller tiles stage each source row for more targets (on the
+    model's grids: 64 for lat-lon -> HEALPix, 96 for HEALPix -> lat-lon)."""
+    if max_rows is None:
+        for rows in (64, 96, 128):
+            t = knn_tiles(neighbors, order, max_targets, rows)
+            if rows == 128 or len(order) >= 12 * (t["start"].numel() - 1):
+                return t
+    if not (0 < max_targets <= 16) or max_rows <= 0 or max_rows % 8 or max_rows > 128:
+        raise ValueError("max_targets must be in 1..16 and max_rows a multiple of 8 in 8..128")
+    nb = neighbors.detach().cpu().long().numpy()
+    S_to, K = nb.shape
+    if K > max_rows:
+        raise ValueError(f"{K} neighbours do not fit tiles of {max_rows} rows")
+    nb = nb[order.detach().cpu().long().numpy()]
+    starts, srcs, nsrc = [0], [], []
+    slot = np.empty((S_to, K), dtype=np.int32)
+    pos = 0
+    while pos < S_to:
+        cand = nb[pos:pos + max_targets]
+        _, first = np.unique(cand.ravel(), return_index=True)
+        grown = np.cumsum(np.bincount(first // K, minlength=len(cand)))
+        m = int(np.searchsorted(grown, max_rows, side="right"))   # targets whose union fits
+        uniq, inv = np.unique(cand[:m].ravel(), return_inverse=True)
+        slot[pos:pos + m] = inv.reshape(m, K)
+        row = np.full(max_rows, uniq[-1], dtype=np.int64)
+        row[:len(uniq)] = uniq
+        srcs.append(row)
+        nsrc.append(len(uniq))
+        pos += m
+        starts.append(pos)
+    as32 = lambda a: torch.from_numpy(np.ascontiguousarray(np.asarray(a), dtype=np.int32))
+    return {"start": as32(starts), "src": as32(np.stack(srcs)), "nsrc": as32(nsrc), "slot": as32(slot),
+            "max_rows": max_rows}
+
+
 def _snhd(t: torch.Tensor) -> _lib.Bnhd:
     # [S, B, H, 64] -> the ABI's (stride_b = member, stride_n = point, stride_h = head)
     return _lib.Bnhd(t.data_ptr(), t.stride(1), t.stride(0), t.stride(2))
@@ -62,7 +108,8 @@ def _snhd(t: torch.Tensor) -> _lib.Bnhd:
 
 def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel_pos: torch.Tensor,
                   w_q: torch.Tensor, scale: float | None = None,
-                  target_order: torch.Tensor | None = None, round_products: bool = False) -> torch.Tensor:
+                  target_order: torch.Tensor | None = None, round_products: bool = False,
+                  tiles: dict | None = None) -> torch.Tensor:
     """The gather-attention of CrossAttentionInterpolate.forward (primitives.py:265-283).
 
     k, v: [S_from, B, H, 64] (views of the kv projection are fine); neighbors: [S_to, K]
@@ -72,7 +119,9 @@ def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel
     e.g. ``spatial_order`` of the target positions) changes only the order the targets are
     computed in, not the result.  ``round_products`` rounds every product of the two weighted
     sums to bf16 before it is added (the reference's eager elementwise ops); by default the
-    products are exact and summed in fp32 (its compiled path).
+    products are exact and summed in fp32 (its compiled path).  ``tiles`` (``knn_tiles`` of
+    the neighbours and ``target_order``, on k's device) selects the LDS-staged kernel for the
+    fp32 form: the same output bit for bit.
     """
     forward_only("knn_attention", k, v, rel_pos, w_q)
     if k.dim() != 4 or k.shape != v.shape or k.shape[-1] != 64:
@@ -103,8 +152,17 @@ def knn_attention(k: torch.Tensor, v: torch.Tensor, neighbors: torch.Tensor, rel
         order = target_order.to(device=k.device, dtype=torch.int32).contiguous()
     out = torch.empty(S_to, B, H, d, dtype=torch.bfloat16, device=k.device)
     flags = _lib.KNN_ROUND_PRODUCTS if round_products else 0
+    tl = None
+    if tiles is not None:
+        if order is None:
+            raise ValueError("tiles are built over a target order: pass target_order as well")
+        parts = [tiles[n].to(device=k.device, dtype=torch.int32).contiguous() for n in ("start", "src", "nsrc", "slot")]
+        if tuple(parts[3].shape) != (S_to, K):
+            raise ValueError(f"tiles['slot'] must be [S_to, K] = [{S_to}, {K}], got {tuple(parts[3].shape)}")
+        tl = _lib.KnnTiles(*(t.data_ptr() for t in parts), parts[0].numel() - 1, int(tiles["max_rows"]))
     st = _lib.lib().mosaic_knn_interp_fwd_ex(_snhd(k), _snhd(v), nb.data_ptr(), rp.data_ptr(), wq.data_ptr(),
                                              None if order is None else order.data_ptr(),
+                                             None if tl is None else ctypes.byref(tl),
                                              S_from, S_to, B, H, d, K, 0.0 if scale is None else float(scale),
                                              flags, out.data_ptr(), stream_of(k))
     _lib.check(st, "mosaic_knn_interp_fwd_ex")
@@ -139,6 +197,10 @@ class CrossAttentionInterpolate(nn.Module):
         # the kernel's target order (int32, not part of the state dict): derived from the
         # target positions with the neighbours
         self.register_buffer("target_order", None, persistent=False)
+        # tiles of targets for the LDS-staged kernel (int32, derived with the order)
+        self.knn_tile_rows = 64
+        for n in ("start", "src", "nsrc", "slot"):
+            self.register_buffer("knn_tile_" + n, None, persistent=False)
 
     @torch.no_grad()
     def initialize_interpolation_scheme(self, pos_from_rad: torch.Tensor, pos_to_rad: torch.Tensor):
@@ -149,7 +211,12 @@ class CrossAttentionInterpolate(nn.Module):
         rel = (to_xyz.unsqueeze(1) - from_xyz[neighbors]).contiguous()
         self.neighbors = neighbors
         self.rel_pos = torch.nn.functional.normalize(rel, dim=-1).contiguous()
-        self.target_order = spatial_order(pos_to_rad).to(device=pos_from_rad.device, dtype=torch.int32)
+        order = spatial_order(pos_to_rad)
+        self.target_order = order.to(device=pos_from_rad.device, dtype=torch.int32)
+        tiles = knn_tiles(neighbors, order)
+        for n in ("start", "src", "nsrc", "slot"):
+            setattr(self, "knn_tile_" + n, tiles[n].to(pos_from_rad.device))
+        self.knn_tile_rows = tiles["max_rows"]
 
     def forward(self, x_from: torch.Tensor) -> torch.Tensor:
         if self.neighbors is None or self.rel_pos is None:
@@ -158,6 +225,10 @@ class CrossAttentionInterpolate(nn.Module):
         kv = self.to_kv(self.kv_norm(x_from))
         k = kv[..., :dim].unflatten(-1, (self.num_heads, self.head_dim))
         v = kv[..., dim:].unflatten(-1, (self.num_heads, self.head_dim))
+        tiles = None
+        if self.knn_tile_start is not None:
+            tiles = {"start": self.knn_tile_start, "src": self.knn_tile_src, "nsrc": self.knn_tile_nsrc,
+                     "slot": self.knn_tile_slot, "max_rows": self.knn_tile_rows}
         out = knn_attention(k, v, self.neighbors, self.rel_pos, self.to_q.weight, self.scale, self.target_order,
-                            round_products=self.round_products)
+                            round_products=self.round_products, tiles=tiles)
         return self.to_o(out.to(x_from.dtype).flatten(-2))

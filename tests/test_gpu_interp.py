@@ -231,7 +231,7 @@ def test_knn_attention_negative_point_stride_equals_forward_order(round_products
     out = torch.empty_like(fwd)
     flags = _lib.KNN_ROUND_PRODUCTS if round_products else 0
     st = _lib.lib().mosaic_knn_interp_fwd_ex(reversed_view(kr), reversed_view(vr), nb32.data_ptr(),
-                                             rel_d.float().contiguous().data_ptr(), w_q.data_ptr(), None,
+                                             rel_d.float().contiguous().data_ptr(), w_q.data_ptr(), None, None,
                                              S, len(ll), B, H, 64, 24, 0.125, flags, out.data_ptr(),
                                              torch.cuda.current_stream().cuda_stream)
     _lib.check(st, "mosaic_knn_interp_fwd_ex")
@@ -278,5 +278,91 @@ def test_knn_attention_legacy_entry_points_round_products():
     torch.cuda.synchronize()
     assert torch.equal(out, want)
     st = _lib.lib().mosaic_knn_interp_fwd_ex(kv[0], kv[1], nb32.data_ptr(), rel32.data_ptr(), w_q.data_ptr(), None,
-                                             S, len(hp), B, H, 64, 24, 0.125, 2, out.data_ptr(), stream)
+                                             None, S, len(hp), B, H, 64, 24, 0.125, 2, out.data_ptr(), stream)
     assert st == _lib.ERR_MODE
+
+
+def tiles_on(nb, order, max_targets=16, max_rows=None):
+    from mosaic_amd.interp import knn_tiles
+    t = knn_tiles(nb, order, max_targets, max_rows)
+    return {n: (x.to(DEV) if torch.is_tensor(x) else x) for n, x in t.items()}
+
+
+@pytest.mark.parametrize("max_targets,max_rows", [(16, 64), (16, 128), (5, 32), (1, 32)])
+@pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
+@pytest.mark.parametrize("K", [32, 24, 20, 13, 7, 1])
+def test_knn_attention_tiled_equals_direct(direction, K, max_targets, max_rows):
+    """The LDS-staged kernel (tiles of targets sharing staged source rows) against the
+    per-target kernel in the fp32-product form: the same output bit for bit, at any tile
+    limits, K (one to four neighbour slots per lane) and direction."""
+    if K > max_rows:
+        pytest.skip("tiles hold at least K rows")
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    src, dst = (ll, hp) if direction == "ll_to_hp" else (hp, ll)
+    nb, rel = scheme(src, dst, K)
+    B, H = 3, 2
+    k, v = rand(len(src), B, H, 64, seed=K + 300), rand(len(src), B, H, 64, seed=K + 400)
+    w_q = rand(H * 64, 3, seed=K + 500, scale=2.0)
+    order = spatial_order(dst)
+    args = (k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
+    direct = knn_attention(*args, target_order=order.to(DEV))
+    tiled = knn_attention(*args, target_order=order.to(DEV), tiles=tiles_on(nb, order, max_targets, max_rows))
+    torch.cuda.synchronize()
+    assert torch.equal(tiled, direct)
+    close(tiled, oracle(k, v, nb, rel, w_q, 0.125, False))
+
+
+@pytest.mark.parametrize("scale", [0.125, 0.3])
+def test_knn_attention_tiled_random_lists_and_members(scale):
+    """Neighbour lists without spatial structure (repeats allowed: a tile's source list holds
+    each once), K 24, an odd member count (the member loop runs two members per pass) and a
+    scale that is not a power of two."""
+    S_from, S_to, K = 3000, 200, 24
+    g = torch.Generator().manual_seed(80)
+    nb = torch.randint(0, S_from, (S_to, K), generator=g)
+    rel = torch.nn.functional.normalize(torch.randn(S_to, K, 3, generator=g), dim=-1)
+    for B in (1, 5):
+        k, v = rand(S_from, B, 3, 64, seed=81), rand(S_from, B, 3, 64, seed=82)
+        w_q = rand(3 * 64, 3, seed=83)
+        order = torch.randperm(S_to, generator=g)
+        args = (k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), scale)
+        direct = knn_attention(*args, target_order=order.to(DEV))
+        tiled = knn_attention(*args, target_order=order.to(DEV), tiles=tiles_on(nb, order, 16, 128))
+        assert torch.equal(tiled, direct)
+        close(tiled, oracle(k, v, nb, rel, w_q, scale, False))
+
+
+@pytest.mark.parametrize("direction", ["ll_to_hp", "hp_to_ll"])
+def test_knn_attention_tiled_full_size(direction):
+    """Model grids (121 x 240 lat-lon, HEALPix nside 64), K 24, 12 heads, 2 members, the
+    module's tiles: equal to the per-target kernel everywhere, sampled targets against the
+    oracle."""
+    ll, hp = lonlat_grid(240, 121), torch.deg2rad(get_healpix_grid(64))
+    src, dst = (ll, hp) if direction == "ll_to_hp" else (hp, ll)
+    K, B, H = 24, 2, 12
+    nb, rel = scheme(src, dst, K)
+    k, v = rand(len(src), B, H, 64, seed=90), rand(len(src), B, H, 64, seed=91)
+    w_q = rand(H * 64, 3, seed=92)
+    order = spatial_order(dst)
+    args = (k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
+    direct = knn_attention(*args, target_order=order.to(DEV))
+    tiled = knn_attention(*args, target_order=order.to(DEV), tiles=tiles_on(nb, order))
+    torch.cuda.synchronize()
+    assert torch.equal(tiled, direct)
+    g = torch.Generator().manual_seed(93)
+    sample = torch.randint(0, len(dst), (512,), generator=g)
+    close(tiled.cpu()[sample], oracle(k, v, nb[sample], rel[sample], w_q, 0.125, False))
+
+
+def test_knn_attention_tiles_argument_checks():
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(ll, hp, 24)
+    k = rand(len(ll), 1, 2, 64, seed=95).to(DEV)
+    w_q = rand(2 * 64, 3, seed=96).to(DEV)
+    order = spatial_order(hp)
+    tiles = tiles_on(nb, order)
+    with pytest.raises(ValueError, match="target_order"):
+        knn_attention(k, k, nb.to(DEV), rel.to(DEV), w_q, 0.125, tiles=tiles)
+    bad = dict(tiles, max_rows=60)
+    with pytest.raises(RuntimeError):
+        knn_attention(k, k, nb.to(DEV), rel.to(DEV), w_q, 0.125, target_order=order.to(DEV), tiles=bad)

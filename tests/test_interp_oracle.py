@@ -179,3 +179,39 @@ def test_spatial_order_is_a_permutation_that_follows_the_sphere():
     assert step(o) < 2.5 * spacing and step(torch.arange(len(pts))) > 10 * spacing
     same = torch.zeros(5, 2)
     assert spatial_order(same).tolist() == [0, 1, 2, 3, 4]
+
+
+@pytest.mark.parametrize("max_targets,max_rows", [(16, 64), (16, 128), (5, 32), (1, 32)])
+def test_knn_tiles_partition_the_order(max_targets, max_rows):
+    """knn_tiles: consecutive runs of the order, each within max_targets targets and max_rows
+    distinct sources, taken greedily (the next target would break a limit), and every
+    neighbour found at its slot of its tile's source list."""
+    from mosaic_amd.interp import knn_tiles, spatial_order
+    ll, hp = _grids()
+    K = 20
+    nb, _ = _scheme(ll, hp, K)
+    order = spatial_order(hp)
+    t = knn_tiles(nb, order, max_targets, max_rows)
+    start, src, nsrc, slot = (t[n].long() for n in ("start", "src", "nsrc", "slot"))
+    assert start[0] == 0 and start[-1] == len(hp) and bool((start[1:] > start[:-1]).all())
+    assert src.shape == (len(start) - 1, max_rows) and slot.shape == (len(hp), K)
+    nb_ord = nb[order]
+    for i in range(len(start) - 1):
+        a, b = start[i].item(), start[i + 1].item()
+        n = nsrc[i].item()
+        assert b - a <= max_targets and 0 < n <= max_rows
+        uniq = torch.unique(nb_ord[a:b])
+        assert torch.equal(src[i, :n], uniq)                       # ascending distinct sources
+        assert torch.equal(src[i, n:], uniq[-1].expand(max_rows - n))
+        assert torch.equal(src[i][slot[a:b]], nb_ord[a:b])          # every neighbour at its slot
+        if b < len(hp) and b - a < max_targets:                     # greedy: the next target did not fit
+            assert len(torch.unique(nb_ord[a:b + 1])) > max_rows
+
+
+def test_knn_tiles_reject_bad_limits():
+    from mosaic_amd.interp import knn_tiles
+    nb = torch.zeros(4, 24, dtype=torch.long)
+    order = torch.arange(4)
+    for mt, mr in ((0, 64), (17, 64), (16, 60), (16, 136), (16, 16)):
+        with pytest.raises(ValueError):
+            knn_tiles(nb, order, mt, mr)
