@@ -15,6 +15,7 @@ elementwise ops do.
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import numpy as np
 import torch
@@ -197,8 +198,12 @@ class CrossAttentionInterpolate(nn.Module):
         # the kernel's target order (int32, not part of the state dict): derived from the
         # target positions with the neighbours
         self.register_buffer("target_order", None, persistent=False)
-        # tiles of targets for the LDS-staged kernel (int32, derived with the order)
+        # tiles of targets for the LDS-staged kernel (int32, derived from the neighbours and
+        # the order); _tile_source identifies the neighbours tensor they were built from (a weak
+        # reference and its in-place version counter), so a later change of it (a new tensor,
+        # or load_state_dict copying into the buffer) rebuilds them
         self.knn_tile_rows = 64
+        self._tile_source = None
         for n in ("start", "src", "nsrc", "slot"):
             self.register_buffer("knn_tile_" + n, None, persistent=False)
 
@@ -213,10 +218,27 @@ class CrossAttentionInterpolate(nn.Module):
         self.rel_pos = torch.nn.functional.normalize(rel, dim=-1).contiguous()
         order = spatial_order(pos_to_rad)
         self.target_order = order.to(device=pos_from_rad.device, dtype=torch.int32)
-        tiles = knn_tiles(neighbors, order)
+        self._build_tiles()
+
+    @torch.no_grad()
+    def _build_tiles(self):
+        tiles = knn_tiles(self.neighbors, self.target_order)
         for n in ("start", "src", "nsrc", "slot"):
-            setattr(self, "knn_tile_" + n, tiles[n].to(pos_from_rad.device))
+            setattr(self, "knn_tile_" + n, tiles[n].to(self.neighbors.device))
         self.knn_tile_rows = tiles["max_rows"]
+        self._tile_source = (weakref.ref(self.neighbors), self.neighbors._version)
+
+    def _current_tiles(self):
+        """The tile tables for the current neighbours (rebuilt if the neighbours tensor was
+        replaced or modified in place since they were built), or None without an order."""
+        if self.target_order is None:
+            return None
+        src = self._tile_source
+        if self.knn_tile_start is None or src is None or src[0]() is not self.neighbors or \
+                src[1] != self.neighbors._version:
+            self._build_tiles()
+        return {"start": self.knn_tile_start, "src": self.knn_tile_src, "nsrc": self.knn_tile_nsrc,
+                "slot": self.knn_tile_slot, "max_rows": self.knn_tile_rows}
 
     def forward(self, x_from: torch.Tensor) -> torch.Tensor:
         if self.neighbors is None or self.rel_pos is None:
@@ -225,10 +247,7 @@ class CrossAttentionInterpolate(nn.Module):
         kv = self.to_kv(self.kv_norm(x_from))
         k = kv[..., :dim].unflatten(-1, (self.num_heads, self.head_dim))
         v = kv[..., dim:].unflatten(-1, (self.num_heads, self.head_dim))
-        tiles = None
-        if self.knn_tile_start is not None:
-            tiles = {"start": self.knn_tile_start, "src": self.knn_tile_src, "nsrc": self.knn_tile_nsrc,
-                     "slot": self.knn_tile_slot, "max_rows": self.knn_tile_rows}
+        tiles = self._current_tiles()
         out = knn_attention(k, v, self.neighbors, self.rel_pos, self.to_q.weight, self.scale, self.target_order,
                             round_products=self.round_products, tiles=tiles)
         return self.to_o(out.to(x_from.dtype).flatten(-2))

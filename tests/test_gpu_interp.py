@@ -366,3 +366,31 @@ def test_knn_attention_tiles_argument_checks():
     bad = dict(tiles, max_rows=60)
     with pytest.raises(RuntimeError):
         knn_attention(k, k, nb.to(DEV), rel.to(DEV), w_q, 0.125, target_order=order.to(DEV), tiles=bad)
+
+
+def test_module_rebuilds_tiles_when_neighbours_change():
+    """The module's tile tables follow its neighbours: after load_state_dict copies other
+    neighbour lists (and relative positions) into the buffers, the output equals the
+    per-target kernel on the new lists."""
+    from types import SimpleNamespace
+    cfg = SimpleNamespace(k_neighbors=16, dim=128, num_heads=2, rmsnorm_elementwise_affine=True)
+    torch.manual_seed(1)
+    m = CrossAttentionInterpolate(cfg)
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    m.initialize_interpolation_scheme(ll, hp)
+    m = m.to(DEV).to(torch.bfloat16)
+    x = torch.randn(len(ll), 2, 128, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        m(x)                                          # tiles built for the first lists
+        sd = m.state_dict()
+        g = torch.Generator().manual_seed(2)
+        sd["neighbors"] = torch.randint(0, len(ll), sd["neighbors"].shape, generator=g).to(DEV)
+        sd["rel_pos"] = torch.nn.functional.normalize(torch.randn(sd["rel_pos"].shape, generator=g), dim=-1).to(DEV)
+        m.load_state_dict(sd)
+        y = m(x)
+        kv = m.to_kv(m.kv_norm(x))
+        k = kv[..., :128].unflatten(-1, (2, 64))
+        v = kv[..., 128:].unflatten(-1, (2, 64))
+        att = knn_attention(k, v, m.neighbors, m.rel_pos, m.to_q.weight, m.scale)   # per-target kernel
+        ref = m.to_o(att.to(x.dtype).flatten(-2))
+    assert torch.equal(y, ref)
