@@ -511,11 +511,14 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t 
 #pragma clang diagnostic pop
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Three slots' score partials (K 17..24, the model's 24) as one block of dot products: the
-// three chains interleaved, each from a literal 0 addend, accumulating through their own
-// addend (no wait between them), then the three wait states a dot product's result needs
-// before another VALU instruction reads it.  The builtin form moves 0 into each accumulator
-// first.  Same products and order as score_dot.
+// Three slots' scores (K 17..24, the model's 24) as one block: the three dot-product chains
+// interleaved, each from a literal 0 addend, accumulating through their own addend (no wait
+// between them); the three wait states a dot product's result needs before another VALU
+// instruction reads it; then the sums over the 8 chunk lanes of each neighbour group as DPP
+// adds (lanes l ^ 1, l ^ 2, then the half-row mirror), the three slots interleaved so each
+// DPP read of a register comes at least two instructions after its write.  Same products,
+// order and sums as chunk_sum(score_dot(...)) (the builtin form moves 0 into each
+// accumulator first, and two of its three half-mirror adds compiled to a move and an add).
 __device__ __forceinline__ void score_dot3(const uint32_t (&q)[3][4], const uint4 (&k)[3], float (&a)[3]) {
     asm("v_dot2_f32_bf16 %0, %3, %15, 0\n\t"
         "v_dot2_f32_bf16 %1, %7, %19, 0\n\t"
@@ -529,7 +532,16 @@ __device__ __forceinline__ void score_dot3(const uint32_t (&q)[3][4], const uint
         "v_dot2_f32_bf16 %0, %6, %18, %0\n\t"
         "v_dot2_f32_bf16 %1, %10, %22, %1\n\t"
         "v_dot2_f32_bf16 %2, %14, %26, %2\n\t"
-        "s_nop 2"
+        "s_nop 2\n\t"
+        "v_add_f32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %2, %2, %2 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %2, %2, %2 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %1, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "v_add_f32_dpp %2, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
         : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2])
         : "v"(q[0][0]), "v"(q[0][1]), "v"(q[0][2]), "v"(q[0][3]), "v"(q[1][0]), "v"(q[1][1]), "v"(q[1][2]),
           "v"(q[1][3]), "v"(q[2][0]), "v"(q[2][1]), "v"(q[2][2]), "v"(q[2][3]), "v"(k[0].x), "v"(k[0].y),
@@ -636,7 +648,7 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_tile_kernel(InterpParam
 #pragma unroll
     for (int r = 0; r < kTileWaveTargets; ++r) {
         const int pos = min(t0 + wave + kInterpWaves * r, p.S_to - 1);
-        const int s = p.target_order ? min(max(p.target_order[pos], 0), p.S_to - 1) : pos;
+        const int s = __builtin_amdgcn_readfirstlane(p.target_order ? min(max(p.target_order[pos], 0), p.S_to - 1) : pos);
         tgt[r] = s;
 #pragma unroll
         for (int i = 0; i < NSLOT; ++i) {
@@ -679,7 +691,8 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_tile_kernel(InterpParam
             }
 #pragma unroll
             for (int i = 0; i < NSLOT; ++i) {
-                sc[i] = i < NSLOT - 1 || jg + 8 * i < K ? scaled_score<POW2>(chunk_sum(part[i]), p) : -INFINITY;
+                const float sum = NSLOT == 3 ? part[i] : chunk_sum(part[i]);  // score_dot3 sums the chunk lanes itself
+                sc[i] = i < NSLOT - 1 || jg + 8 * i < K ? scaled_score<POW2>(sum, p) : -INFINITY;
                 m = i == 0 ? sc[0] : fmaxf(m, sc[i]);
             }
             float wt[NSLOT], acc[8];
@@ -693,7 +706,8 @@ __global__ __launch_bounds__(kInterpWaves * 64) void knn_tile_kernel(InterpParam
                 weighted_sum_fp32(wt, vw, acc);
             }
             const float o = reduce_scatter(acc, lane);
-            p.out[(((int64_t)tgt[r] * p.B + b) * p.H + h) * 64 + dout] = (bf16_t)(pack_bf16x2(o, 0.f) & 0xffffu);
+            bf16_t* orow = p.out + (((int64_t)tgt[r] * p.B + b) * p.H + h) * 64;  // uniform
+            orow[dout] = (bf16_t)(pack_bf16x2(o, 0.f) & 0xffffu);
         }
         wait_vmem();
         __syncthreads();
