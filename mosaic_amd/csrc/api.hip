@@ -69,7 +69,7 @@ int choose_splits(int B, int nb, int Hk) {
 
 struct Layout {
     int nb = 0, nb_pad = 0, nsplit = 1;
-    size_t qc = 0, kfr = 0, vfr = 0, sbar = 0, idx = 0, kbnd = 0, opart = 0, ml = 0, ocmp = 0, total = 0;
+    size_t qc = 0, kfr = 0, vfr = 0, sbar = 0, idx = 0, kbnd = 0, opart = 0, ml = 0, ocmp = 0, tail = 0, total = 0;
 };
 
 bool uses_selection(int mode) { return mode == MOSAIC_BSA_FULL || mode == MOSAIC_BSA_NO_COMPRESSION; }
@@ -126,6 +126,7 @@ Layout layout_of(const mosaic_bsa_args* a) {
         L.sbar = off; off = align_up(off + B * Hk * nb * nbp * 2);
         L.idx = off; off = align_up(off + B * nb * Hk * K * 4);
         L.kbnd = off; off = align_up(off + B * nb * Hk * 8 * 4);
+        L.tail = off; off = align_up(off + 4);  // the attention kernel's dynamic-tail counter
     }
     L.total = off;
     return L;
@@ -142,12 +143,30 @@ AttnParams attn_params(const mosaic_bnhd& q, const mosaic_bnhd& k, const mosaic_
     p.head_groups = p.G / waves;
     p.qtiles = N / kTile;
     p.total_wgs = B * Hk * p.head_groups * p.qtiles;
+    p.n_static = p.total_wgs;  // no dynamic tail unless set_dynamic_tail
     p.scale = scale;
     p.scale_log2 = scale * kLog2e;
     return p;
 }
 
 int launch_status(hipError_t e) { return e == hipSuccess ? MOSAIC_OK : MOSAIC_ERR_LAUNCH; }
+
+// The attention kernel's dynamic tail (modes with a top-k pass, which zeroes the counter): the
+// last kTailItems items are taken by kTailItems + kTailExtra workgroups launched after the
+// static ones.  Launches of fewer than 4 * kTailItems items keep the static mapping.
+#ifndef MOSAIC_TAIL_ITEMS
+#define MOSAIC_TAIL_ITEMS 512
+#endif
+#ifndef MOSAIC_TAIL_EXTRA
+#define MOSAIC_TAIL_EXTRA 512
+#endif
+constexpr int kTailItems = MOSAIC_TAIL_ITEMS, kTailExtra = MOSAIC_TAIL_EXTRA;
+void set_dynamic_tail(AttnParams& p, int* ctr) {
+    if (kTailItems <= 0 || p.total_wgs < 4 * kTailItems) return;
+    p.tail_ctr = ctr;
+    p.n_static = p.total_wgs - kTailItems;
+    p.tail_wgs = kTailItems + kTailExtra;
+}
 
 // Device address of `scratch` on the current device, resolved once per device (each GPU holds
 // its own copy of the array at its own address) and cached.
@@ -300,6 +319,8 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
             tp.idx64 = a->block_indices_out;
             tp.B = B; tp.nb = L.nb; tp.nb_pad = L.nb_pad; tp.Hk = Hk; tp.K = a->sparse_block_count;
             tp.rows = B * Hk * L.nb;
+            tp.zero_ctr = reinterpret_cast<int*>(w + L.tail);
+            set_dynamic_tail(ap, tp.zero_ctr);
             if (run(MOSAIC_BSA_STAGE_TOPK))
                 if (int e = launch_status(launch_topk(tp, s))) return e;
             ap.idx = tp.idx32;

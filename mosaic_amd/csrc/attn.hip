@@ -336,7 +336,24 @@ void bsa_attn_kernel(AttnParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, r = lane & 31, hh = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int L = xcd_remap(blockIdx.x, p.total_wgs);
+    int L;
+    if ((int)blockIdx.x < p.n_static) {
+        L = xcd_remap(blockIdx.x, p.n_static);
+    } else {
+        // dynamic tail: the next unclaimed item, or none (the whole workgroup leaves before
+        // any other barrier); the last of the tail_wgs takers resets the counter for the next
+        // launch
+        __shared__ int claimed;
+        if (tid == 0) {
+            const int t = __hip_atomic_fetch_add(p.tail_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (t == p.tail_wgs - 1) __hip_atomic_store(p.tail_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            claimed = t;
+        }
+        __syncthreads();
+        const int t = claimed;
+        if (t >= p.total_wgs - p.n_static) return;
+        L = p.n_static + t;
+    }
     const int qtile = L % p.qtiles;
     const int rest = L / p.qtiles;
     const int hgs = p.Hk * p.head_groups;
@@ -899,7 +916,7 @@ void bsa_attn_kernel(AttnParams p) {
 
 template <int NW>
 hipError_t launch_nw(const AttnParams& p, int mode, bool idx64, hipStream_t s) {
-    const dim3 grid(p.total_wgs), block(NW * 64);
+    const dim3 grid(p.n_static + p.tail_wgs), block(NW * 64);
     void* args[] = {const_cast<AttnParams*>(&p)};
     const void* fn = nullptr;
     switch (mode) {

@@ -263,6 +263,7 @@ struct TopkParams {
     int B, nb, nb_pad, Hk, K, rows;
     int G;               // query heads per kv head (heads g*Hk + h of row h are combined)
     CombineParams cmb;   // cmb.ocmp == nullptr: no compressed-branch combine
+    int* zero_ctr;       // optional: set to 0 (the attention kernel's dynamic-tail counter)
 };
 
 enum AttnMode : int {
@@ -292,7 +293,13 @@ struct AttnParams {
     int bs_l, bs, K, nb;
     int head_groups;         // G / waves-per-workgroup
     int qtiles;              // N / 64
-    int total_wgs;
+    int total_wgs;           // work items (b, kv head, head group, query tile)
+    // Dynamic tail: items [n_static, total_wgs) go to the tail_wgs workgroups launched after
+    // the n_static statically mapped ones, each taking the next item from *tail_ctr (0 at
+    // launch; the last taker resets it), so the compute units that finish their static items
+    // first take more of the last items.  tail_ctr null: n_static = total_wgs, no tail.
+    int n_static, tail_wgs;
+    int* tail_ctr;
     float scale;             // softmax scale
     float scale_log2;        // softmax scale * log2(e)
 };

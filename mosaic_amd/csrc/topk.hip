@@ -11,6 +11,8 @@ namespace {
 template <int PL>  // keys per lane: nb <= 64 * PL
 __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
     const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));  // one per wave
+    if (p.zero_ctr != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(p.zero_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (row >= p.rows) return;  // uniform per wave; no barriers in this kernel
     const int lane = threadIdx.x & 63;
     const bf16_t* src = p.sbar + (int64_t)row * p.nb_pad;
