@@ -394,3 +394,51 @@ def test_module_rebuilds_tiles_when_neighbours_change():
         att = knn_attention(k, v, m.neighbors, m.rel_pos, m.to_q.weight, m.scale)   # per-target kernel
         ref = m.to_o(att.to(x.dtype).flatten(-2))
     assert torch.equal(y, ref)
+
+
+def test_knn_attention_tiles_fall_back_with_64_bit_offsets():
+    """Tiles given for k / v views the tiled kernel cannot address with 32-bit offsets (a
+    negative point stride): the per-target kernel runs instead, with the same result as the
+    tiled call on the forward-order copy."""
+    from mosaic_amd import _lib
+    from mosaic_amd.interp import knn_tiles
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(hp, ll, 24)
+    S, B, H = len(hp), 2, 3
+    k, v = rand(S, B, H, 64, seed=110).to(DEV), rand(S, B, H, 64, seed=111).to(DEV)
+    w_q = rand(H * 64, 3, seed=112).to(DEV)
+    order = spatial_order(ll)
+    tiles = tiles_on(nb, order)
+    fwd = knn_attention(k, v, nb.to(DEV), rel.to(DEV), w_q, 0.125, target_order=order.to(DEV), tiles=tiles)
+    kr, vr = k.flip(0).contiguous(), v.flip(0).contiguous()
+
+    def reversed_view(t):
+        last = t[S - 1]
+        return _lib.Bnhd(last.data_ptr(), t.stride(1), -t.stride(0), t.stride(2))
+    parts = [tiles[n] for n in ("start", "src", "nsrc", "slot")]
+    tl = _lib.KnnTiles(*(t.data_ptr() for t in parts), parts[0].numel() - 1, tiles["max_rows"])
+    import ctypes
+    nb32 = nb.to(DEV, torch.int32).contiguous()
+    out = torch.empty_like(fwd)
+    st = _lib.lib().mosaic_knn_interp_fwd_ex(reversed_view(kr), reversed_view(vr), nb32.data_ptr(),
+                                             rel.to(DEV).float().contiguous().data_ptr(), w_q.data_ptr(),
+                                             order.to(DEV, torch.int32).data_ptr(), ctypes.byref(tl), S, len(ll), B,
+                                             H, 64, 24, 0.125, 0, out.data_ptr(),
+                                             torch.cuda.current_stream().cuda_stream)
+    _lib.check(st, "mosaic_knn_interp_fwd_ex")
+    torch.cuda.synchronize()
+    assert torch.equal(out, fwd)
+
+
+@pytest.mark.parametrize("H,B", [(1, 1), (1, 3), (5, 2)])
+def test_knn_attention_tiled_head_and_member_counts(H, B):
+    ll, hp = lonlat_grid(24, 13), torch.deg2rad(get_healpix_grid(4))
+    nb, rel = scheme(ll, hp, 24)
+    k, v = rand(len(ll), B, H, 64, seed=120 + H), rand(len(ll), B, H, 64, seed=130 + B)
+    w_q = rand(H * 64, 3, seed=140)
+    order = spatial_order(hp)
+    args = (k.to(DEV), v.to(DEV), nb.to(DEV), rel.to(DEV), w_q.to(DEV), 0.125)
+    direct = knn_attention(*args, target_order=order.to(DEV))
+    tiled = knn_attention(*args, target_order=order.to(DEV), tiles=tiles_on(nb, order))
+    assert torch.equal(tiled, direct)
+    close(tiled, oracle(k, v, nb, rel, w_q, 0.125, False))
