@@ -184,6 +184,75 @@ __device__ __forceinline__ void select_topk(const uint32_t (&raw)[PL], int nb, i
     }
 }
 
+// Batcher's odd-even merge sort network over N keys (N a power of two), descending.  All
+// indices are compile-time constants, so the keys stay in registers; keys fixed at zero
+// (padding) fold away.
+template <int N>
+__device__ __forceinline__ void sort_desc(uint32_t (&a)[N]) {
+#pragma unroll
+    for (int p = 1; p < N; p += p)
+#pragma unroll
+        for (int k = p; k > 0; k >>= 1)
+#pragma unroll
+            for (int j = k % p; j < N - k; j += k + k)
+#pragma unroll
+                for (int i = 0; i < k; ++i)
+                    if (i + j + k < N && (i + j) / (p + p) == (i + j + k) / (p + p)) {
+                        const uint32_t x = a[i + j], y = a[i + j + k];
+                        a[i + j] = max(x, y);
+                        a[i + j + k] = min(x, y);
+                    }
+}
+
+// Row stride (words) of the per-lane sorted key lists of select_topk_sorted: at least PL + 1
+// (the list and a zero sentinel), odd so the 64 lanes' reads of one round hit distinct banks.
+template <int PL>
+constexpr int kSortedStride = (PL + 1) | 1;
+
+// The same selection as select_topk (same keys, same order of the emitted indices) for
+// PL <= 16 and K <= 64, with no branch in a round: each lane first sorts its keys (a sorting
+// network in registers) and writes them, descending and followed by a zero, to its row of
+// `list` (this wave's 64 x kSortedStride<PL> words of LDS).  A round is then the wave
+// maximum of the lanes' current keys (head), a compare, and the winner's step to its next
+// key, read from LDS one round ahead (nxt), so the read's latency overlaps the next round's
+// reduction.  Lane kk keeps the kk-th emitted key; the indices are stored once at the end.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+
+template <int PL>
+__device__ __forceinline__ void select_topk_sorted(const uint32_t (&raw)[PL], int nb, int K, int lane,
+                                                   int64_t out0, int32_t* idx32, int64_t* idx64,
+                                                   lds_u32* list) {
+    constexpr int N = PL <= 1 ? 1 : PL <= 2 ? 2 : PL <= 4 ? 4 : PL <= 8 ? 8 : 16;
+    static_assert(PL <= 16, "at most 16 keys per lane");
+    uint32_t key[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int u = lane + 64 * i;
+        key[i] = (i < PL && u < nb) ? ((order16(raw[i < PL ? i : 0]) << 16) | (0xffffu - (uint32_t)u)) : 0u;
+    }
+    sort_desc<N>(key);
+    lds_u32* row = list + lane * kSortedStride<PL>;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) row[i] = key[i];
+    row[PL] = 0u;
+    uint32_t head = key[0], nxt = row[1];  // row[w], row[w + 1]
+    int w = 0;  // keys of this lane emitted so far
+    uint32_t mine = 0;
+    for (int kk = 0; kk < K; ++kk) {
+        const uint32_t mx = wave_max_all_u32(head);
+        const bool win = head == mx;
+        w += win ? 1 : 0;
+        head = win ? nxt : head;
+        nxt = row[min(w + 1, PL)];
+        mine = kk == lane ? mx : mine;
+    }
+    if (lane < K) {
+        const int u = (int)(0xffffu - (mine & 0xffffu));
+        if (idx32) idx32[out0 + lane] = u;
+        if (idx64) idx64[out0 + lane] = u;
+    }
+}
+
 // 2-D RoPE of one bf16 pair (x0, x1) packed in a word, by angle (c = cos, s = sin):
 // (x0 c - x1 s, x1 c + x0 s) in fp32 with both products and the sum rounded separately (no
 // fused multiply-add), as the reference's elementwise tensor ops round them
@@ -377,44 +446,62 @@ constexpr int kMaxSplits = 4;
 // All loads of all heads and splits are issued before any arithmetic (one memory round trip).
 // They are unconditional (past nsplit: the last split again, not used): loads under a branch
 // leave the compiler's count of loads in flight unknown at the join, and the first wait after
-// it then waits for all of them.
+// it then waits for all of them.  combine_load issues the loads and combine_store combines
+// and stores; other work can sit between the two, so the loads' latency overlaps it.
 template <int NH>
-__device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int nb, int t, int j0, int jstep, int lane) {
+struct CombineRows {
+    float2 mlv[NH][kMaxSplits];
+    float ov[NH][kMaxSplits];
+};
+
+template <int NH>
+__device__ __forceinline__ void combine_load(CombineRows<NH>& r, const CombineParams& c, int b, int nb, int t, int j0,
+                                             int jstep, int lane) {
     const int64_t stride = (int64_t)nb * c.Hq;
     // written by an earlier launch and only read here: the constant address space lets the
     // compiler take the scalar path for the uniform (max, sum) rows
     typedef const __attribute__((address_space(4))) float cfloat;
     cfloat* ml = (cfloat*)c.ml;
-    float2 mlv[NH][kMaxSplits];
-    float ov[NH][kMaxSplits];
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         const int64_t row0 = ((int64_t)b * c.nsplit * nb + t) * c.Hq + j0 + h * jstep;
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; ++sp) {
             const int64_t row = row0 + min(sp, c.nsplit - 1) * stride;
-            mlv[h][sp] = make_float2(ml[2 * row], ml[2 * row + 1]);
-            ov[h][sp] = c.opart[row * kHeadDim + lane];
+            r.mlv[h][sp] = make_float2(ml[2 * row], ml[2 * row + 1]);
+            r.ov[h][sp] = c.opart[row * kHeadDim + lane];
         }
     }
+}
+
+template <int NH>
+__device__ __forceinline__ void combine_store(const CombineRows<NH>& r, const CombineParams& c, int b, int nb, int t,
+                                              int j0, int jstep, int lane) {
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         float M = -INFINITY;
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; ++sp)
-            if (sp < c.nsplit) M = fmaxf(M, mlv[h][sp].x);
+            if (sp < c.nsplit) M = fmaxf(M, r.mlv[h][sp].x);
         float L = 0.f, acc = 0.f;
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; ++sp) {
             if (sp < c.nsplit) {
-                const float a = __builtin_amdgcn_exp2f(mlv[h][sp].x - M);
-                L += a * mlv[h][sp].y;
-                acc += a * ov[h][sp];
+                const float a = __builtin_amdgcn_exp2f(r.mlv[h][sp].x - M);
+                L += a * r.mlv[h][sp].y;
+                acc += a * r.ov[h][sp];
             }
         }
         const int j = j0 + h * jstep;
         c.ocmp[(((int64_t)b * nb + t) * c.Hq + j) * kHeadDim + lane] = (bf16_t)(pack_bf16x2(acc / L, 0.f) & 0xffffu);
     }
+}
+
+template <int NH>
+__device__ __forceinline__ void combine_ocmp(const CombineParams& c, int b, int nb, int t, int j0, int jstep, int lane) {
+    CombineRows<NH> r;
+    combine_load<NH>(r, c, b, nb, t, j0, jstep, lane);
+    combine_store<NH>(r, c, b, nb, t, j0, jstep, lane);
 }
 
 }  // namespace mosaic

@@ -16,9 +16,11 @@
 // selection row h sit in one workgroup and are reduced through LDS (bf16 tiles, 8-byte
 // reads and stores).
 //
-// The loop over key-block tiles is latency-bound (little arithmetic per tile): the K and
-// V^T fragments of the next tile are loaded into registers while the current one is
-// computed (two register sets, unrolled by two).  The pooling kernel writes K and V in MFMA
+// The loop over key-block tiles is latency-bound (little arithmetic per tile, one wave per
+// SIMD at the usual sizes): it is software-pipelined by one tile (the S product of the next
+// tile runs on the matrix cores during the mean and softmax of the current one), and the K
+// and V^T fragments are requested one to two tiles ahead into separate double-buffered
+// register sets (unrolled by two).  The pooling kernel writes K and V in MFMA
 // operand order (kfrag_index / vfrag_index), so each fragment is one coalesced 16-byte load
 // per lane; gathering them from row-major K and transposed V (32 rows per instruction) made
 // this kernel memory-pipeline bound (27.5 us against 15.7 us at Nside 64).  All loads are
@@ -32,27 +34,28 @@ namespace {
 constexpr int XSB = 40;  // row stride (bf16) of the per-head score exchange tile [32 t][32 u]
 constexpr float kTau = 8.0f;
 
-struct CmpFrags {
-    uint4 k[4];        // A operand of S^T = K Q^T: k_cmp[u0 + r][16*ds + 8*hh ..]
+struct KFrags {
+    uint4 k[4];  // A operand of S^T = K Q^T: k_cmp[u0 + r][16*ds + 8*hh ..]
+};
+struct VFrags {
     uint2 v[2][2][2];  // A operand of O^T += V^T P^T: [dt][s2][lo/hi]
 };
 
 // One 32-block tile's fragments: contiguous 1 KB runs of the operand-ordered pooled K / V
 // (blocks past nb are zero there; their scores are masked or never stored).
-template <bool ATTN>
-__device__ __forceinline__ void load_frags(CmpFrags& f, const CmpParams& p, int b, int c, int ut, int lane) {
+__device__ __forceinline__ void load_k(KFrags& f, const CmpParams& p, int b, int c, int ut, int lane) {
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) f.k[ds] = ld16(p.kfr + kfrag_index(b, c, p.Hk, p.ut_total, ut, ds, lane));
-    if constexpr (ATTN) {
+}
+__device__ __forceinline__ void load_v(VFrags& f, const CmpParams& p, int b, int c, int ut, int lane) {
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt)
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                const uint4 w = ld16(p.vfr + vfrag_index(b, c, p.Hk, p.ut_total, ut, dt, s2, lane));
-                f.v[dt][s2][0] = make_uint2(w.x, w.y);
-                f.v[dt][s2][1] = make_uint2(w.z, w.w);
-            }
-    }
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const uint4 w = ld16(p.vfr + vfrag_index(b, c, p.Hk, p.ut_total, ut, dt, s2, lane));
+            f.v[dt][s2][0] = make_uint2(w.x, w.y);
+            f.v[dt][s2][1] = make_uint2(w.z, w.w);
+        }
 }
 
 // Mean over the G heads of one 32x32 tile of bf16 scores in LDS, rounded to bf16 and stored
@@ -140,82 +143,111 @@ void cmp_kernel(CmpParams p) {
         for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
     float m = -INFINITY, l = 0.f;
 
-    // one key-block tile: S, the score mean, the online softmax and PV
-    auto step = [&](const CmpFrags& cur, int ut) __attribute__((always_inline)) {
-        const int u0 = ut * 32;
+    // S^T of one key tile for this head (fp32)
+    auto scores_of = [&](const KFrags& kf) __attribute__((always_inline)) {
         f32x16 s;
 #pragma unroll
         for (int e = 0; e < 16; ++e) s[e] = 0.f;
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds) s = mfma32(as_bf16x8(cur.k[ds]), qf[ds], s);
-
-        if constexpr (SCORES) {
-            // lane holds S^T[u0 + 8*(e/4) + 4*hh + e%4][t0 + r]: bf16(S) of this head to LDS
-            bf16_t* xb = xs + ((ut - ut0) & 1) * (kMaxG * 32 * XSB);
+        for (int ds = 0; ds < 4; ++ds) s = mfma32(as_bf16x8(kf.k[ds]), qf[ds], s);
+        return s;
+    };
+    // lane holds S^T[u0 + 8*(e/4) + 4*hh + e%4][t0 + r]: bf16(S) of this head to exchange buffer buf
+    auto publish = [&](const f32x16& s, int buf) __attribute__((always_inline)) {
+        bf16_t* xb = xs + buf * (kMaxG * 32 * XSB);
 #pragma unroll
-            for (int g4 = 0; g4 < 4; ++g4)
-                *reinterpret_cast<uint2*>(xb + (g * 32 + r) * XSB + 8 * g4 + 4 * hh) =
-                    make_uint2(pack_bf16x2(s[4 * g4 + 0], s[4 * g4 + 1]), pack_bf16x2(s[4 * g4 + 2], s[4 * g4 + 3]));
-            __syncthreads();  // buffer (ut & 1) is next written two tiles later, after another barrier
-            store_mean<G>(xb, srow0 + u0, p.nb_pad, p.nb - t0, tid, ng);
+        for (int g4 = 0; g4 < 4; ++g4)
+            *reinterpret_cast<uint2*>(xb + (g * 32 + r) * XSB + 8 * g4 + 4 * hh) =
+                make_uint2(pack_bf16x2(s[4 * g4 + 0], s[4 * g4 + 1]), pack_bf16x2(s[4 * g4 + 2], s[4 * g4 + 3]));
+    };
+    // the online softmax of one tile's logits and O^T += V^T P^T
+    auto attend = [&](f32x16 s, const VFrags& vf, int ut) __attribute__((always_inline)) {
+        const int u0 = ut * 32;
+        if (u0 + 32 > p.nb) {  // last, partial tile: blocks past the end get no weight
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                if (u0 + 8 * (e >> 2) + 4 * hh + (e & 3) >= p.nb) s[e] = -INFINITY;
         }
-
-        if constexpr (ATTN) {
-            if (u0 + 32 > p.nb) {  // last, partial tile: blocks past the end get no weight
+        float mx = s[0];
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
-                    if (u0 + 8 * (e >> 2) + 4 * hh + (e & 3) >= p.nb) s[e] = -INFINITY;
-            }
-            float mx = s[0];
+        for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
+        mx = xor32_max(mx) * p.scale_log2;
+        // lazy reference: moves only when a tile's max exceeds it by more than kTau (the
+        // first tile always moves it), so P <= 2^kTau and O is rarely rescaled
+        if (__builtin_amdgcn_ballot_w64(mx > m + kTau)) {
+            const float mnew = mx > m + kTau ? mx : m;
+            const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+            l *= alpha;
 #pragma unroll
-            for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
-            mx = xor32_max(mx) * p.scale_log2;
-            // lazy reference: moves only when a tile's max exceeds it by more than kTau (the
-            // first tile always moves it), so P <= 2^kTau and O is rarely rescaled
-            if (__builtin_amdgcn_ballot_w64(mx > m + kTau)) {
-                const float mnew = mx > m + kTau ? mx : m;
-                const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-                l *= alpha;
+            for (int dt = 0; dt < 2; ++dt) o[dt] *= alpha;
+            m = mnew;
+        }
+        float sum = 0.f;
 #pragma unroll
-                for (int dt = 0; dt < 2; ++dt) o[dt] *= alpha;
-                m = mnew;
-            }
-            float sum = 0.f;
+        for (int e = 0; e < 16; ++e) {
+            const float pe = __builtin_amdgcn_exp2f(fmaf(s[e], p.scale_log2, -m));
+            s[e] = pe;
+            sum += pe;
+        }
+        l += sum;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float pe = __builtin_amdgcn_exp2f(fmaf(s[e], p.scale_log2, -m));
-                s[e] = pe;
-                sum += pe;
-            }
-            l += sum;
+        for (int s2 = 0; s2 < 2; ++s2) {
+            uint4 pu;
+            pu.x = pack_bf16x2(s[8 * s2 + 0], s[8 * s2 + 1]);
+            pu.y = pack_bf16x2(s[8 * s2 + 2], s[8 * s2 + 3]);
+            pu.z = pack_bf16x2(s[8 * s2 + 4], s[8 * s2 + 5]);
+            pu.w = pack_bf16x2(s[8 * s2 + 6], s[8 * s2 + 7]);
+            const bf16x8 pb = as_bf16x8(pu);
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2) {
-                uint4 pu;
-                pu.x = pack_bf16x2(s[8 * s2 + 0], s[8 * s2 + 1]);
-                pu.y = pack_bf16x2(s[8 * s2 + 2], s[8 * s2 + 3]);
-                pu.z = pack_bf16x2(s[8 * s2 + 4], s[8 * s2 + 5]);
-                pu.w = pack_bf16x2(s[8 * s2 + 6], s[8 * s2 + 7]);
-                const bf16x8 pb = as_bf16x8(pu);
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
-                    const uint2 lo = cur.v[dt][s2][0], hi = cur.v[dt][s2][1];
-                    o[dt] = mfma32(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb, o[dt]);
-                }
+            for (int dt = 0; dt < 2; ++dt) {
+                const uint2 lo = vf.v[dt][s2][0], hi = vf.v[dt][s2][1];
+                o[dt] = mfma32(as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y)), pb, o[dt]);
             }
         }
     };
-    // Two fragment sets swap roles; the next tile is always requested (past the last tile,
-    // the last one again, never used), so every wait targets exactly the set about to be used.
+    // Software-pipelined by one tile: the S product of tile ut + 1 is issued before the score
+    // mean and the softmax of tile ut, so the matrix cores run it while those execute, and
+    // bf16(S) of tile ut + 1 is published (one barrier per tile) after them.  K and V
+    // fragments are double-buffered separately: K of tile ut + 2 and V of tile ut + 1 are
+    // requested while tile ut is processed.  Past the last tile the requests repeat the last
+    // tile (never used), so every load is unconditional and every wait targets exactly the
+    // fragments about to be used.  Exchange buffer (ut - ut0) & 1 holds tile ut; it is
+    // rewritten two tiles later, after the barrier that follows every wave's mean of it.
     if (ut0 < ut1) {
-        CmpFrags f0, f1;
-        load_frags<ATTN>(f0, p, b, c, ut0, lane);
+        KFrags ka, kb;
+        VFrags va, vb;
+        load_k(ka, p, b, c, ut0, lane);
+        load_v(va, p, b, c, ut0, lane);
+        load_k(kb, p, b, c, min(ut0 + 1, ut1 - 1), lane);
+        f32x16 sa = scores_of(ka), sb;
+        if constexpr (SCORES) {
+            publish(sa, 0);
+            __syncthreads();
+        }
         for (int ut = ut0;; ut += 2) {
-            load_frags<ATTN>(f1, p, b, c, min(ut + 1, ut1 - 1), lane);
-            step(f0, ut);
+            // tile ut: S in sa (published in buffer 0), V in va; K of tile ut + 1 in kb
+            sb = scores_of(kb);
+            load_k(ka, p, b, c, min(ut + 2, ut1 - 1), lane);
+            if constexpr (ATTN) load_v(vb, p, b, c, min(ut + 1, ut1 - 1), lane);
+            if constexpr (SCORES) store_mean<G>(xs, srow0 + ut * 32, p.nb_pad, p.nb - t0, tid, ng);
+            if constexpr (ATTN) attend(sa, va, ut);
             if (ut + 1 >= ut1) break;
-            load_frags<ATTN>(f0, p, b, c, min(ut + 2, ut1 - 1), lane);
-            step(f1, ut + 1);
+            if constexpr (SCORES) {
+                publish(sb, 1);
+                __syncthreads();
+            }
+            // tile ut + 1: S in sb (buffer 1), V in vb; K of tile ut + 2 in ka
+            sa = scores_of(ka);
+            load_k(kb, p, b, c, min(ut + 3, ut1 - 1), lane);
+            if constexpr (ATTN) load_v(va, p, b, c, min(ut + 2, ut1 - 1), lane);
+            if constexpr (SCORES)
+                store_mean<G>(xs + kMaxG * 32 * XSB, srow0 + (ut + 1) * 32, p.nb_pad, p.nb - t0, tid, ng);
+            if constexpr (ATTN) attend(sb, vb, ut + 1);
             if (ut + 2 >= ut1) break;
+            if constexpr (SCORES) {
+                publish(sa, 0);
+                __syncthreads();
+            }
         }
     }
 

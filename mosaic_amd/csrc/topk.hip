@@ -1,15 +1,20 @@
 // topk.hip -- per-row top-k block selection over the bf16 selection scores (gfx950).
 //
 // Replaces scores.topk(k=block_count, dim=-1, largest=True) of attn_topk
-// (primitives.py:50).  One wave per row (b, h, t); the selection itself is select_topk
-// (bsa_common.h).
+// (primitives.py:50).  One wave per row (b, h, t); the selection itself is select_topk_sorted
+// (up to 1024 blocks and 64 selected) or select_topk (bsa_common.h).  When the row's
+// compressed-branch output is combined here too, for 1, 2 or 4 query heads per kv head (NH)
+// the split partials are requested before the selection and combined after it, so their
+// memory latency overlaps the selection rounds.
 #include "bsa_common.h"
 
 namespace mosaic {
 namespace {
 
-template <int PL>  // keys per lane: nb <= 64 * PL
+template <int PL, int NH>  // keys per lane: nb <= 64 * PL; NH > 0: G == NH, partials prefetched
 __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
+    constexpr bool kSorted = PL <= 16;
+    __shared__ uint32_t lists[kSorted ? 4 * 64 * kSortedStride<PL> : 1];
     const int row = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));  // one per wave
     if (p.zero_ctr != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
         __hip_atomic_store(p.zero_ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -26,20 +31,44 @@ __global__ __launch_bounds__(256) void topk_kernel(TopkParams p) {
 #pragma unroll
     for (int i = 0; i < PL; ++i) raw[i] = src[min(lane + 64 * i, p.nb_pad - 1)];
 
+    const int64_t out0 = (((int64_t)b * p.nb + t) * p.Hk + h) * p.K;
+    auto select = [&]() __attribute__((always_inline)) {
+        if constexpr (kSorted) {
+            if (p.K <= 64) {
+                select_topk_sorted<PL>(raw, p.nb, p.K, lane, out0, p.idx32, p.idx64,
+                                       (lds_u32*)lists + (threadIdx.x >> 6) * 64 * kSortedStride<PL>);
+                return;
+            }
+        }
+        select_topk<PL>(raw, p.nb, p.K, lane, out0, p.idx32, p.idx64);
+    };
     // compressed-branch output of block t for the G query heads g*Hk + h of this row
-    if (p.cmb.ocmp != nullptr) {
-        int g = 0;
-        for (; g + 4 <= p.G; g += 4) combine_ocmp<4>(p.cmb, b, p.nb, t, g * p.Hk + h, p.Hk, lane);
-        for (; g < p.G; ++g) combine_ocmp<1>(p.cmb, b, p.nb, t, g * p.Hk + h, p.Hk, lane);
+    if constexpr (NH > 0) {
+        const bool cmb = p.cmb.ocmp != nullptr;
+        CombineRows<NH> rows;
+        if (cmb) combine_load<NH>(rows, p.cmb, b, p.nb, t, h, p.Hk, lane);
+        select();
+        if (cmb) combine_store<NH>(rows, p.cmb, b, p.nb, t, h, p.Hk, lane);
+    } else {
+        if (p.cmb.ocmp != nullptr) {
+            int g = 0;
+            for (; g + 4 <= p.G; g += 4) combine_ocmp<4>(p.cmb, b, p.nb, t, g * p.Hk + h, p.Hk, lane);
+            for (; g < p.G; ++g) combine_ocmp<1>(p.cmb, b, p.nb, t, g * p.Hk + h, p.Hk, lane);
+        }
+        select();
     }
-
-    select_topk<PL>(raw, p.nb, p.K, lane, (((int64_t)b * p.nb + t) * p.Hk + h) * p.K, p.idx32, p.idx64);
 }
 
 template <int PL>
 hipError_t launch_pl(const TopkParams& p, hipStream_t s) {
     void* args[] = {const_cast<TopkParams*>(&p)};
-    return hipLaunchKernel((const void*)topk_kernel<PL>, dim3((p.rows + 3) / 4), dim3(256), args, 0, s);
+    const void* fn = (const void*)topk_kernel<PL, 0>;
+    if constexpr (PL <= 16) {
+        if (p.G == 1) fn = (const void*)topk_kernel<PL, 1>;
+        if (p.G == 2) fn = (const void*)topk_kernel<PL, 2>;
+        if (p.G == 4) fn = (const void*)topk_kernel<PL, 4>;
+    }
+    return hipLaunchKernel(fn, dim3((p.rows + 3) / 4), dim3(256), args, 0, s);
 }
 
 // Compressed-branch split combine alone (no selection): one wave per (batch, block).

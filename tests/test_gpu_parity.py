@@ -134,6 +134,18 @@ def test_attn_topk_band_rule(B, nb, Hq, Hk, K):
     assert torch.equal(got[clear], ref[clear])
 
 
+@pytest.mark.parametrize("nb,K", [(768, 16), (192, 64), (192, 80), (1536, 24)],
+                         ids=["sorted_lists_k16", "sorted_lists_k64", "buffered_k80", "buffered_nb1536"])
+def test_attn_topk_ties_lowest_index_first(nb, K):
+    """Every score of every row equal (zero queries): the kernel emits the lowest block indices
+    in ascending order, on both selection paths (per-lane sorted lists for up to 16 keys per
+    lane and 64 selected; the four-key buffers otherwise)."""
+    q_cmp = torch.zeros(1, nb, 8, 64, dtype=torch.bfloat16)
+    k_cmp = rand(1, nb, 2, 64, seed=18)
+    got = M.attn_topk(*dev(q_cmp, k_cmp), K).cpu()
+    assert torch.equal(got, torch.arange(K).expand_as(got))
+
+
 def test_attn_topk_golden_fixture():
     import os
     data = torch.load(os.path.join(os.path.dirname(__file__), "golden", "topk_scores_small.pt"), weights_only=True)
