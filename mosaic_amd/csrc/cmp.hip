@@ -113,7 +113,7 @@ __device__ __forceinline__ void store_mean(const bf16_t* xb, bf16_t* dst_row0, i
 // G > 0: query heads per kv head as a compile-time constant (a power of two); G == 0: any
 // head count (p.G waves, at most 16).
 template <bool SCORES, bool ATTN, int G>
-__global__ __attribute__((amdgpu_flat_work_group_size(1, G > 0 ? G * 64 : 1024), amdgpu_waves_per_eu(1, 2)))
+__global__ __attribute__((amdgpu_flat_work_group_size(1, G > 0 ? G * 64 : 1024), amdgpu_waves_per_eu(1, 3)))
 void cmp_kernel(CmpParams p) {
     constexpr int kMaxG = G > 0 ? G : 16;
     __shared__ __attribute__((aligned(16))) bf16_t xs[SCORES ? 2 * kMaxG * 32 * XSB : 8];  // [2][G][32 t][XSB]
