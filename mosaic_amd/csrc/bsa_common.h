@@ -101,19 +101,28 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return __uint_as_float(max(max(a, b), max(c, d)));
 }
 
-// Unsigned maximum over the wave, in every lane and without scalar round trips: DPP steps
-// within each 16-lane row, then v_permlane16_swap (rows 0 <-> 1 and 2 <-> 3) and
-// v_permlane32_swap (halves), each followed by a max of the two swapped copies.
-__device__ __forceinline__ uint32_t wave_max_all_u32(uint32_t x) {
+// Unsigned maximum over each group of LW consecutive lanes (16, 32 or 64), in every lane of
+// the group and without scalar round trips: DPP steps within each 16-lane row, then
+// v_permlane16_swap (rows 0 <-> 1 and 2 <-> 3) for groups of 32 and v_permlane32_swap
+// (halves) for the whole wave, each followed by a max of the two swapped copies.
+template <int LW>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t x) {
+    static_assert(LW == 16 || LW == 32 || LW == 64, "groups of 16, 32 or 64 lanes");
     x = dpp_max_u32<0xb1>(x);   // quad_perm [1,0,3,2]
     x = dpp_max_u32<0x4e>(x);   // quad_perm [2,3,0,1]
     x = dpp_max_u32<0x141>(x);  // row_half_mirror
     x = dpp_max_u32<0x140>(x);  // row_mirror: every lane of a row holds the row max
-    const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-    x = max((uint32_t)a[0], (uint32_t)a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-    return max((uint32_t)b[0], (uint32_t)b[1]);
+    if constexpr (LW >= 32) {
+        const auto a = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        x = max((uint32_t)a[0], (uint32_t)a[1]);
+    }
+    if constexpr (LW == 64) {
+        const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        x = max((uint32_t)b[0], (uint32_t)b[1]);
+    }
+    return x;
 }
+__device__ __forceinline__ uint32_t wave_max_all_u32(uint32_t x) { return group_max_u32<64>(x); }
 
 // ---------------------------------------------------------------------------------------
 // Top-k of one row of bf16 selection scores held by a wave: torch.topk(k, largest=True,
@@ -210,24 +219,28 @@ template <int PL>
 constexpr int kSortedStride = (PL + 1) | 1;
 
 // The same selection as select_topk (same keys, same order of the emitted indices) for
-// PL <= 16 and K <= 64, with no branch in a round: each lane first sorts its keys (a sorting
-// network in registers) and writes them, descending and followed by a zero, to its row of
-// `list` (this wave's 64 x kSortedStride<PL> words of LDS).  A round is then the wave
-// maximum of the lanes' current keys (head), a compare, and the winner's step to its next
-// key, read from LDS one round ahead (nxt), so the read's latency overlaps the next round's
-// reduction.  Lane kk keeps the kk-th emitted key; the indices are stored once at the end.
+// PL <= 16 and K <= LW, with no branch in a round.  The row is held by a group of LW
+// consecutive lanes (the whole wave, or 2 or 4 rows per wave in groups of 32 or 16); lane lr of
+// the group holds raw[i] = the score of block u = lr + LW i.  Each lane first sorts its keys
+// (a sorting network in registers) and writes them, descending and followed by a zero, to its
+// row of `list` (this wave's 64 x kSortedStride<PL> words of LDS, row = the lane).  A round is
+// then the group maximum of the lanes' current keys (head), a compare, and the winner's step
+// to its next key, read from LDS one round ahead (nxt), so the read's latency overlaps the
+// next round's reduction.  Lane kk of the group keeps the kk-th emitted key; the indices are
+// stored once at the end (not when `live` is false: a group past the last row).
 typedef __attribute__((address_space(3))) uint32_t lds_u32;
 
-template <int PL>
+template <int PL, int LW = 64>
 __device__ __forceinline__ void select_topk_sorted(const uint32_t (&raw)[PL], int nb, int K, int lane,
                                                    int64_t out0, int32_t* idx32, int64_t* idx64,
-                                                   lds_u32* list) {
+                                                   lds_u32* list, int lr = -1, bool live = true) {
     constexpr int N = PL <= 1 ? 1 : PL <= 2 ? 2 : PL <= 4 ? 4 : PL <= 8 ? 8 : 16;
     static_assert(PL <= 16, "at most 16 keys per lane");
+    if (LW == 64) lr = lane;
     uint32_t key[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const int u = lane + 64 * i;
+        const int u = lr + LW * i;
         key[i] = (i < PL && u < nb) ? ((order16(raw[i < PL ? i : 0]) << 16) | (0xffffu - (uint32_t)u)) : 0u;
     }
     sort_desc<N>(key);
@@ -239,17 +252,17 @@ __device__ __forceinline__ void select_topk_sorted(const uint32_t (&raw)[PL], in
     int w = 0;  // keys of this lane emitted so far
     uint32_t mine = 0;
     for (int kk = 0; kk < K; ++kk) {
-        const uint32_t mx = wave_max_all_u32(head);
+        const uint32_t mx = group_max_u32<LW>(head);
         const bool win = head == mx;
         w += win ? 1 : 0;
         head = win ? nxt : head;
         nxt = row[min(w + 1, PL)];
-        mine = kk == lane ? mx : mine;
+        mine = kk == lr ? mx : mine;
     }
-    if (lane < K) {
+    if (live && lr < K) {
         const int u = (int)(0xffffu - (mine & 0xffffu));
-        if (idx32) idx32[out0 + lane] = u;
-        if (idx64) idx64[out0 + lane] = u;
+        if (idx32) idx32[out0 + lr] = u;
+        if (idx64) idx64[out0 + lr] = u;
     }
 }
 
@@ -448,10 +461,10 @@ constexpr int kMaxSplits = 4;
 // leave the compiler's count of loads in flight unknown at the join, and the first wait after
 // it then waits for all of them.  combine_load issues the loads and combine_store combines
 // and stores; other work can sit between the two, so the loads' latency overlaps it.
-template <int NH>
+template <int NH, int E = 1>  // E: elements (dimensions) of each head per lane
 struct CombineRows {
     float2 mlv[NH][kMaxSplits];
-    float ov[NH][kMaxSplits];
+    float ov[NH][kMaxSplits][E];
 };
 
 template <int NH>
@@ -469,9 +482,31 @@ __device__ __forceinline__ void combine_load(CombineRows<NH>& r, const CombinePa
         for (int sp = 0; sp < kMaxSplits; ++sp) {
             const int64_t row = row0 + min(sp, c.nsplit - 1) * stride;
             r.mlv[h][sp] = make_float2(ml[2 * row], ml[2 * row + 1]);
-            r.ov[h][sp] = c.opart[row * kHeadDim + lane];
+            r.ov[h][sp][0] = c.opart[row * kHeadDim + lane];
         }
     }
+}
+
+// Combined value of head h, element e of one lane's loaded partials: exp2 weights relative to
+// the largest split max.  One split: its weight exp2(m - m) is exactly 1, so the value is
+// o / l, taken directly (the same result without the exponentials).
+template <int NH, int E = 1>
+__device__ __forceinline__ float combine_value(const CombineRows<NH, E>& r, int h, int e, int nsplit) {
+    if (nsplit == 1) return r.ov[h][0][e] / r.mlv[h][0].y;
+    float M = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+        if (sp < nsplit) M = fmaxf(M, r.mlv[h][sp].x);
+    float L = 0.f, acc = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp) {
+        if (sp < nsplit) {
+            const float a = __builtin_amdgcn_exp2f(r.mlv[h][sp].x - M);
+            L += a * r.mlv[h][sp].y;
+            acc += a * r.ov[h][sp][e];
+        }
+    }
+    return acc / L;
 }
 
 template <int NH>
@@ -479,21 +514,57 @@ __device__ __forceinline__ void combine_store(const CombineRows<NH>& r, const Co
                                               int j0, int jstep, int lane) {
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
-        float M = -INFINITY;
+        const int j = j0 + h * jstep;
+        c.ocmp[(((int64_t)b * nb + t) * c.Hq + j) * kHeadDim + lane] =
+            (bf16_t)(pack_bf16x2(combine_value<NH>(r, h, 0, c.nsplit), 0.f) & 0xffffu);
+    }
+}
+
+// The same for E = 64 / LW dimensions per lane, when a row's 64 dimensions are spread over a
+// group of LW lanes (lane lr of the group: dimensions E lr .. E lr + E - 1).  The (max, sum)
+// pairs differ between the groups of a wave, so they are vector loads here.
+template <int NH, int E>
+__device__ __forceinline__ void combine_load_group(CombineRows<NH, E>& r, const CombineParams& c, int b, int nb,
+                                                   int t, int j0, int jstep, int lr) {
+    const int64_t stride = (int64_t)nb * c.Hq;
 #pragma unroll
-        for (int sp = 0; sp < kMaxSplits; ++sp)
-            if (sp < c.nsplit) M = fmaxf(M, r.mlv[h][sp].x);
-        float L = 0.f, acc = 0.f;
+    for (int h = 0; h < NH; ++h) {
+        const int64_t row0 = ((int64_t)b * c.nsplit * nb + t) * c.Hq + j0 + h * jstep;
 #pragma unroll
         for (int sp = 0; sp < kMaxSplits; ++sp) {
-            if (sp < c.nsplit) {
-                const float a = __builtin_amdgcn_exp2f(r.mlv[h][sp].x - M);
-                L += a * r.mlv[h][sp].y;
-                acc += a * r.ov[h][sp];
+            const int64_t row = row0 + min(sp, c.nsplit - 1) * stride;
+            r.mlv[h][sp] = c.ml[row];
+            const float* src = c.opart + row * kHeadDim + E * lr;
+            if constexpr (E == 4) {
+                const float4 v = *reinterpret_cast<const float4*>(src);
+                r.ov[h][sp][0] = v.x; r.ov[h][sp][1] = v.y; r.ov[h][sp][2] = v.z; r.ov[h][sp][3] = v.w;
+            } else if constexpr (E == 2) {
+                const float2 v = *reinterpret_cast<const float2*>(src);
+                r.ov[h][sp][0] = v.x; r.ov[h][sp][1] = v.y;
+            } else {
+                r.ov[h][sp][0] = src[0];
             }
         }
+    }
+}
+
+template <int NH, int E>
+__device__ __forceinline__ void combine_store_group(const CombineRows<NH, E>& r, const CombineParams& c, int b, int nb,
+                                                    int t, int j0, int jstep, int lr) {
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
         const int j = j0 + h * jstep;
-        c.ocmp[(((int64_t)b * nb + t) * c.Hq + j) * kHeadDim + lane] = (bf16_t)(pack_bf16x2(acc / L, 0.f) & 0xffffu);
+        bf16_t* dst = c.ocmp + (((int64_t)b * nb + t) * c.Hq + j) * kHeadDim + E * lr;
+        uint32_t w[(E + 1) / 2];
+#pragma unroll
+        for (int e = 0; e < E; e += 2) {
+            const float v0 = combine_value<NH, E>(r, h, e, c.nsplit);
+            const float v1 = e + 1 < E ? combine_value<NH, E>(r, h, e + 1 < E ? e + 1 : e, c.nsplit) : 0.f;
+            w[e / 2] = pack_bf16x2(v0, v1);
+        }
+        if constexpr (E == 4) *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+        else if constexpr (E == 2) *reinterpret_cast<uint32_t*>(dst) = w[0];
+        else *dst = (bf16_t)(w[0] & 0xffffu);
     }
 }
 

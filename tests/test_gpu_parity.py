@@ -134,14 +134,41 @@ def test_attn_topk_band_rule(B, nb, Hq, Hk, K):
     assert torch.equal(got[clear], ref[clear])
 
 
-@pytest.mark.parametrize("nb,K", [(768, 16), (192, 64), (192, 80), (1536, 24)],
-                         ids=["sorted_lists_k16", "sorted_lists_k64", "buffered_k80", "buffered_nb1536"])
-def test_attn_topk_ties_lowest_index_first(nb, K):
+@pytest.mark.parametrize("B,nb,Hq,Hk,K", [(24, 192, 16, 4, 16), (12, 384, 12, 3, 24), (31, 91, 6, 3, 7)],
+                         ids=["four_rows_per_wave", "two_rows_per_wave", "four_rows_partial_last_group"])
+def test_attn_topk_rows_per_wave(B, nb, Hq, Hk, K):
+    """Many short rows: the kernel selects 4 (groups of 16 lanes) or 2 (of 32) rows per wave.
+    Band rule on every row, and the rows without a tie inside the band equal the oracle as
+    ordered lists; 8463 rows leave the last wave's last group empty."""
+    print(f"top-k rows per wave B={B} nb={nb} heads {Hq}/{Hk} K={K}", flush=True)
+    q_cmp = rand(B, nb, Hq, 64, seed=19) / 8
+    k_cmp = rand(B, nb, Hk, 64, seed=20) / 8
+    got = M.attn_topk(*dev(q_cmp.to(torch.bfloat16), k_cmp.to(torch.bfloat16)), K).cpu()
+    scores = O.topk_scores(q_cmp.to(torch.bfloat16), k_cmp.to(torch.bfloat16)).permute(0, 2, 1, 3)
+    bad, amb, rows = O.selection_band_check(scores, got, K)
+    assert bad == 0, f"{bad} of {rows} rows violate the band rule"
+    ref = O.attn_topk(q_cmp.to(torch.bfloat16), k_cmp.to(torch.bfloat16), K)
+    srt = scores.float().sort(-1, descending=True).values
+    # rows whose K-th and (K+1)-th scores are apart: the same set of blocks
+    boundary = (srt[..., K - 1] - srt[..., K]).abs() > 1e-3
+    assert boundary.any()
+    assert torch.equal(got[boundary].sort(-1).values, ref[boundary].sort(-1).values)
+    # rows without a tie among their K + 1 largest: the same ordered list
+    clear = (srt[..., :K] - srt[..., 1:K + 1]).abs().min(-1).values > 1e-3
+    assert torch.equal(got[clear], ref[clear])
+
+
+@pytest.mark.parametrize("B,nb,K", [(1, 768, 16), (1, 192, 64), (1, 192, 80), (1, 1536, 24), (48, 192, 16),
+                                    (24, 384, 24)],
+                         ids=["sorted_lists_k16", "sorted_lists_k64", "buffered_k80", "buffered_nb1536",
+                              "four_rows_per_wave", "two_rows_per_wave"])
+def test_attn_topk_ties_lowest_index_first(B, nb, K):
     """Every score of every row equal (zero queries): the kernel emits the lowest block indices
-    in ascending order, on both selection paths (per-lane sorted lists for up to 16 keys per
-    lane and 64 selected; the four-key buffers otherwise)."""
-    q_cmp = torch.zeros(1, nb, 8, 64, dtype=torch.bfloat16)
-    k_cmp = rand(1, nb, 2, 64, seed=18)
+    in ascending order, on every selection path (per-lane sorted lists for up to 16 keys per
+    lane and 64 selected, with one, two or four rows per wave; the four-key buffers
+    otherwise)."""
+    q_cmp = torch.zeros(B, nb, 8, 64, dtype=torch.bfloat16)
+    k_cmp = rand(B, nb, 2, 64, seed=18)
     got = M.attn_topk(*dev(q_cmp, k_cmp), K).cpu()
     assert torch.equal(got, torch.arange(K).expand_as(got))
 
