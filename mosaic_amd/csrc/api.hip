@@ -303,6 +303,8 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
         cp.B = B; cp.nb = L.nb; cp.nb_pad = L.nb_pad; cp.Hq = Hq; cp.Hk = Hk; cp.G = Hq / Hk;
         cp.nsplit = L.nsplit; cp.ut_total = L.nb_pad / 32;
         cp.scale_log2 = scale * kLog2e;
+        // one split: the scores pass writes the compressed-branch output, nothing to combine
+        cp.ocmp = (cmp && L.nsplit == 1) ? reinterpret_cast<bf16_t*>(w + L.ocmp) : nullptr;
         if (run(MOSAIC_BSA_STAGE_CMP))
             if (int e = launch_status(launch_cmp(cp, sel, cmp, s))) return e;
         if (int e = record(events, 2, s)) return e;
@@ -314,6 +316,7 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
             TopkParams tp{};
             tp.G = Hq / Hk;
             tp.cmb = cb;
+            if (cp.ocmp != nullptr) tp.cmb.ocmp = nullptr;
             tp.sbar = cp.sbar;
             tp.idx32 = reinterpret_cast<int32_t*>(w + L.idx);
             tp.idx64 = a->block_indices_out;
@@ -325,7 +328,7 @@ int bsa_forward(const mosaic_bsa_args* a, void* ws, size_t ws_bytes, void* strea
                 if (int e = launch_status(launch_topk(tp, s))) return e;
             ap.idx = tp.idx32;
             ap.kbnd = pp.kbnd;
-        } else if (cmp) {
+        } else if (cmp && cp.ocmp == nullptr) {
             if (run(MOSAIC_BSA_STAGE_TOPK))
                 if (int e = launch_status(launch_combine(cb, B, L.nb, s))) return e;
         }

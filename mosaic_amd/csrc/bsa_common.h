@@ -324,6 +324,9 @@ struct CmpParams {
     bf16_t* sbar;                                  // selection scores [B, Hk, nb, nb_pad]
     float* opart;                                  // [B, U, nb, Hq, 64] unnormalised O
     float2* ml;                                    // [B, U, nb, Hq] (running max, sum), log2 units
+    bf16_t* ocmp;                                  // one split (nsplit == 1): the compressed-branch
+                                                   // output [B, nb, Hq, 64] = bf16(O / l), written
+                                                   // here instead of opart / ml; else null
     int B, nb, nb_pad, Hq, Hk, G, nsplit, ut_total;
     float scale_log2;                              // softmax_scale * log2(e)
 };

@@ -9,7 +9,8 @@
 //   attention   flash_attn_func(q_cmp, k_cmp, v_cmp) (primitives.py:77): logits S*scale,
 //               online softmax in base 2 over this split's range of key blocks, P -> bf16,
 //               O^T += v_cmp^T P^T.  Each split writes its unnormalised O and (max, sum);
-//               the top-k kernel combines the splits.
+//               the top-k kernel combines the splits.  With one split the kernel writes
+//               the output bf16(O / l) itself.
 //
 // Grid: (query-block tiles of 32, selection row h, batch * splits).  Workgroup: G waves;
 // wave g handles query head j = g*Hk + h against kv head j / G, so the G heads averaged by
@@ -253,7 +254,18 @@ void cmp_kernel(CmpParams p) {
 
     if constexpr (ATTN) {
         const float ltot = xor32_add(l);
-        if (tvalid) {
+        if (tvalid && p.ocmp != nullptr) {
+            // one split: the output itself, O / l rounded to bf16 (the combine's value for one
+            // split, the same division)
+            bf16_t* op = p.ocmp + (((int64_t)b * p.nb + t0 + r) * p.Hq + j) * kHeadDim;
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4)
+                    *reinterpret_cast<uint2*>(op + 32 * dt + 8 * g4 + 4 * hh) =
+                        make_uint2(pack_bf16x2(o[dt][4 * g4 + 0] / ltot, o[dt][4 * g4 + 1] / ltot),
+                                   pack_bf16x2(o[dt][4 * g4 + 2] / ltot, o[dt][4 * g4 + 3] / ltot));
+        } else if (tvalid) {
             const int64_t row = (((int64_t)b * p.nsplit + split) * p.nb + t0 + r) * p.Hq + j;
             if (hh == 0) p.ml[row] = make_float2(m, ltot);
             float* op = p.opart + row * kHeadDim;
