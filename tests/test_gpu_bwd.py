@@ -3,7 +3,7 @@ against the CPU oracle ``bsa_oracle.sparse_attn_bwd`` (marked ``gpu``).
 
 Both backward passes take the same forward output and LSE (the HIP forward's), so the
 comparison isolates the backward.  Bars per gradient: relative L2 <= 1e-2 and max-abs <=
-2e-2 * max(1, max |ref|) -- the north-star output bars, scaled to the gradient's magnitude
+2e-2 * max(1, max |ref|) -- the forward op's output bars, scaled to the gradient's magnitude
 (gradients are bf16 like the outputs).
 """
 
