@@ -1,8 +1,9 @@
 // topk.hip -- per-row top-k block selection over the bf16 selection scores (gfx950).
 //
 // Replaces scores.topk(k=block_count, dim=-1, largest=True) of attn_topk
-// (primitives.py:50).  One wave per row (b, h, t); the selection itself is select_topk_sorted
-// (up to 1024 blocks and 64 selected) or select_topk (bsa_common.h).  When the row's
+// (primitives.py:50).  One wave per row (b, h, t), or 2 or 4 rows per wave when the rows are
+// many and short (topk_rows_kernel); the selection itself is select_topk_sorted (up to 16 keys
+// per lane of the row's lanes and 64 selected) or select_topk (bsa_common.h).  When the row's
 // compressed-branch output is combined here too, for 1, 2 or 4 query heads per kv head (NH)
 // the split partials are requested before the selection and combined after it, so their
 // memory latency overlaps the selection rounds.
