@@ -158,6 +158,31 @@ def test_attn_topk_rows_per_wave(B, nb, Hq, Hk, K):
     assert torch.equal(got[clear], ref[clear])
 
 
+@pytest.mark.parametrize("B,nb,Hk,K", [(1, 768, 3, 16), (1, 192, 2, 64), (1, 192, 2, 80), (1, 1536, 2, 24),
+                                       (48, 192, 2, 16), (24, 384, 2, 24), (31, 91, 3, 7)],
+                         ids=["sorted_lists_k16", "sorted_lists_k64", "buffered_k80", "buffered_nb1536",
+                              "four_rows_per_wave", "two_rows_per_wave", "four_rows_partial_last_group"])
+def test_attn_topk_exact_order_with_ties(B, nb, Hk, K):
+    """Pooled q / k with entries in {-1, 0, 1} and 8 nonzero dimensions: every score and head
+    mean is exact in bf16 (multiples of 1/4 up to 8), so the oracle's scores are the kernel's,
+    and most rows hold many exactly tied blocks.  The indices must be the K largest scores in
+    descending order, equal scores by ascending block index (a stable sort), on every selection
+    path."""
+    print(f"top-k exact order B={B} nb={nb} Hk={Hk} K={K}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    Hq = 4 * Hk
+    q_cmp = torch.zeros(B, nb, Hq, 64)
+    k_cmp = torch.zeros(B, nb, Hk, 64)
+    q_cmp[..., :8] = torch.randint(-1, 2, (B, nb, Hq, 8), generator=g).float()
+    k_cmp[..., :8] = torch.randint(-1, 2, (B, nb, Hk, 8), generator=g).float()
+    q_cmp, k_cmp = q_cmp.to(torch.bfloat16), k_cmp.to(torch.bfloat16)
+    got = M.attn_topk(*dev(q_cmp, k_cmp), K).cpu()
+    scores = O.topk_scores(q_cmp, k_cmp).permute(0, 2, 1, 3).float()   # [B, nb, Hk, nb]
+    assert (scores * 4 == (scores * 4).round()).all()
+    want = torch.sort(-scores, dim=-1, stable=True).indices[..., :K]
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("B,nb,K", [(1, 768, 16), (1, 192, 64), (1, 192, 80), (1, 1536, 24), (48, 192, 16),
                                     (24, 384, 24)],
                          ids=["sorted_lists_k16", "sorted_lists_k64", "buffered_k80", "buffered_nb1536",
