@@ -431,6 +431,26 @@ def test_full_size_workloads(wl, nsample):
     close(got_rows, ref_rows)
 
 
+def test_two_rows_per_wave_with_split_combine():
+    """8 members of 384 blocks, 12/3 heads, top-16: two key splits in the scores pass and 9216
+    selection rows, so top-k selects two rows per wave and each lane combines two dimensions of
+    its row's compressed-branch partials.  Band rule on every row; sampled blocks against the
+    oracle."""
+    B, N, Hq, Hk, bs, K = 8, 384 * 64, 12, 3, 64, 16
+    print(f"two rows per wave with split combine B={B} N={N}", flush=True)
+    q, k, v = rand(B, N, Hq, 64, seed=22), rand(B, N, Hk, 64, seed=23), rand(B, N, Hk, 64, seed=24)
+    w = torch.sigmoid(torch.randn(3, B, N, Hq, generator=torch.Generator().manual_seed(25))).to(torch.bfloat16)
+    w = w.unsqueeze(-1)
+    out, idx = _run_full(q, k, v, w, 64, bs, K)
+    assert torch.isfinite(out.float()).all()
+    blocks = torch.randperm(N // bs, generator=torch.Generator().manual_seed(26))[:16].sort().values
+    ref_rows, parts = O.mosaic_attn_func_blocks(q, k, v, w, 64, bs, K, blocks, block_indices=idx)
+    bad, amb, rows = O.selection_band_check(parts["scores"].permute(0, 2, 1, 3), idx, K)
+    assert bad == 0, f"{bad}/{rows} rows violate the band rule ({amb} rows have ties in the band)"
+    got_rows = torch.cat([out[:, i * bs:(i + 1) * bs] for i in blocks.tolist()], dim=1)
+    close(got_rows, ref_rows)
+
+
 def test_mosaic_attention_module_runs():
     from types import SimpleNamespace
     cfg = SimpleNamespace(block_attn_size=64, sparse_block_size=64, sparse_block_count=4, num_heads=12,
